@@ -1,0 +1,231 @@
+"""Benchmark of the EXL3 quantized-linear hot path on one MI355X.
+
+Headline (BASELINE.json metric): effective HBM GB/s of the batch-1 QMV on the
+north-star shape (in=4096, out=14336, K=4, 3INST), plus QMM TFLOPS at M=512
+on the same shape.  A step is one EXL3 linear forward over one batch.
+
+Protocol:
+* weights: one seeded synthetic trellis (mlxl3_amd.synth) replicated into
+  ceil(2 GiB / trellis bytes) device copies; consecutive steps rotate over the
+  copies so every launch streams its weights from HBM, not from the 256 MB
+  Infinity Cache;
+* the timed steps run as HIP graph replays on one stream, bracketed by
+  torch.cuda.synchronize() and HIP events recorded on that stream;
+* value = algorithmic bytes per step / time per step, bytes =
+  in*out*K/8 + M*in*2 + M*out*2 + in*2 + out*2 (each tensor once);
+* cpu_baseline: the C oracle (oracle/, decode-at-use GEMV, OpenMP) on the same
+  shape on this host's cores, over a bounded sample.
+
+    python bench.py [--gpus 1] [--steps 2000] [--warmup 200]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+FP16_MFMA_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 FLOP/clk, dense
+ROTATE_BYTES = 2 << 30
+
+
+def alg_bytes(n_in, n_out, k, rows, bias=False):
+    return n_in * n_out * k // 8 + rows * n_in * 2 + rows * n_out * 2 + n_in * 2 + n_out * 2 + (
+        n_out * 2 if bias else 0)
+
+
+def make_rotation(n_in, n_out, k, cb, seed, max_copies=None):
+    import numpy as np
+    import torch
+
+    import mlxl3_amd
+    from mlxl3_amd import synth
+
+    tr, suh, svh, _ = synth.linear_layer(seed, 0, n_in, n_out, k)
+    dev = torch.device("cuda")
+    base = torch.from_numpy(tr.view(np.int16)).to(dev)
+    suh_t = torch.from_numpy(suh).to(dev)
+    svh_t = torch.from_numpy(svh).to(dev)
+    copies = max(2, math.ceil(ROTATE_BYTES / base.numel() / 2))
+    if max_copies:
+        copies = min(copies, max_copies)
+    weights = [base] + [base.clone() for _ in range(copies - 1)]
+    lins = [mlxl3_amd.Exl3Linear(w, suh_t, svh_t, None, k, cb) for w in weights]
+    return lins, weights
+
+
+def time_steps(lins, x, steps, warmup, ws):
+    """Run warmup + timed steps as graph replays; returns (ms per step, y)."""
+    import torch
+
+    n = len(lins)
+    stream = torch.cuda.current_stream()
+
+    def capture(count):
+        g = torch.cuda.CUDAGraph()
+        outs = []
+        with torch.cuda.graph(g):
+            for i in range(count):
+                outs.append(lins[i % n].forward(x, workspace=ws))
+        return g, outs
+
+    # eager warm-up of every handle (no allocation inside the timed region)
+    for lin in lins:
+        lin.forward(x, workspace=ws)
+    torch.cuda.synchronize()
+    full, outs = capture(n)
+    rest = steps % n
+    part = capture(rest)[0] if rest else None
+
+    def run(count):
+        for _ in range(count // n):
+            full.replay()
+        if count % n:
+            (part if count % n == rest else capture(count % n)[0]).replay()
+
+    run(warmup)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    run(steps)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    return ms, outs[0]
+
+
+def cpu_baseline(n_in, n_out, k, cb, rows, budget_s=12.0):
+    import numpy as np
+
+    import oracle
+    from mlxl3_amd import synth
+
+    tr, suh, svh, _ = synth.linear_layer(1, 0, n_in, n_out, k)
+    x = synth.activations(1, 0, rows, n_in)
+    threads = min(os.cpu_count() or 1, 16)
+    oracle.forward(x, tr, suh, svh, k, cb, mode=1, threads=threads)  # table build, warm caches
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        oracle.forward(x, tr, suh, svh, k, cb, mode=1, threads=threads)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or calls >= 200:
+            break
+    per_call = el / calls
+    gbs = alg_bytes(n_in, n_out, k, rows) / per_call / 1e9
+    return {
+        "value": round(gbs, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{calls} calls of the C oracle forward (engine semantics, decode-at-use, "
+                  f"OpenMP {threads} threads) at in={n_in} out={n_out} K={k} rows={rows}; "
+                  f"{per_call * 1e3:.2f} ms/call",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-qmm", action="store_true", help="skip the QMM M=512 leg")
+    ap.add_argument("--k", type=int, default=4)
+    ap.add_argument("--cb", type=int, default=0)
+    ap.add_argument("--in-features", type=int, default=4096)
+    ap.add_argument("--out-features", type=int, default=14336)
+    ap.add_argument("--rows", type=int, default=1)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build's path runs on a single MI355X "
+              "(multi-GPU sharding is design-only); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from mlxl3_amd import synth
+
+    torch.cuda.init()
+    n_in, n_out, k, cb, rows = args.in_features, args.out_features, args.k, args.cb, args.rows
+    lins, _w = make_rotation(n_in, n_out, k, cb, seed=2)
+    x = torch.from_numpy(synth.activations(2, 0, rows, n_in)).cuda()
+    ws = torch.zeros(max(l.workspace_bytes(max(rows, 512)) for l in lins[:1]) + 4096,
+                     dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    ms, _ = time_steps(lins, x, args.steps, args.warmup, ws)
+    nbytes = alg_bytes(n_in, n_out, k, rows)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+
+    result = {
+        "metric": "QMV effective HBM GB/s (% of peak) at 4bpw; QMM TFLOPS (% MFMA peak) at M=512",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded splitmix64 trellis, +-U(0.5,1.5) suh/svh, N(0,1) f16 x)",
+        "config": {
+            "workload": f"qmv_{n_in}x{n_out}_k{k}_{['3inst', 'mcg', 'mul1'][cb]}_m{rows}",
+            "in": n_in, "out": n_out, "k": k, "codebook": cb, "rows": rows,
+            "weight_copies_rotated": len(lins), "bytes_per_step": nbytes,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+    }
+    del lins, _w
+    torch.cuda.empty_cache()
+
+    if not args.no_qmm:
+        m = 512
+        qlins, _qw = make_rotation(n_in, n_out, k, cb, seed=2, max_copies=16)
+        xq = torch.from_numpy(synth.activations(2, 1, m, n_in, outlier_frac=0.01)).cuda()
+        wsq = torch.zeros(qlins[0].workspace_bytes(m) + 4096, dtype=torch.uint8, device="cuda")
+        qsteps = max(16, args.steps // 20)
+        qms, _ = time_steps(qlins, xq, qsteps, max(4, args.warmup // 20), wsq)
+        tflops = 2.0 * m * n_in * n_out / (qms * 1e-3) / 1e12
+        result["qmm"] = {
+            "workload": f"qmm_{n_in}x{n_out}_k{k}_m{m}",
+            "tflops": round(tflops, 2),
+            "ms_per_step": round(qms, 6),
+            "steps": qsteps,
+            "roofline": {
+                "bound": "mfma",
+                "achieved": round(tflops, 2),
+                "peak": FP16_MFMA_PEAK_TFLOPS,
+                "unit": "TFLOP/s",
+                "frac": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4),
+                "traffic": None,
+            },
+        }
+        del qlins, _qw
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(n_in, n_out, k, cb, rows)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

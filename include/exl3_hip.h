@@ -1,0 +1,131 @@
+/*
+ * exl3_hip.h -- C ABI of the MI355X (gfx950) EXL3 quantized-linear library.
+ *
+ * Drop-in boundary for the reference engine's EXL3 operator API.  The
+ * reference dispatches every EXL3 projection through
+ *   Exl3Linear::new      native/src/linear.rs:577-653
+ *   Exl3Linear::forward  native/src/linear.rs:731-998
+ *   Exl3Group::forward   native/src/linear.rs:2382
+ *   Exl3SwitchGlu        native/src/moe.rs:611-1085 (forward :905-975)
+ * which reach the GPU through the generic C entry point
+ *   int mlxl3_metal_kernel(...)   native/ffi/mlx_bridge.cpp:860-911
+ * with errors as int status + a thread-local message (mlxl3_mlx_error,
+ * mlx_bridge.cpp:49-66, :176).  This header replaces that boundary with typed
+ * entry points; the calling conventions are kept: int status, thread-local
+ * error text, dtype codes of mlx_bridge.cpp:71-80, codebook codes of
+ * native/src/codec.rs:5-23.
+ *
+ * Memory: every pointer is a device pointer owned by the caller (hipMalloc or
+ * any allocator of device memory).  Handles borrow the weight buffers and hold
+ * only shapes and launch parameters, so the buffers must outlive the handle.
+ * Execution is asynchronous on the given stream (a hipStream_t passed as
+ * void*, NULL for the default stream); the caller synchronises.
+ *
+ * Workspace: forward calls take a caller-owned device workspace of at least
+ * *_workspace_bytes(rows) bytes.  A workspace must be zero-filled once before
+ * its first use (exl3_workspace_init does that on a stream); every call leaves
+ * it reusable.  Calls that share one workspace must not run concurrently.
+ *
+ * Threading: handles are immutable after creation and may be used from any
+ * thread; error messages are per thread.
+ */
+#ifndef EXL3_HIP_H
+#define EXL3_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  EXL3_OK = 0,
+  EXL3_EINVAL = -1,      /* bad argument or shape (nothing launched) */
+  EXL3_EDEVICE = -2,     /* HIP runtime / launch error */
+  EXL3_ENOMEM = -3,      /* host allocation failed */
+  EXL3_EUNSUPPORTED = -4 /* valid request outside this build */
+} exl3_status;
+
+/* dtype codes of mlx_bridge.cpp:71-80 */
+typedef enum { EXL3_F16 = 9, EXL3_F32 = 10, EXL3_BF16 = 12 } exl3_dtype;
+
+/* codec.rs:5-23: Default (3INST), Mcg, Mul1 */
+typedef enum { EXL3_CB_3INST = 0, EXL3_CB_MCG = 1, EXL3_CB_MUL1 = 2 } exl3_codebook;
+
+typedef struct exl3_linear exl3_linear;
+typedef struct exl3_moe exl3_moe;
+
+/* Message of the last failed call on this thread ("" if none).
+ * Replaces mlxl3_mlx_error, mlx_bridge.cpp:176. */
+const char* exl3_last_error(void);
+
+/* Library version string. */
+const char* exl3_version(void);
+
+/* Exl3Linear::new, linear.rs:577-653.  trellis: [in/16][out/16][16k] u16
+ * (I16 accepted by the caller's reinterpretation); suh f16[in]; svh f16[out];
+ * bias f16[out] or NULL; k in 1..8; cb an exl3_codebook.  in and out must be
+ * positive multiples of 128 (linear.rs:593-596). */
+int exl3_linear_create(const uint16_t* trellis, int32_t in, int32_t out, int32_t k, int32_t cb,
+                       const uint16_t* suh, const uint16_t* svh, const uint16_t* bias,
+                       exl3_linear** out_handle);
+void exl3_linear_destroy(exl3_linear* handle);
+
+/* Input / output features of a handle (Exl3Linear::input_dims/output_dims,
+ * linear.rs:655-660). */
+int32_t exl3_linear_in_features(const exl3_linear* handle);
+int32_t exl3_linear_out_features(const exl3_linear* handle);
+
+/* Workspace needed by exl3_linear_forward for `rows` activation rows. */
+size_t exl3_linear_workspace_bytes(const exl3_linear* handle, int64_t rows);
+
+/* Zero-fills a workspace with a kernel on `stream` (no hipMemset, so it may
+ * be recorded into a graph). */
+int exl3_workspace_init(void* workspace, size_t bytes, void* stream);
+
+/* Exl3Linear::forward, linear.rs:731-998: y[rows][out] = EXL3 linear of
+ * x[rows][in].  x_type / y_type: exl3_dtype (the reference returns x's dtype;
+ * other output types are a superset).  rows >= 1.  rows <= 16 runs the fused
+ * multi-row QMV (one launch); larger rows run the prologue and the QMM. */
+int exl3_linear_forward(const exl3_linear* handle, const void* x, int32_t x_type, int64_t rows,
+                        void* y, int32_t y_type, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* Exl3Group::forward, linear.rs:2313-2382: several projections with the same
+ * input width applied to one x; ys[i] receives parts[i]'s output (dtype of
+ * x).  Workspace: the maximum of the parts' requirements. */
+int exl3_group_forward(const exl3_linear* const* parts, int32_t count, const void* x,
+                       int32_t x_type, int64_t rows, void* const* ys, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/* Exl3SwitchGlu::new, moe.rs:809-900 (SiLU).  gu_trellis
+ * [in/16][2*E*H/16][16k] (gate tiles of expert e at columns [e*H/16,
+ * (e+1)*H/16), up tiles at [(E+e)*H/16, ...), moe.rs:756-760); gu_suh
+ * f16[E][2][in]; gu_svh f16[E][2][H]; down_trellis [H/16][E*in/16][16k];
+ * down_suh f16[E][H]; down_svh f16[E][in]. */
+int exl3_moe_create(const uint16_t* gu_trellis, const uint16_t* gu_suh, const uint16_t* gu_svh,
+                    const uint16_t* down_trellis, const uint16_t* down_suh,
+                    const uint16_t* down_svh, int32_t in, int32_t hidden, int32_t experts,
+                    int32_t top_k, int32_t k, int32_t cb, exl3_moe** out_handle);
+void exl3_moe_destroy(exl3_moe* handle);
+size_t exl3_moe_workspace_bytes(const exl3_moe* handle, int64_t rows);
+
+/* Exl3SwitchGlu::forward, moe.rs:905-975: x f16[rows][in], selected
+ * u32[rows][top_k] (< experts), scores f16[rows][top_k]; y f16[rows][in].
+ * The routing plan (moe.rs:66-182) is built on the device. */
+int exl3_moe_forward(const exl3_moe* handle, const uint16_t* x, int64_t rows,
+                     const uint32_t* selected, const uint16_t* scores, uint16_t* y,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Decode hook, the reference's `metal-decode` codec op (exl3.metal:102-109,
+ * main.rs:945-967): for every tile, states[t*256 + i] (nullable) and the f16
+ * bits values[t*256 + i] of state index i, in the tile's stored order. */
+int exl3_decode_tiles(const uint16_t* packed, int64_t tiles, int32_t k, int32_t cb,
+                      uint16_t* states, uint16_t* values, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EXL3_HIP_H */

@@ -1,0 +1,355 @@
+"""MI355X (gfx950) EXL3 quantized-linear library: Python mirror of the operator API.
+
+The compute lives in ``libexl3_hip.so`` (hand-written HIP kernels behind the C
+ABI of ``include/exl3_hip.h``).  This module mirrors the reference engine's
+operator types on top of that ABI, with the same argument meaning and error
+behaviour:
+
+* :class:`Exl3Linear`   -- ``Exl3Linear::new`` / ``forward`` (native/src/linear.rs:577-998)
+* :class:`Exl3Group`    -- ``Exl3Group::forward`` (linear.rs:2285-2382)
+* :class:`Exl3SwitchGlu` -- ``Exl3SwitchGlu::new`` / ``forward`` (native/src/moe.rs:809-975)
+* :func:`decode_tiles`  -- the ``metal-decode`` codec op (exl3.metal:102-109)
+
+PyTorch is used only to own device memory and to name the current stream.
+There is no CPU fallback: without the built library every entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import enum
+from pathlib import Path
+from typing import Optional, Sequence
+
+LIB_PATH = Path(__file__).resolve().parent / "libexl3_hip.so"
+
+__all__ = [
+    "Codebook",
+    "Exl3Error",
+    "Exl3Linear",
+    "Exl3Group",
+    "Exl3SwitchGlu",
+    "decode_tiles",
+    "load_library",
+    "LIB_PATH",
+]
+
+
+class Codebook(enum.IntEnum):
+    """codec.rs:5-23."""
+
+    DEFAULT = 0  # 3INST
+    MCG = 1
+    MUL1 = 2
+
+
+class Exl3Error(RuntimeError):
+    """A non-zero status from the C ABI, carrying exl3_last_error()."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+
+
+_DTYPE_CODES = {}  # torch dtype -> mlx_bridge dtype code, filled lazily
+_lib: Optional[ctypes.CDLL] = None
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_sz = ctypes.c_size_t
+
+_SIGNATURES = {
+    "exl3_last_error": (ctypes.c_char_p, []),
+    "exl3_version": (ctypes.c_char_p, []),
+    "exl3_linear_create": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, ctypes.POINTER(_vp)]),
+    "exl3_linear_destroy": (None, [_vp]),
+    "exl3_linear_in_features": (_i32, [_vp]),
+    "exl3_linear_out_features": (_i32, [_vp]),
+    "exl3_linear_workspace_bytes": (_sz, [_vp, _i64]),
+    "exl3_workspace_init": (_i32, [_vp, _sz, _vp]),
+    "exl3_linear_forward": (_i32, [_vp, _vp, _i32, _i64, _vp, _i32, _vp, _sz, _vp]),
+    "exl3_group_forward": (_i32, [_vp, _i32, _vp, _i32, _i64, _vp, _vp, _sz, _vp]),
+    "exl3_moe_create": (
+        _i32,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_vp)],
+    ),
+    "exl3_moe_destroy": (None, [_vp]),
+    "exl3_moe_workspace_bytes": (_sz, [_vp, _i64]),
+    "exl3_moe_forward": (_i32, [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "exl3_decode_tiles": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _vp]),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+
+def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
+    """Load libexl3_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise Exl3Error(
+            -4, f"{p} is missing: build it with `python -m mlxl3_amd.build` (no CPU fallback exists)"
+        )
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        msg = load_library().exl3_last_error().decode("utf-8", "replace")
+        raise Exl3Error(status, msg)
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+def _dtype_code(dtype) -> int:
+    torch = _torch()
+    if not _DTYPE_CODES:
+        _DTYPE_CODES.update({torch.float16: 9, torch.float32: 10, torch.bfloat16: 12})
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise Exl3Error(-1, f"unsupported activation dtype {dtype}") from None
+
+
+def _stream_ptr(device) -> int:
+    torch = _torch()
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _require_device(t, name: str, dtypes=None):
+    torch = _torch()
+    if t is None:
+        return None
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise Exl3Error(-1, f"{name} must be a device tensor")
+    if dtypes is not None and t.dtype not in dtypes:
+        raise Exl3Error(-1, f"{name} has dtype {t.dtype}, expected one of {dtypes}")
+    return t.contiguous()
+
+
+class _Workspace:
+    """Per-device zero-initialised workspace, grown on demand."""
+
+    def __init__(self):
+        self.buf = None
+
+    def get(self, nbytes: int, device):
+        torch = _torch()
+        nbytes = max(256, (nbytes + 255) // 256 * 256)
+        if self.buf is None or self.buf.numel() < nbytes or self.buf.device != device:
+            self.buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        return self.buf
+
+
+class Exl3Linear:
+    """Exl3Linear (native/src/linear.rs:424-998) on one MI355X.
+
+    trellis: int16/uint16 tensor [in/16, out/16, 16*k]; suh [in]; svh [out];
+    bias [out] or None (any float dtype, stored as f16); k in 1..8; cb a Codebook.
+    """
+
+    def __init__(self, trellis, suh, svh, bias=None, k: int = 4, cb: int = Codebook.DEFAULT):
+        torch = _torch()
+        lib = load_library()
+        if not (1 <= int(k) <= 8):
+            raise Exl3Error(-1, f"K must be in 1..=8, got {k}")
+        shape = tuple(trellis.shape)
+        if len(shape) != 3 or shape[2] != 16 * int(k) or any(d <= 0 for d in shape):
+            raise Exl3Error(-1, "invalid trellis shape")
+        if trellis.dtype not in (torch.int16, torch.uint16):
+            raise Exl3Error(-1, "EXL3 trellis must contain 16-bit integers")
+        rows, cols = shape[0] * 16, shape[1] * 16
+        if rows % 128 or cols % 128:
+            raise Exl3Error(-1, "public EXL3 projections require 128-aligned dimensions")
+        if tuple(suh.shape) != (rows,) or tuple(svh.shape) != (cols,):
+            raise Exl3Error(-1, "EXL3 scales have wrong dimensions")
+        if bias is not None and tuple(bias.shape) != (cols,):
+            raise Exl3Error(-1, "EXL3 bias has wrong dimensions")
+        self.trellis = _require_device(trellis, "trellis")
+        self.suh = _require_device(suh, "suh").to(torch.float16).contiguous()
+        self.svh = _require_device(svh, "svh").to(torch.float16).contiguous()
+        self.bias = None if bias is None else _require_device(bias, "bias").to(torch.float16).contiguous()
+        self.k, self.cb = int(k), int(cb)
+        self.in_features, self.out_features = rows, cols
+        h = _vp()
+        _check(
+            lib.exl3_linear_create(
+                _ptr(self.trellis), rows, cols, self.k, self.cb, _ptr(self.suh), _ptr(self.svh),
+                _ptr(self.bias), ctypes.byref(h),
+            )
+        )
+        self._handle = h
+        self._ws = _Workspace()
+
+    def __del__(self):
+        h = getattr(self, "_handle", None)
+        if h is not None and h.value and _lib is not None:
+            _lib.exl3_linear_destroy(h)
+            self._handle = None
+
+    @property
+    def handle(self):
+        return self._handle
+
+    def workspace_bytes(self, rows: int) -> int:
+        return int(load_library().exl3_linear_workspace_bytes(self._handle, int(rows)))
+
+    def forward(self, x, out_dtype=None, workspace=None):
+        """y = linear(x) for x [..., in]; output dtype = x.dtype unless given."""
+        torch = _torch()
+        x = _require_device(x, "x", (torch.float16, torch.bfloat16, torch.float32))
+        if x.shape[-1] != self.in_features or x.numel() % self.in_features:
+            raise Exl3Error(-1, f"invalid EXL3 linear input for {self.in_features} inputs")
+        rows = x.numel() // self.in_features
+        if rows == 0:
+            raise Exl3Error(-1, "EXL3 linear input cannot be empty")
+        out_dtype = x.dtype if out_dtype is None else out_dtype
+        y = torch.empty(*x.shape[:-1], self.out_features, dtype=out_dtype, device=x.device)
+        need = self.workspace_bytes(rows)
+        ws = workspace if workspace is not None else self._ws.get(need, x.device)
+        _check(
+            load_library().exl3_linear_forward(
+                self._handle, _ptr(x), _dtype_code(x.dtype), rows, _ptr(y), _dtype_code(out_dtype),
+                _ptr(ws), ws.numel() * ws.element_size(), _stream_ptr(x.device),
+            )
+        )
+        return y
+
+    __call__ = forward
+
+
+class Exl3Group:
+    """Exl3Group (linear.rs:2285-2815): projections sharing x, one output each."""
+
+    def __init__(self, linears: Sequence[Exl3Linear]):
+        if not linears:
+            raise Exl3Error(-1, "empty EXL3 group")
+        first = linears[0]
+        for lin in linears:
+            if (lin.in_features, lin.k, lin.cb) != (first.in_features, first.k, first.cb):
+                raise Exl3Error(-1, "EXL3 group members need the same input width, K and codebook")
+        self.linears = list(linears)
+        self._ws = _Workspace()
+
+    def forward(self, x):
+        torch = _torch()
+        x = _require_device(x, "x", (torch.float16, torch.bfloat16, torch.float32))
+        n_in = self.linears[0].in_features
+        if x.shape[-1] != n_in:
+            raise Exl3Error(-1, f"invalid EXL3 linear input for {n_in} inputs")
+        rows = x.numel() // n_in
+        ys = [torch.empty(*x.shape[:-1], l.out_features, dtype=x.dtype, device=x.device) for l in self.linears]
+        need = max(l.workspace_bytes(rows) for l in self.linears)
+        ws = self._ws.get(need, x.device)
+        handles = (_vp * len(self.linears))(*[l.handle.value for l in self.linears])
+        outs = (_vp * len(ys))(*[y.data_ptr() for y in ys])
+        _check(
+            load_library().exl3_group_forward(
+                handles, len(self.linears), _ptr(x), _dtype_code(x.dtype), rows, outs, _ptr(ws),
+                ws.numel(), _stream_ptr(x.device),
+            )
+        )
+        return ys
+
+    __call__ = forward
+
+
+class Exl3SwitchGlu:
+    """Exl3SwitchGlu (native/src/moe.rs:611-1085), SiLU experts, grouped expert QMM."""
+
+    def __init__(self, gu_trellis, gu_suh, gu_svh, down_trellis, down_suh, down_svh, top_k: int,
+                 k: int, cb: int = Codebook.DEFAULT):
+        torch = _torch()
+        lib = load_library()
+        in_tiles, gu_cols, k16 = gu_trellis.shape
+        experts = gu_suh.shape[0]
+        hidden = gu_svh.shape[-1]
+        self.input, self.hidden, self.experts, self.top_k = in_tiles * 16, hidden, experts, int(top_k)
+        self.k, self.cb = int(k), int(cb)
+        self.tensors = [
+            _require_device(gu_trellis, "gu_trellis"),
+            _require_device(gu_suh, "gu_suh").to(torch.float16).contiguous(),
+            _require_device(gu_svh, "gu_svh").to(torch.float16).contiguous(),
+            _require_device(down_trellis, "down_trellis"),
+            _require_device(down_suh, "down_suh").to(torch.float16).contiguous(),
+            _require_device(down_svh, "down_svh").to(torch.float16).contiguous(),
+        ]
+        h = _vp()
+        _check(
+            lib.exl3_moe_create(
+                *[_ptr(t) for t in self.tensors], self.input, self.hidden, self.experts, self.top_k,
+                self.k, self.cb, ctypes.byref(h),
+            )
+        )
+        self._handle = h
+        self._ws = _Workspace()
+
+    def __del__(self):
+        h = getattr(self, "_handle", None)
+        if h is not None and h.value and _lib is not None:
+            _lib.exl3_moe_destroy(h)
+            self._handle = None
+
+    def forward(self, x, selected, scores):
+        torch = _torch()
+        x = _require_device(x, "x", (torch.float16,))
+        rows = x.shape[0]
+        if x.dim() != 2 or x.shape[1] != self.input or tuple(selected.shape) != (rows, self.top_k) \
+                or tuple(scores.shape) != (rows, self.top_k):
+            raise Exl3Error(-1, "invalid SwitchGLU input/routes")
+        selected = _require_device(selected, "selected").to(torch.int32).contiguous()
+        scores = _require_device(scores, "scores").to(torch.float16).contiguous()
+        y = torch.empty_like(x)
+        need = int(load_library().exl3_moe_workspace_bytes(self._handle, rows))
+        ws = self._ws.get(need, x.device)
+        _check(
+            load_library().exl3_moe_forward(
+                self._handle, _ptr(x), rows, _ptr(selected), _ptr(scores), _ptr(y), _ptr(ws),
+                ws.numel(), _stream_ptr(x.device),
+            )
+        )
+        return y
+
+    __call__ = forward
+
+
+def decode_tiles(packed, k: int, cb: int, with_states: bool = True):
+    """Decode every tile of a packed trellis on the GPU.
+
+    packed: device int16/uint16 tensor whose size is a multiple of 16*k.
+    Returns (states uint16 [tiles, 256] or None, values float16 [tiles, 256])
+    in each tile's stored (permuted) order.
+    """
+    torch = _torch()
+    packed = _require_device(packed, "packed")
+    if not (1 <= int(k) <= 8):
+        raise Exl3Error(-1, f"K must be in 1..=8, got {k}")
+    if packed.numel() % (16 * k):
+        raise Exl3Error(-1, "packed length is not a whole tile")
+    tiles = packed.numel() // (16 * k)
+    values = torch.empty(tiles, 256, dtype=torch.float16, device=packed.device)
+    states = torch.empty(tiles, 256, dtype=torch.uint16, device=packed.device) if with_states else None
+    _check(
+        load_library().exl3_decode_tiles(
+            _ptr(packed), tiles, int(k), int(cb), _ptr(states), _ptr(values), _stream_ptr(packed.device)
+        )
+    )
+    return states, values

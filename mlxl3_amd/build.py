@@ -1,0 +1,81 @@
+"""Build the gfx950 EXL3 library (mlxl3_amd/libexl3_hip.so) with hipcc.
+
+Each kernel family is its own translation unit; they compile in parallel and
+link into one shared object that exports the C ABI of include/exl3_hip.h.
+
+    python -m mlxl3_amd.build            # build (always recompiles)
+"""
+
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE / "csrc"
+LIB = HERE / "libexl3_hip.so"
+SOURCES = ["exl3_api.hip", "exl3_qmv.hip", "exl3_qmm.hip", "exl3_moe.hip"]
+ARCH = "gfx950"
+
+# -ffp-contract=off: every f32 multiply/add in the glue is rounded separately,
+# as the reference's stages are; -packed-fp32-ops off: no v_pk_*_f32.
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-ffp-contract=off",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(path).exists():
+        raise RuntimeError("hipcc not found; the EXL3 library needs ROCm's hipcc")
+    return path
+
+
+def _compile(src: Path, obj: Path) -> None:
+    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(line for line in res.stderr.splitlines() if noise not in line)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{err}")
+    if err.strip():
+        print(err, file=sys.stderr)
+
+
+def build(verbose: bool = True) -> Path:
+    """Compile every translation unit and link LIB; returns its path."""
+    srcs = [CSRC / s for s in SOURCES]
+    with tempfile.TemporaryDirectory(prefix="exl3_build_") as tmp:
+        objs = [Path(tmp) / (s.stem + ".o") for s in srcs]
+        jobs = min(len(srcs), max(1, os.cpu_count() or 1))
+        with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+            list(pool.map(_compile, srcs, objs))
+        tmp_lib = Path(tmp) / LIB.name
+        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp_lib)]
+        cmd += [str(o) for o in objs]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"link failed:\n{res.stderr}")
+        shutil.copy2(tmp_lib, LIB)
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+if __name__ == "__main__":
+    build()

@@ -1,0 +1,44 @@
+// Launcher tables shared between the host translation unit and the kernel
+// translation units (each kernel family is compiled in its own file so the
+// instantiations over K x codebook build in parallel).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "exl3_params.hpp"
+
+namespace exl3 {
+
+typedef void (*QmvFn)(const QmvParams&, dim3, size_t, hipStream_t);
+typedef void (*QmmFn)(const QmmParams&, dim3, hipStream_t);
+typedef void (*DecodeFn)(const uint32_t*, int64_t, uint16_t*, uint16_t*, dim3, hipStream_t);
+
+// [K-1][codebook]
+extern const QmvFn kQmv[8][3];
+extern const DecodeFn kDecode[8][3];
+extern const QmmFn kQmm2[8][3];  // 128-row workgroup tile
+extern const QmmFn kQmm4[8][3];  // 256-row workgroup tile
+
+void launch_prologue(const void* x, int x_dtype, const uint16_t* suh, int in, int rows,
+                     uint16_t* xhat, hipStream_t s);
+void launch_fill_zero(uint32_t* p, size_t words, hipStream_t s);
+
+// Records the thread-local error message and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Converts a pending launch error into EXL3_EDEVICE.
+int check_launch(const char* what);
+
+}  // namespace exl3
+
+#define EXL3_CB_ROW(F, K) {F<K, 0>, F<K, 1>, F<K, 2>}
+#define EXL3_TABLE(F)                                                              \
+  {EXL3_CB_ROW(F, 1), EXL3_CB_ROW(F, 2), EXL3_CB_ROW(F, 3), EXL3_CB_ROW(F, 4), \
+   EXL3_CB_ROW(F, 5), EXL3_CB_ROW(F, 6), EXL3_CB_ROW(F, 7), EXL3_CB_ROW(F, 8)}
+
+// Explicit instantiation over K = 1..8 and the three codebooks, so both the
+// device pass and the host pass see every kernel.
+#define EXL3_INST_CB(M, K) M(K, 0) M(K, 1) M(K, 2)
+#define EXL3_INSTANTIATE(M)                                                        \
+  EXL3_INST_CB(M, 1) EXL3_INST_CB(M, 2) EXL3_INST_CB(M, 3) EXL3_INST_CB(M, 4) \
+  EXL3_INST_CB(M, 5) EXL3_INST_CB(M, 6) EXL3_INST_CB(M, 7) EXL3_INST_CB(M, 8)

@@ -1,0 +1,31 @@
+// Kernel parameter blocks (plain structs passed by value to the kernels).
+#pragma once
+
+#include <stdint.h>
+
+namespace exl3 {
+
+struct QmvParams {
+  const uint32_t* trellis;  // [in/16][out/16][8K] u32
+  const void* x;            // [M][in] of x_dtype
+  const uint16_t* suh;      // [in] f16
+  const uint16_t* svh;      // [out] f16
+  const uint16_t* bias;     // [out] f16 or null
+  void* y;                  // [M][out] of y_dtype
+  float* partials;          // [splits][M][out]
+  uint32_t* counters;       // [out/128], zero between calls
+  int in, out, M, splits;
+  int x_dtype, y_dtype;
+};
+
+struct QmmParams {
+  const uint32_t* trellis;  // [in/16][out/16][8K] u32
+  const uint16_t* xhat;     // [M][in] f16 (prologue output)
+  const uint16_t* svh;      // [out]
+  const uint16_t* bias;     // [out] or null
+  void* y;                  // [M][out]
+  int in, out, M, y_dtype;
+  int col_blocks;           // out / 128
+};
+
+}  // namespace exl3

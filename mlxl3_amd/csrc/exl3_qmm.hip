@@ -1,0 +1,45 @@
+// Instantiations of the prologue and the QMM over K x codebook x row tile.
+#include "exl3_launch.hpp"
+#include "exl3_qmm.hpp"
+
+namespace exl3 {
+
+#define EXL3_QMM_INST(K, CB)                                   \
+  template __global__ void qmm_kernel<K, CB, 2>(QmmParams); \
+  template __global__ void qmm_kernel<K, CB, 4>(QmmParams);
+EXL3_INSTANTIATE(EXL3_QMM_INST)
+
+__global__ void fill_zero_kernel(uint32_t* p, size_t words) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < words; i += stride) p[i] = 0u;
+}
+
+// Host-side launchers (not part of the device compilation pass).
+#ifndef __HIP_DEVICE_COMPILE__
+template <int K, int CB>
+static void run_qmm2(const QmmParams& p, dim3 g, hipStream_t s) {
+  hipLaunchKernelGGL((qmm_kernel<K, CB, 2>), g, dim3(256), 0, s, p);
+}
+template <int K, int CB>
+static void run_qmm4(const QmmParams& p, dim3 g, hipStream_t s) {
+  hipLaunchKernelGGL((qmm_kernel<K, CB, 4>), g, dim3(256), 0, s, p);
+}
+
+const QmmFn kQmm2[8][3] = EXL3_TABLE(run_qmm2);
+const QmmFn kQmm4[8][3] = EXL3_TABLE(run_qmm4);
+
+void launch_prologue(const void* x, int x_dtype, const uint16_t* suh, int in, int rows,
+                     uint16_t* xhat, hipStream_t s) {
+  hipLaunchKernelGGL(prologue_kernel, dim3(in / 128, rows), dim3(64), 0, s, x, x_dtype, suh, in,
+                     xhat);
+}
+
+void launch_fill_zero(uint32_t* p, size_t words, hipStream_t s) {
+  unsigned blocks = (unsigned)((words + 255) / 256 < 4096 ? (words + 255) / 256 : 4096);
+  hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0, s, p, words);
+}
+
+#endif
+
+}  // namespace exl3

@@ -1,0 +1,205 @@
+"""ctypes wrapper of the C oracle (oracle/liboracle_exl3.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker or the timed CPU baseline.  The
+product package (mlxl3_amd) never imports it.
+
+Function-by-function citations are in exl3_oracle.h / exl3_oracle.c.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle_exl3.so"
+
+_lib = None
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_vp = ctypes.c_void_p
+
+DT_F16, DT_F32, DT_BF16 = 9, 10, 12
+
+
+def build() -> Path:
+    """Compile the oracle with gcc (oracle/Makefile)."""
+    subprocess.run(["make", "-s", "-B", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.exl3o_f16_to_f32.restype = ctypes.c_float
+        L.exl3o_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.exl3o_f32_to_f16.restype = ctypes.c_uint16
+        L.exl3o_f32_to_f16.argtypes = [ctypes.c_float]
+        L.exl3o_f64_to_f16.restype = ctypes.c_uint16
+        L.exl3o_f64_to_f16.argtypes = [ctypes.c_double]
+        L.exl3o_bf16_to_f32.restype = ctypes.c_float
+        L.exl3o_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        L.exl3o_f32_to_bf16.restype = ctypes.c_uint16
+        L.exl3o_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.exl3o_codeword.restype = ctypes.c_uint16
+        L.exl3o_codeword.argtypes = [ctypes.c_uint16, ctypes.c_int]
+        L.exl3o_codebook.restype = None
+        L.exl3o_codebook.argtypes = [ctypes.c_int, _u16p]
+        L.exl3o_unpack.restype = ctypes.c_int
+        L.exl3o_unpack.argtypes = [_u16p, ctypes.c_int64, ctypes.c_int, _u16p]
+        L.exl3o_pack.restype = ctypes.c_int
+        L.exl3o_pack.argtypes = [_u16p, ctypes.c_int64, ctypes.c_int, _u16p]
+        L.exl3o_permutation.restype = None
+        L.exl3o_permutation.argtypes = [_u16p]
+        L.exl3o_reconstruct_inner.restype = ctypes.c_int
+        L.exl3o_reconstruct_inner.argtypes = [_u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
+                                              ctypes.c_int64, _u16p]
+        L.exl3o_h128_f32.restype = None
+        L.exl3o_h128_f32.argtypes = [_f32p, ctypes.c_int64]
+        L.exl3o_h128_staged.restype = None
+        L.exl3o_h128_staged.argtypes = [_f32p, ctypes.c_int64]
+        L.exl3o_forward.restype = ctypes.c_int
+        L.exl3o_forward.argtypes = [ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int64, _u16p,
+                                    ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _u16p,
+                                    _u16p, _vp, _vp, _vp, ctypes.c_int]
+        L.exl3o_prologue.restype = ctypes.c_int
+        L.exl3o_prologue.argtypes = [_vp, ctypes.c_int, ctypes.c_int64, ctypes.c_int, _u16p, _u16p]
+        L.exl3o_moe_forward.restype = ctypes.c_int
+        L.exl3o_moe_forward.argtypes = [_u16p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        _u16p, _u16p, _u16p, _u16p, _u16p, _u16p, _u32p, _u16p,
+                                        _u16p, ctypes.c_int]
+        _lib = L
+    return _lib
+
+
+def _u16(a) -> np.ndarray:
+    a = np.asarray(a)
+    if a.dtype == np.float16:
+        a = a.view(np.uint16)
+    if a.dtype == np.int16:
+        a = a.view(np.uint16)
+    return np.ascontiguousarray(a, dtype=np.uint16)
+
+
+def _dtype_code(a: np.ndarray) -> int:
+    if a.dtype == np.float16:
+        return DT_F16
+    if a.dtype == np.float32:
+        return DT_F32
+    raise ValueError(f"oracle activations are float16 or float32, got {a.dtype}")
+
+
+def codeword(state: int, cb: int) -> int:
+    return int(lib().exl3o_codeword(state & 0xFFFF, cb))
+
+
+def codebook(cb: int) -> np.ndarray:
+    """f16 bits of every state, [65536] uint16."""
+    out = np.empty(65536, np.uint16)
+    lib().exl3o_codebook(cb, out)
+    return out
+
+
+def unpack(packed, k: int) -> np.ndarray:
+    p = _u16(packed).ravel()
+    if p.size % (16 * k):
+        raise ValueError("packed length is not a whole tile")
+    tiles = p.size // (16 * k)
+    out = np.empty(tiles * 256, np.uint16)
+    if lib().exl3o_unpack(p, tiles, k, out):
+        raise ValueError(f"K must be in 1..=8, got {k}")
+    return out.reshape(tiles, 256)
+
+
+def pack(states, k: int) -> np.ndarray:
+    s = _u16(states).ravel()
+    if s.size % 256:
+        raise ValueError("encoded length must be a multiple of 256")
+    tiles = s.size // 256
+    out = np.empty(tiles * 16 * k, np.uint16)
+    if lib().exl3o_pack(s, tiles, k, out):
+        raise ValueError(f"K must be in 1..=8, got {k}")
+    return out.reshape(tiles, 16 * k)
+
+
+def permutation() -> np.ndarray:
+    out = np.empty(256, np.uint16)
+    lib().exl3o_permutation(out)
+    return out.astype(np.int64)
+
+
+def reconstruct_inner(packed, k: int, cb: int, rows: int, cols: int) -> np.ndarray:
+    """Dense W_inner [rows, cols] float16 (codec.rs:158-190)."""
+    out = np.empty(rows * cols, np.uint16)
+    if lib().exl3o_reconstruct_inner(_u16(packed).ravel(), k, cb, rows, cols, out):
+        raise ValueError("invalid reconstruct arguments")
+    return out.view(np.float16).reshape(rows, cols)
+
+
+def h128_f32(v) -> np.ndarray:
+    a = np.ascontiguousarray(v, dtype=np.float32).copy()
+    lib().exl3o_h128_f32(a.reshape(-1), a.size)
+    return a
+
+
+def h128_staged(v) -> np.ndarray:
+    a = np.ascontiguousarray(v, dtype=np.float32).copy()
+    lib().exl3o_h128_staged(a.reshape(-1), a.size)
+    return a
+
+
+def prologue(x, suh) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    rows, n = x.reshape(-1, x.shape[-1]).shape
+    out = np.empty(rows * n, np.uint16)
+    rc = lib().exl3o_prologue(x.ctypes.data, _dtype_code(x), rows, n, _u16(suh), out)
+    if rc:
+        raise ValueError("invalid prologue arguments")
+    return out.view(np.float16).reshape(rows, n)
+
+
+def forward(x, trellis, suh, svh, k: int, cb: int, bias=None, mode: int = 1, threads: int = 0,
+            return_yhat: bool = False):
+    """EXL3 linear on the CPU.  mode 1: engine glue semantics; mode 0: ref/forward.py."""
+    x = np.ascontiguousarray(x)
+    n_in = int(x.shape[-1])
+    rows = x.size // n_in
+    tr = _u16(trellis)
+    n_out = int(tr.shape[1]) * 16 if tr.ndim == 3 else int(len(svh))
+    y = np.empty((rows, n_out), x.dtype)
+    yhat = np.empty((rows, n_out), np.float32) if return_yhat else None
+    b = None if bias is None else _u16(bias)
+    rc = lib().exl3o_forward(mode, x.ctypes.data, _dtype_code(x), rows, tr.ravel(), n_in, n_out,
+                             k, cb, _u16(suh), _u16(svh), None if b is None else b.ctypes.data,
+                             y.ctypes.data, None if yhat is None else yhat.ctypes.data, threads)
+    if rc:
+        raise ValueError(f"oracle forward failed ({rc})")
+    y = y.reshape(*x.shape[:-1], n_out)
+    return (y, yhat) if return_yhat else y
+
+
+def moe_forward(x, selected, scores, gu_trellis, gu_suh, gu_svh, down_trellis, down_suh,
+                down_svh, k: int, cb: int, threads: int = 0) -> np.ndarray:
+    x = _u16(x)
+    rows, n_in = x.shape
+    experts, hidden = gu_svh.shape[0], gu_svh.shape[-1]
+    top_k = selected.shape[1]
+    y = np.empty((rows, n_in), np.uint16)
+    rc = lib().exl3o_moe_forward(x.ravel(), rows, n_in, hidden, experts, top_k, k, cb,
+                                 _u16(gu_trellis).ravel(), _u16(gu_suh).ravel(),
+                                 _u16(gu_svh).ravel(), _u16(down_trellis).ravel(),
+                                 _u16(down_suh).ravel(), _u16(down_svh).ravel(),
+                                 np.ascontiguousarray(selected, np.uint32).ravel(),
+                                 _u16(scores).ravel(), y.ravel(), threads)
+    if rc:
+        raise ValueError(f"oracle MoE forward failed ({rc})")
+    return y.view(np.float16)

@@ -1,0 +1,91 @@
+/*
+ * CPU oracle for the EXL3 quantized-linear path.  TEST INFRASTRUCTURE ONLY:
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg are the only
+ * callers.  The product library (mlxl3_amd/libexl3_hip.so) never links or
+ * calls anything here.
+ *
+ * Every function restates the reference algorithm it names (file:line under
+ * the reference tree) in plain C; f16/bf16 conversions are done bit-exactly by
+ * hand so the oracle does not depend on compiler half-precision support.
+ */
+#ifndef EXL3_ORACLE_H
+#define EXL3_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- scalar conversions (IEEE binary16 / bfloat16, round-to-nearest-even) ---- */
+float exl3o_f16_to_f32(uint16_t h);
+uint16_t exl3o_f64_to_f16(double d);
+uint16_t exl3o_f32_to_f16(float f);
+float exl3o_bf16_to_f32(uint16_t h);
+uint16_t exl3o_f32_to_bf16(float f);
+
+/* ---- codec (native/src/codec.rs) ---- */
+/* decode_codeword, codec.rs:52-71.  Returns f16 bits.  cb: 0 3INST, 1 MCG, 2 MUL1. */
+uint16_t exl3o_codeword(uint16_t state, int cb);
+/* codebook over all 65536 states (exhaustive table) */
+void exl3o_codebook(int cb, uint16_t* out65536);
+/* unpack, codec.rs:102-124 (+ unpack_window :40-46, packed_pair :48-50).
+ * packed: tiles*16*k u16, states: tiles*256 u16.  Returns 0 or -1 (bad k). */
+int exl3o_unpack(const uint16_t* packed, int64_t tiles, int k, uint16_t* states);
+/* pack, codec.rs:73-100 (+ pack_source :34-38). */
+int exl3o_pack(const uint16_t* states, int64_t tiles, int k, uint16_t* packed);
+/* permutation, codec.rs:126-138: out[state index] = row*16 + col */
+void exl3o_permutation(uint16_t out[256]);
+/* reconstruct_inner, codec.rs:158-190: dense W_inner [rows][cols] f16 bits. */
+int exl3o_reconstruct_inner(const uint16_t* packed, int k, int cb, int64_t rows,
+                            int64_t cols, uint16_t* out);
+
+/* ---- Hadamard-128 (in place over count values, count % 128 == 0) ---- */
+/* MLX f32 hadamard_transform semantics: ascending-stride radix-2 butterflies
+ * in f32, then * f32(1/sqrt(128)).  Pinned bit-exactly by the reference's
+ * tests/fixtures/native-converter-host/hadamard.npz. */
+void exl3o_h128_f32(float* v, int64_t count);
+/* Engine f16 staging (exl3.metal:154-170, linear.rs:1380-1427): same
+ * butterflies, values rounded to f16 after the stride-8 and stride-64 stages,
+ * then f16(v * f32(1/sqrt(128))).  Values are returned as f32 holding f16. */
+void exl3o_h128_staged(float* v, int64_t count);
+
+/* ---- forward of one EXL3 linear ----
+ * x: rows*in values of x_dtype (9 f16, 10 f32, 12 bf16), y: rows*out of the
+ * same dtype.  trellis [in/16][out/16][16k] u16; suh [in] f16; svh [out] f16;
+ * bias [out] f16 or NULL.
+ * mode 0: ponyexl3/ref/forward.py:14-49 (f32 H128 with suh/svh in f32,
+ *         f16 roundings at xh, y and the output) evaluated with f64 sums.
+ * mode 1: engine glue semantics (linear.rs:847-865 prologue, :984-997
+ *         epilogue): f16(x)*suh in f16, f16-staged H128, f32 GEMV, f16(y),
+ *         f16-staged H128, *svh in f16, cast, + bias.
+ * yhat_out (optional, rows*out f32): the raw inner product before rounding.
+ * threads <= 0 uses all cores.  Returns 0 or a negative error. */
+int exl3o_forward(int mode, const void* x, int x_dtype, int64_t rows, const uint16_t* trellis,
+                  int in, int out, int k, int cb, const uint16_t* suh, const uint16_t* svh,
+                  const uint16_t* bias, void* y, float* yhat_out, int threads);
+
+/* xhat of the engine prologue (mode 1), rows*in f16 bits. */
+int exl3o_prologue(const void* x, int x_dtype, int64_t rows, int in, const uint16_t* suh,
+                   uint16_t* xhat);
+
+/* ---- MoE SwitchGLU (moe.rs:66-609 semantics, one expert at a time) ----
+ * gu_trellis [in/16][2*E*H/16][16k]: for expert e, gate columns are tile
+ * columns [e*H/16, (e+1)*H/16) and up columns [(E+e)*H/16, ...) (moe.rs:756-760).
+ * down_trellis [H/16][E*in/16][16k], expert e at tile columns [e*in/16, ...).
+ * gu_suh [E][2][in], gu_svh [E][2][H], down_suh [E][H], down_svh [E][in] f16.
+ * selected [rows][top_k] u32, scores [rows][top_k] f16.  x, y: rows*in f16.
+ * Each routed slot: gate = lin(x), up = lin(x) (f16 outputs), act =
+ * f16(silu(gate) * up), down = lin(act) (f16), y = f16(sum_t f32(score*down)). */
+int exl3o_moe_forward(const uint16_t* x, int64_t rows, int in, int hidden, int experts,
+                      int top_k, int k, int cb, const uint16_t* gu_trellis,
+                      const uint16_t* gu_suh, const uint16_t* gu_svh,
+                      const uint16_t* down_trellis, const uint16_t* down_suh,
+                      const uint16_t* down_svh, const uint32_t* selected,
+                      const uint16_t* scores, uint16_t* y, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,120 @@
+"""The C-ABI library loads and exports what include/exl3_hip.h declares, and
+host-side validation rejects bad arguments before any launch (no GPU needed:
+none of these calls reaches the device)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+import mlxl3_amd
+from mlxl3_amd import LIB_PATH, EXPORTED_SYMBOLS
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "exl3_hip.h"
+
+pytestmark = pytest.mark.skipif(not LIB_PATH.exists(), reason="libexl3_hip.so not built")
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(exl3_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    lib = ctypes.CDLL(str(LIB_PATH))
+    names = declared_functions()
+    assert len(names) >= 15
+    for name in names:
+        assert hasattr(lib, name), name
+    assert sorted(EXPORTED_SYMBOLS) == names
+
+
+def test_version_and_empty_error():
+    lib = mlxl3_amd.load_library()
+    assert b"gfx950" in lib.exl3_version()
+    assert isinstance(lib.exl3_last_error(), bytes)
+
+
+FAKE = 0x1000  # never dereferenced by create
+
+
+def create(k=4, cb=0, n_in=256, n_out=256, trellis=FAKE, suh=FAKE, svh=FAKE):
+    lib = mlxl3_amd.load_library()
+    h = ctypes.c_void_p()
+    rc = lib.exl3_linear_create(trellis, n_in, n_out, k, cb, suh, svh, None, ctypes.byref(h))
+    return rc, h, lib.exl3_last_error().decode()
+
+
+@pytest.mark.parametrize(
+    "kwargs,msg",
+    [
+        (dict(k=0), "K must be in 1..=8, got 0"),
+        (dict(k=9), "K must be in 1..=8, got 9"),
+        (dict(cb=3), "invalid EXL3 codebook 3"),
+        (dict(n_in=192), "128-aligned"),
+        (dict(n_out=100), "128-aligned"),
+        (dict(trellis=None), "null weight pointer"),
+    ],
+)
+def test_create_rejects_like_the_reference(kwargs, msg):
+    rc, h, err = create(**kwargs)
+    assert rc == -1 and not h.value
+    assert msg in err
+
+
+def test_create_and_workspace_sizes():
+    lib = mlxl3_amd.load_library()
+    rc, h, _ = create(n_in=4096, n_out=14336)
+    assert rc == 0 and h.value
+    try:
+        assert lib.exl3_linear_in_features(h) == 4096
+        assert lib.exl3_linear_out_features(h) == 14336
+        ws1 = lib.exl3_linear_workspace_bytes(h, 1)
+        ws16 = lib.exl3_linear_workspace_bytes(h, 16)
+        ws512 = lib.exl3_linear_workspace_bytes(h, 512)
+        assert 0 < ws1 < ws16
+        assert ws512 >= 512 * 4096 * 2
+        assert lib.exl3_linear_workspace_bytes(h, 0) == 0
+    finally:
+        lib.exl3_linear_destroy(h)
+
+
+def test_forward_rejects_before_launch():
+    lib = mlxl3_amd.load_library()
+    rc, h, _ = create()
+    try:
+        # rows < 1
+        assert lib.exl3_linear_forward(h, FAKE, 9, 0, FAKE, 9, FAKE, 1 << 20, None) == -1
+        assert "empty" in lib.exl3_last_error().decode()
+        # bad dtype
+        assert lib.exl3_linear_forward(h, FAKE, 7, 1, FAKE, 9, FAKE, 1 << 20, None) == -1
+        # workspace too small
+        assert lib.exl3_linear_forward(h, FAKE, 9, 1, FAKE, 9, FAKE, 4, None) == -1
+        assert "workspace too small" in lib.exl3_last_error().decode()
+        # null activations
+        assert lib.exl3_linear_forward(h, None, 9, 1, FAKE, 9, FAKE, 1 << 20, None) == -1
+    finally:
+        lib.exl3_linear_destroy(h)
+
+
+def test_decode_rejects_bad_k_and_cb():
+    lib = mlxl3_amd.load_library()
+    assert lib.exl3_decode_tiles(FAKE, 1, 0, 0, None, FAKE, None) == -1
+    assert lib.exl3_decode_tiles(FAKE, 1, 4, 5, None, FAKE, None) == -1
+    assert lib.exl3_decode_tiles(FAKE, 0, 4, 0, None, FAKE, None) == 0  # nothing to do
+
+
+def test_group_rejects_mismatched_members():
+    lib = mlxl3_amd.load_library()
+    rc1, a, _ = create(n_in=256)
+    rc2, b, _ = create(n_in=512)
+    try:
+        parts = (ctypes.c_void_p * 2)(a.value, b.value)
+        ys = (ctypes.c_void_p * 2)(FAKE, FAKE)
+        assert lib.exl3_group_forward(parts, 2, FAKE, 9, 1, ys, FAKE, 1 << 20, None) == -1
+        assert "same input width" in lib.exl3_last_error().decode()
+    finally:
+        lib.exl3_linear_destroy(a)
+        lib.exl3_linear_destroy(b)

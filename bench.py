@@ -57,7 +57,7 @@ def make_rotation(n_in, n_out, k, cb, seed, max_copies=None):
     svh_t = torch.from_numpy(svh).to(dev)
     copies = max(2, math.ceil(ROTATE_BYTES / base.numel() / 2))
     if max_copies:
-        copies = min(copies, max_copies)
+        copies = max(1, min(copies, max_copies))
     weights = [base] + [base.clone() for _ in range(copies - 1)]
     lins = [mlxl3_amd.Exl3Linear(w, suh_t, svh_t, None, k, cb) for w in weights]
     return lins, weights
@@ -146,6 +146,8 @@ def main():
     ap.add_argument("--in-features", type=int, default=4096)
     ap.add_argument("--out-features", type=int, default=14336)
     ap.add_argument("--rows", type=int, default=1)
+    ap.add_argument("--copies", type=int, default=0,
+                    help="cap on rotated weight copies (0: enough for 2 GiB; 1 keeps weights cache-resident)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -159,7 +161,7 @@ def main():
 
     torch.cuda.init()
     n_in, n_out, k, cb, rows = args.in_features, args.out_features, args.k, args.cb, args.rows
-    lins, _w = make_rotation(n_in, n_out, k, cb, seed=2)
+    lins, _w = make_rotation(n_in, n_out, k, cb, seed=2, max_copies=args.copies or None)
     x = torch.from_numpy(synth.activations(2, 0, rows, n_in)).cuda()
     ws = torch.zeros(max(l.workspace_bytes(max(rows, 512)) for l in lins[:1]) + 4096,
                      dtype=torch.uint8, device="cuda")

@@ -46,25 +46,36 @@ struct exl3_linear {
   const uint16_t* bias;
   int in, out, k, cb;
   int qmv_splits;
+  int qmv_kw;  // K-parts per column pair inside a workgroup (1, 2, 4)
 };
 
 static constexpr int kQmvMaxRows = 16;
 static constexpr size_t kAlign = 256;
 static size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
-// Split-K count of the fused QMV: enough workgroups to cover the 256 CUs a
-// few times over, at most 8 Hadamard blocks (1024 rows) per split so the LDS
-// copy of xhat stays small, and never more splits than 128-row blocks.
-static int choose_qmv_splits(int in, int out) {
+// QMV launch shape.  Workgroups: out/128 column blocks x `splits` K-ranges
+// (global split-K, reduced by the last workgroup of a column block); inside a
+// workgroup KW waves per column pair split the K-range again (LDS reduction).
+// Target: about two workgroups of 4*KW waves per CU, at most 8 Hadamard
+// blocks (1024 rows) per K-range so xhat fits LDS.  EXL3_QMV_SPLITS and
+// EXL3_QMV_KW override (tuning).
+static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
   const int nb = in / 128, col_blocks = out / 128;
-  if (const char* env = getenv("EXL3_QMV_SPLITS")) {
-    int s = atoi(env);
-    if (s >= 1) return std::min(s, nb);
+  const int min_splits = (nb + 7) / 8;
+  int kw = 2;
+  if (const char* env = getenv("EXL3_QMV_KW")) {
+    int v = atoi(env);
+    if (v == 1 || v == 2 || v == 4) kw = v;
   }
-  const int target_wgs = 1024;
+  const int target_wgs = 512;
   int s = (target_wgs + col_blocks - 1) / col_blocks;
-  s = std::max(s, (nb + 7) / 8);
-  return std::max(1, std::min(s, nb));
+  if (const char* env = getenv("EXL3_QMV_SPLITS")) {
+    int v = atoi(env);
+    if (v >= 1) s = v;
+  }
+  s = std::max(1, std::min(std::max(s, min_splits), nb));
+  *splits_out = s;
+  *kw_out = kw;
 }
 
 static size_t linear_ws_bytes(const exl3_linear* h, int64_t rows) {
@@ -114,7 +125,8 @@ static int linear_forward(const exl3_linear* h, const void* x, int x_type, int64
     for (int s = 0; s < p.splits; ++s)
       max_blocks = std::max(max_blocks, (s + 1) * nb / p.splits - s * nb / p.splits);
     size_t lds = sizeof(uint16_t) * (size_t)rows * max_blocks * 128;
-    kQmv[kidx][cb](p, dim3(h->out / 128, p.splits), lds, stream);
+    const int kwi = h->qmv_kw == 4 ? 2 : h->qmv_kw == 2 ? 1 : 0;
+    kQmv[kwi][kidx][cb](p, dim3(h->out / 128, p.splits), lds, stream);
     return check_launch("EXL3 QMV launch");
   }
 
@@ -132,7 +144,7 @@ static int linear_forward(const exl3_linear* h, const void* x, int x_type, int64
   q.M = (int)rows;
   q.y_dtype = y_type;
   q.col_blocks = h->out / 128;
-  const int mbw = rows >= 512 ? 4 : 2;
+  const int mbw = rows >= 4096 ? 4 : 2;
   const int bm = 64 * mbw;
   const int mtiles = (int)((rows + bm - 1) / bm);
   dim3 grid((unsigned)(mtiles * q.col_blocks));
@@ -170,7 +182,7 @@ int exl3_linear_create(const uint16_t* trellis, int32_t in, int32_t out, int32_t
   h->out = out;
   h->k = k;
   h->cb = cb;
-  h->qmv_splits = choose_qmv_splits(in, out);
+  choose_qmv_shape(in, out, &h->qmv_splits, &h->qmv_kw);
   *out_handle = h;
   return EXL3_OK;
 }

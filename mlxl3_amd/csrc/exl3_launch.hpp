@@ -15,7 +15,7 @@ typedef void (*QmmFn)(const QmmParams&, dim3, hipStream_t);
 typedef void (*DecodeFn)(const uint32_t*, int64_t, uint16_t*, uint16_t*, dim3, hipStream_t);
 
 // [K-1][codebook]
-extern const QmvFn kQmv[8][3];
+extern const QmvFn kQmv[3][8][3];  // [log2 KW]: 1, 2 or 4 K-parts per column pair
 extern const DecodeFn kDecode[8][3];
 extern const QmmFn kQmm2[8][3];  // 128-row workgroup tile
 extern const QmmFn kQmm4[8][3];  // 256-row workgroup tile

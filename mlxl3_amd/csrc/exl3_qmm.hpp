@@ -62,7 +62,7 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
   for (int mb = 0; mb < MBW; ++mb) {
     int row = row_base + 16 * mb + n;
     avalid[mb] = row < p.M;
-    arow[mb] = p.xhat + (size_t)(avalid[mb] ? row : 0) * p.in + g * 16;
+    arow[mb] = p.xhat + (size_t)(avalid[mb] ? row : 0) * p.in + g * 16;  // clamped, in bounds
   }
 
   float4v acc[MBW][8];
@@ -71,42 +71,61 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
 #pragma unroll
     for (int f = 0; f < 8; ++f) acc[mb][f] = float4v{0.f, 0.f, 0.f, 0.f};
 
-  uint32_t wcur[K];
-  load_slice<K>(tp, wcur);
+  // Software pipeline per step q: the trellis slice of q+2 and the A
+  // fragments of q+1 are in flight while step q decodes and multiplies.  All
+  // loads are unconditional (clamped to the last step) so waits stay partial.
+  uint32_t w0[K], w1[K];
+  load_slice<K>(tp, w0);
+  load_slice<K>(tp + (size_t)min(1, nquads - 1) * qstride, w1);
   const half8 zero8 = {};
-  for (int q = 0; q < nquads; ++q) {
+  half8 an[MBW][2];
+  auto load_a = [&](int q) {
+#pragma unroll
+    for (int mb = 0; mb < MBW; ++mb) {
+      const half8* src = (const half8*)(arow[mb] + min(q, nquads - 1) * 64);
+      an[mb][0] = src[0];
+      an[mb][1] = src[1];
+    }
+  };
+  load_a(0);
+  auto step = [&](uint32_t(&w)[K], int q) {
     const int buf = q & 1;
+    half8 a[MBW][2];
+#pragma unroll
+    for (int mb = 0; mb < MBW; ++mb) {
+      a[mb][0] = avalid[mb] ? an[mb][0] : zero8;
+      a[mb][1] = avalid[mb] ? an[mb][1] : zero8;
+    }
+    load_a(q + 1);
     {
       uint32_t B[K + 1];
-      B[0] = prev_word(wcur[K - 1], lane);
+      B[0] = prev_word(w[K - 1], lane);
 #pragma unroll
-      for (int i = 0; i < K; ++i) B[i + 1] = wcur[i];
-      if (q + 1 < nquads) load_slice<K>(tp + (size_t)(q + 1) * qstride, wcur);
+      for (int i = 0; i < K; ++i) B[i + 1] = w[i];
       uint32_t src[32];
       extract_states<K>(B, src);
+      load_slice<K>(tp + (size_t)min(q + 2, nquads - 1) * qstride, w);
       bsh[buf][wave][0][lane] = __builtin_bit_cast(u32x4, decode_fragment<CB, K, 0, 0>(src));
       bsh[buf][wave][1][lane] = __builtin_bit_cast(u32x4, decode_fragment<CB, K, 0, 1>(src));
       bsh[buf][wave][2][lane] = __builtin_bit_cast(u32x4, decode_fragment<CB, K, 1, 0>(src));
       bsh[buf][wave][3][lane] = __builtin_bit_cast(u32x4, decode_fragment<CB, K, 1, 1>(src));
     }
-    half8 a[MBW][2];
-#pragma unroll
-    for (int mb = 0; mb < MBW; ++mb) {
-      a[mb][0] = avalid[mb] ? *(const half8*)(arow[mb] + q * 64) : zero8;
-      a[mb][1] = avalid[mb] ? *(const half8*)(arow[mb] + q * 64 + 8) : zero8;
-    }
     __syncthreads();
 #pragma unroll
-    for (int w = 0; w < 4; ++w)
+    for (int w2 = 0; w2 < 4; ++w2)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int cg = 0; cg < 2; ++cg) {
-          half8 b = __builtin_bit_cast(half8, bsh[buf][w][h * 2 + cg][lane]);
+          half8 b = __builtin_bit_cast(half8, bsh[buf][w2][h * 2 + cg][lane]);
 #pragma unroll
           for (int mb = 0; mb < MBW; ++mb)
-            acc[mb][w * 2 + cg] = mfma16(a[mb][h], b, acc[mb][w * 2 + cg]);
+            acc[mb][w2 * 2 + cg] = mfma16(a[mb][h], b, acc[mb][w2 * 2 + cg]);
         }
+  };
+  for (int q = 0; q < nquads; q += 2) {
+    step(w0, q);
+    if (q + 1 < nquads) step(w1, q + 1);
   }
 
   // in-register epilogue; v[f] with f = 2*w + cg is column 32w + 16*(n>>3) + 8cg + (n&7)

@@ -26,6 +26,18 @@
 namespace exl3 {
 
 
+// Slices per prefetch set of the QMV weight stream (two sets in flight).
+template <int K>
+constexpr int kQmvDepth = K <= 4 ? 4 : 2;
+
+// Split-K partials cross workgroups (and XCDs): agent-scope relaxed atomics.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Load the K words of this lane's slice of a tile.
 template <int K>
 __device__ __forceinline__ void load_slice(const uint32_t* __restrict__ p, uint32_t (&w)[K]) {
@@ -82,78 +94,160 @@ __device__ __forceinline__ void finish_row128(float v0, float v1, int lane, int 
   store_out(y, y_dtype, row_off + c1, v1, bias, c1);
 }
 
-// Prologue for one row of one 128-input block: returns xhat for elements
-// (lane, lane+64) of the block.
-__device__ __forceinline__ void prepare_row128(const void* x, int x_dtype, size_t off,
-                                               const uint16_t* __restrict__ suh, int e0, int lane,
-                                               float& v0, float& v1) {
-  v0 = round_f16(round_f16(load_act(x, x_dtype, off + lane)) * h2f(suh[e0 + lane]));
-  v1 = round_f16(round_f16(load_act(x, x_dtype, off + lane + 64)) * h2f(suh[e0 + lane + 64]));
+// Prologue for one row of one 128-input block, split into its loads and its
+// arithmetic so callers can put other memory traffic between the two:
+// xhat = f16(H128(f16(f16(x) * suh)) / sqrt(128)) for elements (lane, lane+64).
+struct PrologueIn {
+  uint32_t x0lo, x0hi, x1lo, x1hi;  // raw 16-bit halves of the two activations
+  uint32_t s0, s1;                  // raw suh bits (f16)
+};
+// Raw 16-bit loads only (two per element, the second one covers the high half
+// of an f32; for 16-bit types it re-reads the element): no dtype branch, so
+// the loads stay in flight until prologue_finish consumes them.
+__device__ __forceinline__ PrologueIn prologue_load(const void* x, int x_dtype, size_t off,
+                                                    const uint16_t* __restrict__ suh, int e0,
+                                                    int lane) {
+  const uint16_t* xb = (const uint16_t*)x;
+  const size_t esz = x_dtype == DT_F32 ? 2 : 1;  // u16 words per element
+  const size_t hi = esz - 1;
+  const size_t i0 = (off + lane) * esz, i1 = (off + lane + 64) * esz;
+  PrologueIn in;
+  in.x0lo = xb[i0];
+  in.x0hi = xb[i0 + hi];
+  in.x1lo = xb[i1];
+  in.x1hi = xb[i1 + hi];
+  in.s0 = suh[e0 + lane];
+  in.s1 = suh[e0 + lane + 64];
+  return in;
+}
+__device__ __forceinline__ float raw_act(uint32_t bits, int x_dtype) {
+  if (x_dtype == DT_F32) return __builtin_bit_cast(float, bits);
+  if (x_dtype == DT_BF16) return bf2f((uint16_t)bits);
+  return h2f((uint16_t)bits);
+}
+__device__ __forceinline__ void prologue_finish(const PrologueIn& in, int x_dtype, int lane,
+                                                float& v0, float& v1) {
+  const uint32_t x0 = in.x0lo | (in.x0hi << 16), x1 = in.x1lo | (in.x1hi << 16);
+  v0 = round_f16(round_f16(raw_act(x0, x_dtype)) * h2f((uint16_t)in.s0));
+  v1 = round_f16(round_f16(raw_act(x1, x_dtype)) * h2f((uint16_t)in.s1));
   h128_wave<true>(v0, v1, lane);
   v0 = round_f16(v0 * kHadScale);
   v1 = round_f16(v1 * kHadScale);
 }
+__device__ __forceinline__ void prepare_row128(const void* x, int x_dtype, size_t off,
+                                               const uint16_t* __restrict__ suh, int e0, int lane,
+                                               float& v0, float& v1) {
+  prologue_finish(prologue_load(x, x_dtype, off, suh, e0, lane), x_dtype, lane, v0, v1);
+}
 
-template <int K, int CB>
-__global__ __launch_bounds__(256) void qmv_kernel(QmvParams p) {
+// KW waves share each column pair and split the workgroup's K-range between
+// them (reduced through LDS in a fixed order), so a workgroup of 4*KW waves
+// amortises one prologue over KW times more weight stream.
+template <int K, int CB, int KW>
+__global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   extern __shared__ __attribute__((aligned(16))) _Float16 xs[];  // [M][rows of split]
   __shared__ int s_last;
+  __shared__ float4v red[KW > 1 ? KW - 1 : 1][4][2][64];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int pair = wave & 3, kpart = wave >> 2;
   const int TN = p.out >> 4, NB = p.in >> 7;
   const int cblk = blockIdx.x, split = blockIdx.y;
   const int b0 = split * NB / p.splits, b1 = (split + 1) * NB / p.splits;
-  const int row0 = b0 * 128, nrows = (b1 - b0) * 128, nquads = nrows >> 6;
+  const int row0 = b0 * 128, nrows = (b1 - b0) * 128, nq_wg = nrows >> 6;
+  const int q_lo = kpart * nq_wg / KW, q_hi = (kpart + 1) * nq_wg / KW;
+  const int nquads = q_hi - q_lo;
   const int M = p.M;
 
-  // weight stream pointers; first loads go out before the prologue
+  // The first prologue job's activation loads go out first, then the weight
+  // stream's first set, so the Hadamard below waits only for the (shared,
+  // cache-resident) activations while the weight loads are in flight.
+  const int nb = b1 - b0;
+  const int njobs = M * nb;
+  PrologueIn first;
+  {
+    const int job = min(wave, njobs - 1);  // waves without a job load a valid one
+    const int m = job / nb, b = job - m * nb;
+    first = prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128, p.suh,
+                          row0 + b * 128, lane);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
   const int g = lane >> 4, hsel = (lane >> 3) & 1, j = lane & 7;
-  const int tn0 = cblk * 8 + wave * 2;
+  const int tn0 = cblk * 8 + pair * 2;
   const size_t qstride = (size_t)4 * TN * 8 * K;
-  const uint32_t* tp =
-      p.trellis + ((size_t)((row0 >> 4) + g) * TN + tn0 + hsel) * (8 * K) + (size_t)j * K;
-  uint32_t wa[K], wb[K];
-  load_slice<K>(tp, wa);
-  if (nquads > 1) load_slice<K>(tp + qstride, wb);
+  const uint32_t* tp = p.trellis +
+                       ((size_t)((row0 >> 4) + 4 * q_lo + g) * TN + tn0 + hsel) * (8 * K) +
+                       (size_t)j * K;
+  constexpr int D = kQmvDepth<K>;
+  uint32_t setA[D][K], setB[D][K];
+  const int qlast = nquads > 0 ? nquads - 1 : 0;
+#pragma unroll
+  for (int d = 0; d < D; ++d) load_slice<K>(tp + (size_t)min(d, qlast) * qstride, setA[d]);
+  __builtin_amdgcn_sched_barrier(0);
 
   // prologue into LDS
-  const int nb = b1 - b0;
-  for (int job = wave; job < M * nb; job += 4) {
-    int m = job / nb, b = job - m * nb;
+  for (int job = wave; job < njobs; job += 4 * KW) {
+    const int m = job / nb, b = job - m * nb;
+    PrologueIn in = job == wave ? first
+                                : prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128,
+                                                p.suh, row0 + b * 128, lane);
     float v0, v1;
-    prepare_row128(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128, p.suh, row0 + b * 128, lane,
-                   v0, v1);
+    prologue_finish(in, p.x_dtype, lane, v0, v1);
     xs[m * nrows + b * 128 + lane] = (_Float16)v0;
     xs[m * nrows + b * 128 + lane + 64] = (_Float16)v1;
   }
   __syncthreads();
 
-  // main loop
+  // main loop: two sets of D slices in ping-pong; the D loads of one set are
+  // issued together, then the other set (already in flight for D steps) is
+  // decoded, so a wait at any point still has D steps of decode behind it
   const int am = lane & 15;
   const bool arow = am < M;
-  const _Float16* xrow = xs + (size_t)am * nrows + g * 16;
+  const _Float16* xrow = xs + (size_t)am * nrows + 64 * q_lo + g * 16;
   float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   const half8 zero8 = {};
-  for (int q = 0; q < nquads; q += 2) {
-    {
-      half8 a0 = arow ? *(const half8*)(xrow + q * 64) : zero8;
-      half8 a1 = arow ? *(const half8*)(xrow + q * 64 + 8) : zero8;
-      uint32_t cur[K];
+  auto compute = [&](uint32_t(&set)[D][K], int qbase) {
 #pragma unroll
-      for (int i = 0; i < K; ++i) cur[i] = wa[i];
-      if (q + 2 < nquads) load_slice<K>(tp + (size_t)(q + 2) * qstride, wa);
-      qmv_step<K, CB>(cur, lane, a0, a1, acc0, acc1);
+    for (int d = 0; d < D; ++d) {
+      const int q = qbase + d;
+      if (q < nquads) {
+        half8 a0 = arow ? *(const half8*)(xrow + q * 64) : zero8;
+        half8 a1 = arow ? *(const half8*)(xrow + q * 64 + 8) : zero8;
+        qmv_step<K, CB>(set[d], lane, a0, a1, acc0, acc1);
+      }
     }
-    if (q + 1 < nquads) {
-      half8 a0 = arow ? *(const half8*)(xrow + (q + 1) * 64) : zero8;
-      half8 a1 = arow ? *(const half8*)(xrow + (q + 1) * 64 + 8) : zero8;
-      uint32_t cur[K];
+  };
+  // Unconditional loads (past-the-end quads re-read the last one) keep the
+  // load count static, so the waits before each decode can be partial.
+  auto fetch = [&](uint32_t(&set)[D][K], int qbase) {
 #pragma unroll
-      for (int i = 0; i < K; ++i) cur[i] = wb[i];
-      if (q + 3 < nquads) load_slice<K>(tp + (size_t)(q + 3) * qstride, wb);
-      qmv_step<K, CB>(cur, lane, a0, a1, acc0, acc1);
+    for (int d = 0; d < D; ++d)
+      load_slice<K>(tp + (size_t)min(qbase + d, qlast) * qstride, set[d]);
+  };
+  for (int q0 = 0; q0 < nquads; q0 += 2 * D) {
+    fetch(setB, q0 + D);
+    compute(setA, q0);
+    fetch(setA, q0 + 2 * D);
+    compute(setB, q0 + D);
+  }
+
+  // K-parts of a pair meet in LDS; part 0 adds them in part order
+  if constexpr (KW > 1) {
+    if (kpart > 0) {
+      red[kpart - 1][pair][0][lane] = acc0;
+      red[kpart - 1][pair][1][lane] = acc1;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kp = 0; kp < KW - 1; ++kp) {
+      acc0 += red[kp][pair][0][lane];
+      acc1 += red[kp][pair][1][lane];
     }
   }
+  // every wave stays to the end (each barrier is reached by the whole
+  // workgroup); only K-part 0 stores and finishes
+  const bool writer = kpart == 0;
 
   // accumulator lane l: rows 4*(l/16)+r, column 16*(tn0 + n/8) + n%8 + 8*cg
   const int n = lane & 15;
@@ -162,37 +256,39 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvParams p) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     int m = 4 * g + r;
-    if (m < M) {
-      part[(size_t)m * p.out + col] = acc0[r];
-      part[(size_t)m * p.out + col + 8] = acc1[r];
+    if (writer && m < M) {
+      store_coherent(part + (size_t)m * p.out + col, acc0[r]);
+      store_coherent(part + (size_t)m * p.out + col + 8, acc1[r]);
     }
   }
 
-  // last workgroup of this column block finishes it
+  // last workgroup of this column block finishes it.  Partials and counters
+  // are exchanged only through agent-scope relaxed atomics (served at the
+  // device coherence point, no L2 writeback); s_waitcnt + barrier order every
+  // partial store of the workgroup before its counter increment.
   if (p.splits > 1) {
-    __threadfence();
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
-      __threadfence();
-      uint32_t old = __hip_atomic_fetch_add(&p.counters[cblk], 1u, __ATOMIC_ACQ_REL,
+      uint32_t old = __hip_atomic_fetch_add(&p.counters[cblk], 1u, __ATOMIC_RELAXED,
                                             __HIP_MEMORY_SCOPE_AGENT);
       s_last = (old == (uint32_t)(p.splits - 1));
     }
     __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    if (threadIdx.x == 0) p.counters[cblk] = 0u;
+    if (!s_last) return;  // uniform across the workgroup
+    if (threadIdx.x == 0)
+      __hip_atomic_store(&p.counters[cblk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
-    __threadfence_block();
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
   const int colb = cblk * 128;
-  for (int m = wave; m < M; m += 4) {
+  for (int m = wave; m < M; m += 4 * KW) {
     float v0 = 0.f, v1 = 0.f;
     for (int s = 0; s < p.splits; ++s) {
       const float* ps = p.partials + ((size_t)s * M + m) * p.out + colb;
-      v0 += __builtin_nontemporal_load(ps + lane);
-      v1 += __builtin_nontemporal_load(ps + lane + 64);
+      v0 += load_coherent(ps + lane);
+      v1 += load_coherent(ps + lane + 64);
     }
     finish_row128(v0, v1, lane, colb, p.svh, p.bias, p.y, p.y_dtype, (size_t)m * p.out);
   }

@@ -62,12 +62,12 @@ static size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
   const int nb = in / 128, col_blocks = out / 128;
   const int min_splits = (nb + 7) / 8;
-  int kw = 2;
+  int kw = 1;
   if (const char* env = getenv("EXL3_QMV_KW")) {
     int v = atoi(env);
     if (v == 1 || v == 2 || v == 4) kw = v;
   }
-  const int target_wgs = 512;
+  const int target_wgs = 448;
   int s = (target_wgs + col_blocks - 1) / col_blocks;
   if (const char* env = getenv("EXL3_QMV_SPLITS")) {
     int v = atoi(env);

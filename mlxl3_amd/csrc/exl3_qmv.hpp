@@ -38,6 +38,28 @@ __device__ __forceinline__ float load_coherent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Load the previous lane's last word of the same tile (word j*K-1, wrapping to
+// the tile's last word for j == 0) and then the K words of this lane's slice
+// of a tile: w[0] = previous word, w[1..K] = own words.  `p` points at the
+// lane's own words; `prev_off` is -1 or 8K-1.
+template <int K>
+__device__ __forceinline__ void load_slice_prev(const uint32_t* __restrict__ p, int prev_off,
+                                                uint32_t (&w)[K + 1]) {
+  w[0] = __builtin_nontemporal_load(p + prev_off);
+  if constexpr (K == 4) {
+    u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    w[1] = v[0], w[2] = v[1], w[3] = v[2], w[4] = v[3];
+  } else if constexpr (K == 8) {
+    u32x4 v0 = __builtin_nontemporal_load((const u32x4*)p);
+    u32x4 v1 = __builtin_nontemporal_load((const u32x4*)p + 1);
+    w[1] = v0[0], w[2] = v0[1], w[3] = v0[2], w[4] = v0[3];
+    w[5] = v1[0], w[6] = v1[1], w[7] = v1[2], w[8] = v1[3];
+  } else {
+#pragma unroll
+    for (int i = 0; i < K; ++i) w[i + 1] = __builtin_nontemporal_load(p + i);
+  }
+}
+
 // Load the K words of this lane's slice of a tile.
 template <int K>
 __device__ __forceinline__ void load_slice(const uint32_t* __restrict__ p, uint32_t (&w)[K]) {
@@ -53,6 +75,23 @@ __device__ __forceinline__ void load_slice(const uint32_t* __restrict__ p, uint3
 #pragma unroll
     for (int i = 0; i < K; ++i) w[i] = __builtin_nontemporal_load(p + i);
   }
+}
+
+// Decode the 4 B fragments of one 8-tile load and run the 4 MFMAs.  B[0] is
+// the previous lane's last word of the same tile, B[1..K] the lane's words.
+template <int K, int CB>
+__device__ __forceinline__ void qmv_step_prev(const uint32_t (&B)[K + 1], half8 a0, half8 a1,
+                                              float4v& acc0, float4v& acc1) {
+  uint32_t src[32];
+  extract_states<K>(B, src);
+  half8 b00 = decode_fragment<CB, K, 0, 0>(src);
+  half8 b01 = decode_fragment<CB, K, 0, 1>(src);
+  acc0 = mfma16(a0, b00, acc0);
+  acc1 = mfma16(a0, b01, acc1);
+  half8 b10 = decode_fragment<CB, K, 1, 0>(src);
+  half8 b11 = decode_fragment<CB, K, 1, 1>(src);
+  acc0 = mfma16(a1, b10, acc0);
+  acc1 = mfma16(a1, b11, acc1);
 }
 
 // Decode the 4 B fragments of one 8-tile load and run the 4 MFMAs.
@@ -158,6 +197,10 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   const int q_lo = kpart * nq_wg / KW, q_hi = (kpart + 1) * nq_wg / KW;
   const int nquads = q_hi - q_lo;
   const int M = p.M;
+  // Issue priority falls with progress (3 -> 0 over the K-range): the SIMD's
+  // arbiter otherwise favours the oldest wave, which starves later waves until
+  // it finishes and leaves them to run alone at single-wave efficiency.
+  __builtin_amdgcn_s_setprio(3);
 
   // The first prologue job's activation loads go out first, then the weight
   // stream's first set, so the Hadamard below waits only for the (shared,
@@ -180,10 +223,12 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
                        ((size_t)((row0 >> 4) + 4 * q_lo + g) * TN + tn0 + hsel) * (8 * K) +
                        (size_t)j * K;
   constexpr int D = kQmvDepth<K>;
-  uint32_t setA[D][K], setB[D][K];
+  const int prev_off = j == 0 ? 8 * K - 1 : -1;  // previous lane's last word of the tile
+  uint32_t setA[D][K + 1], setB[D][K + 1];
   const int qlast = nquads > 0 ? nquads - 1 : 0;
 #pragma unroll
-  for (int d = 0; d < D; ++d) load_slice<K>(tp + (size_t)min(d, qlast) * qstride, setA[d]);
+  for (int d = 0; d < D; ++d)
+    load_slice_prev<K>(tp + (size_t)min(d, qlast) * qstride, prev_off, setA[d]);
   __builtin_amdgcn_sched_barrier(0);
 
   // prologue into LDS
@@ -207,23 +252,29 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   const _Float16* xrow = xs + (size_t)am * nrows + 64 * q_lo + g * 16;
   float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   const half8 zero8 = {};
-  auto compute = [&](uint32_t(&set)[D][K], int qbase) {
+  auto compute = [&](uint32_t(&set)[D][K + 1], int qbase) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const int q = qbase + d;
       if (q < nquads) {
         half8 a0 = arow ? *(const half8*)(xrow + q * 64) : zero8;
         half8 a1 = arow ? *(const half8*)(xrow + q * 64 + 8) : zero8;
-        qmv_step<K, CB>(set[d], lane, a0, a1, acc0, acc1);
+        qmv_step_prev<K, CB>(set[d], a0, a1, acc0, acc1);
+        if (4 * (q + 1) / nquads != 4 * q / nquads) {
+          const int level = 4 * (q + 1) / nquads;  // quarter of the K-range completed
+          if (level == 1) __builtin_amdgcn_s_setprio(2);
+          else if (level == 2) __builtin_amdgcn_s_setprio(1);
+          else __builtin_amdgcn_s_setprio(0);
+        }
       }
     }
   };
   // Unconditional loads (past-the-end quads re-read the last one) keep the
   // load count static, so the waits before each decode can be partial.
-  auto fetch = [&](uint32_t(&set)[D][K], int qbase) {
+  auto fetch = [&](uint32_t(&set)[D][K + 1], int qbase) {
 #pragma unroll
     for (int d = 0; d < D; ++d)
-      load_slice<K>(tp + (size_t)min(qbase + d, qlast) * qstride, set[d]);
+      load_slice_prev<K>(tp + (size_t)min(qbase + d, qlast) * qstride, prev_off, set[d]);
   };
   for (int q0 = 0; q0 < nquads; q0 += 2 * D) {
     fetch(setB, q0 + D);

@@ -161,6 +161,38 @@ def test_basis_rows_bit_exact(k, cb, rows):
     assert np.array_equal(y.view(np.uint16), ref.view(np.uint16)), float(np.mean(y == ref))
 
 
+@pytest.mark.parametrize("kw,splits", [(1, 1), (1, 3), (2, 2), (2, 5), (4, 1), (4, 4), (1, 8)])
+def test_qmv_schedules_bit_exact(kw, splits, monkeypatch):
+    """Every QMV schedule (global K-splits x K-parts per workgroup) is
+    bit-exact on basis rows and matches the oracle on random inputs."""
+    import mlxl3_amd
+
+    torch = torch_mod()
+    monkeypatch.setenv("EXL3_QMV_KW", str(kw))
+    monkeypatch.setenv("EXL3_QMV_SPLITS", str(splits))
+    n_in, n_out, k, cb = 1024, 1280, 4, 0
+    tr, _, svh, _ = synth.linear_layer(9000 + 10 * kw + splits, 10, n_in, n_out, k)
+    suh = np.ones(n_in, np.float16)
+    dev = lambda a: torch.from_numpy(a.view(np.int16) if a.dtype == np.uint16 else a).cuda()
+    lin = mlxl3_amd.Exl3Linear(dev(tr), dev(suh), dev(svh), None, k, cb)
+    x, _ = basis_inputs(16, n_in, kw * 10 + splits)
+    y = run(lin, x).cpu().numpy()
+    assert np.array_equal(y.view(np.uint16), oracle.forward(x, tr, suh, svh, k, cb).view(np.uint16))
+    xr = synth.activations(9, kw * 10 + splits, 3, n_in)
+    yr = run(lin, xr).cpu().numpy()
+    check(yr, oracle.forward(xr, tr, suh, svh, k, cb), TOL_MODE1_REL, TOL_MODE1_ULP,
+          f"kw{kw} splits{splits}")
+
+
+def test_north_star_shape_qmv():
+    """4096 x 14336, K=4 3INST, batch 1 (the headline workload) vs the oracle."""
+    lin, (tr, suh, svh, _) = make_layer(2, 4096, 14336, 4, 0)
+    x = synth.activations(2, 0, 1, 4096)
+    y = run(lin, x).cpu().numpy()
+    check(y, oracle.forward(x, tr, suh, svh, 4, 0, mode=1), TOL_MODE1_REL, TOL_MODE1_ULP, "NS mode1")
+    check(y, oracle.forward(x, tr, suh, svh, 4, 0, mode=0), TOL_MODE0_REL, TOL_MODE0_ULP, "NS mode0")
+
+
 def test_qmm_rows_independent_of_batch():
     lin, _ = make_layer(5000, 512, 384, 4, 0)
     x = synth.activations(7, 0, 300, 512)

@@ -104,6 +104,17 @@ def time_steps(lins, x, steps, warmup, ws):
     return ms, outs[0]
 
 
+def measured_traffic(workload):
+    """HBM bytes per launch of the dominant kernel for `workload`, as measured
+    by rocprofv3 FETCH_SIZE + WRITE_SIZE (scaled by a known-size copy) and
+    recorded in profiles/traffic.json; None when not measured."""
+    path = ROOT / "profiles" / "traffic.json"
+    try:
+        return json.loads(path.read_text())[workload]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(n_in, n_out, k, cb, rows, budget_s=12.0):
     import numpy as np
 
@@ -146,6 +157,9 @@ def main():
     ap.add_argument("--in-features", type=int, default=4096)
     ap.add_argument("--out-features", type=int, default=14336)
     ap.add_argument("--rows", type=int, default=1)
+    ap.add_argument("--calibrate-copy-mb", type=int, default=0,
+                    help="first run a device-to-device copy of this many MiB (a known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     ap.add_argument("--copies", type=int, default=0,
                     help="cap on rotated weight copies (0: enough for 2 GiB; 1 keeps weights cache-resident)")
     args = ap.parse_args()
@@ -160,6 +174,13 @@ def main():
     from mlxl3_amd import synth
 
     torch.cuda.init()
+    if args.calibrate_copy_mb:
+        src = torch.ones(args.calibrate_copy_mb << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     n_in, n_out, k, cb, rows = args.in_features, args.out_features, args.k, args.cb, args.rows
     lins, _w = make_rotation(n_in, n_out, k, cb, seed=2, max_copies=args.copies or None)
     x = torch.from_numpy(synth.activations(2, 0, rows, n_in)).cuda()
@@ -194,7 +215,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(f"qmv_{n_in}x{n_out}_k{k}_{['3inst', 'mcg', 'mul1'][cb]}_m{rows}"),
         },
     }
     del lins, _w

@@ -1,24 +1,196 @@
-// MoE SwitchGLU entry points (grouped expert QMM); filled in with the kernels.
+// MoE SwitchGLU entry points (Exl3SwitchGlu, native/src/moe.rs:611-1085):
+// validation as switch_glu_layout (native/src/contracts.rs:4-28) and
+// Exl3SwitchGlu::new (moe.rs:835-886), workspace layout, and the five
+// launches of the grouped expert path (route plan, gather, gate/up QMM with
+// the fused SwiGLU glue, down QMM with the fused per-slot finish, top-k sum).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <new>
+
 #include "../../include/exl3_hip.h"
 #include "exl3_launch.hpp"
+#include "exl3_moe.hpp"
+
+namespace exl3 {
+#define EXL3_MOE_INST(K, CB)                                                  \
+  template __global__ void moe_gateup_kernel<K, CB>(MoeQmmParams);           \
+  template __global__ void moe_down_kernel<K, CB>(MoeQmmParams);
+// K = 7 is not a SwitchGLU width (switch_glu_layout rejects it).
+EXL3_INST_CB(EXL3_MOE_INST, 1)
+EXL3_INST_CB(EXL3_MOE_INST, 2)
+EXL3_INST_CB(EXL3_MOE_INST, 3)
+EXL3_INST_CB(EXL3_MOE_INST, 4)
+EXL3_INST_CB(EXL3_MOE_INST, 5)
+EXL3_INST_CB(EXL3_MOE_INST, 6)
+EXL3_INST_CB(EXL3_MOE_INST, 8)
+}  // namespace exl3
 
 using namespace exl3;
 
+#ifndef __HIP_DEVICE_COMPILE__
+
+typedef void (*MoeKernel)(MoeQmmParams);
+#define EXL3_MOE_ROW(F, K) {F<K, 0>, F<K, 1>, F<K, 2>}
+#define EXL3_MOE_TABLE(F)                                                                 \
+  {EXL3_MOE_ROW(F, 1), EXL3_MOE_ROW(F, 2), EXL3_MOE_ROW(F, 3), EXL3_MOE_ROW(F, 4),        \
+   EXL3_MOE_ROW(F, 5), EXL3_MOE_ROW(F, 6), {nullptr, nullptr, nullptr}, EXL3_MOE_ROW(F, 8)}
+static const MoeKernel kGateUp[8][3] = EXL3_MOE_TABLE(moe_gateup_kernel);
+static const MoeKernel kDown[8][3] = EXL3_MOE_TABLE(moe_down_kernel);
+
 struct exl3_moe {
-  int dummy;
+  const uint16_t *gu_trellis, *gu_suh, *gu_svh;
+  const uint16_t *down_trellis, *down_suh, *down_svh;
+  int in, hidden, experts, top_k, k, cb;
 };
 
+// The largest bank the plan kernel's LDS histogram holds (3 ints per expert).
+static constexpr int kMoeMaxExperts = 4096;
+static constexpr size_t kMoeAlign = 256;
+static size_t moe_align(size_t v) { return (v + kMoeAlign - 1) / kMoeAlign * kMoeAlign; }
+
+namespace {
+// Workspace layout for `slots` = rows * top_k routed slots.
+struct MoeLayout {
+  size_t counts, rank, sorted, expert_count, table, xgu, xd, z, total;
+  int max_blocks;
+};
+
+bool moe_layout(const exl3_moe* h, int64_t rows, MoeLayout& L) {
+  if (rows < 1) return false;
+  const int64_t slots = rows * h->top_k;
+  if (slots > (int64_t)1 << 24) return false;
+  // each expert's last block may be partial: sum ceil(c_e/64) <= slots/64 + E
+  L.max_blocks = (int)(slots / kMoeBlockRows + h->experts + 1);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t at = off;
+    off = moe_align(off + bytes);
+    return at;
+  };
+  L.counts = take(2 * sizeof(int));
+  L.rank = take((size_t)slots * sizeof(int));
+  L.sorted = take((size_t)slots * sizeof(int));
+  L.expert_count = take((size_t)h->experts * sizeof(int));
+  L.table = take((size_t)L.max_blocks * sizeof(int4));
+  L.xgu = take((size_t)2 * slots * h->in * sizeof(uint16_t));
+  L.xd = take((size_t)slots * h->hidden * sizeof(uint16_t));
+  L.z = take((size_t)slots * h->in * sizeof(uint16_t));
+  L.total = off;
+  return true;
+}
+}  // namespace
+
 extern "C" {
-int exl3_moe_create(const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*,
-                    const uint16_t*, const uint16_t*, int32_t, int32_t, int32_t, int32_t, int32_t,
-                    int32_t, exl3_moe** out_handle) {
-  if (out_handle) *out_handle = nullptr;
-  return fail(EXL3_EUNSUPPORTED, "MoE not built yet");
+
+int exl3_moe_create(const uint16_t* gu_trellis, const uint16_t* gu_suh, const uint16_t* gu_svh,
+                    const uint16_t* down_trellis, const uint16_t* down_suh,
+                    const uint16_t* down_svh, int32_t in, int32_t hidden, int32_t experts,
+                    int32_t top_k, int32_t k, int32_t cb, exl3_moe** out_handle) {
+  if (!out_handle) return fail(EXL3_EINVAL, "out_handle is null");
+  *out_handle = nullptr;
+  if (experts <= 0 || top_k <= 0 || top_k > experts || in <= 0 || hidden <= 0 || in % 128 ||
+      hidden % 128 || k < 1 || k > 8 || k == 7 ||
+      (int64_t)experts * hidden > INT32_MAX || (int64_t)experts * in > INT32_MAX)
+    return fail(EXL3_EINVAL, "invalid or overflowing SwitchGLU dimensions");
+  if (cb < 0 || cb > 2) return fail(EXL3_EINVAL, "invalid EXL3 codebook %d", cb);
+  if (!gu_trellis || !gu_suh || !gu_svh || !down_trellis || !down_suh || !down_svh)
+    return fail(EXL3_EINVAL, "SwitchGLU trellis/scales disagree");
+  if (experts > kMoeMaxExperts)
+    return fail(EXL3_EUNSUPPORTED, "SwitchGLU banks of more than %d experts are not supported",
+                kMoeMaxExperts);
+  exl3_moe* h = new (std::nothrow) exl3_moe;
+  if (!h) return fail(EXL3_ENOMEM, "out of host memory");
+  *h = exl3_moe{gu_trellis, gu_suh, gu_svh, down_trellis, down_suh, down_svh,
+                in,         hidden, experts, top_k,       k,        cb};
+  *out_handle = h;
+  return EXL3_OK;
 }
+
 void exl3_moe_destroy(exl3_moe* h) { delete h; }
-size_t exl3_moe_workspace_bytes(const exl3_moe*, int64_t) { return 0; }
-int exl3_moe_forward(const exl3_moe*, const uint16_t*, int64_t, const uint32_t*, const uint16_t*,
-                     uint16_t*, void*, size_t, void*) {
-  return fail(EXL3_EUNSUPPORTED, "MoE not built yet");
+
+size_t exl3_moe_workspace_bytes(const exl3_moe* h, int64_t rows) {
+  MoeLayout L;
+  if (!h || !moe_layout(h, rows, L)) return 0;
+  return L.total;
 }
+
+int exl3_moe_forward(const exl3_moe* h, const uint16_t* x, int64_t rows,
+                     const uint32_t* selected, const uint16_t* scores, uint16_t* y,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  if (!h) return fail(EXL3_EINVAL, "handle is null");
+  if (rows < 1 || !x || !selected || !scores || !y)
+    return fail(EXL3_EINVAL, "invalid SwitchGLU input/routes");
+  MoeLayout L;
+  if (!moe_layout(h, rows, L)) return fail(EXL3_EINVAL, "MoE slot overflow");
+  if (!workspace || workspace_bytes < L.total)
+    return fail(EXL3_EINVAL, "workspace too small: need %zu bytes, got %zu", L.total,
+                workspace_bytes);
+  const MoeKernel gateup = kGateUp[h->k - 1][h->cb], down = kDown[h->k - 1][h->cb];
+  if (!gateup || !down) return fail(EXL3_EUNSUPPORTED, "no SwitchGLU kernel for K=%d", h->k);
+  const int64_t wide = (int64_t)L.max_blocks * (std::max(h->in, h->hidden) / 128);
+  if (wide * 256 >= ((int64_t)1 << 31))
+    return fail(EXL3_EUNSUPPORTED, "SwitchGLU launch of %lld rows is too large", (long long)rows);
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  const int slots = (int)(rows * h->top_k);
+
+  MoePlanParams pp;
+  pp.selected = selected;
+  pp.slots = slots;
+  pp.experts = h->experts;
+  pp.rank = (int*)(ws + L.rank);
+  pp.sorted_slot = (int*)(ws + L.sorted);
+  pp.table = (int4*)(ws + L.table);
+  pp.counts = (int*)(ws + L.counts);
+  pp.expert_count = (int*)(ws + L.expert_count);
+  moe_plan_kernel<<<1, 1024, (3 * h->experts + 1) * sizeof(int), s>>>(pp);
+  if (int rc = check_launch("moe plan")) return rc;
+
+  uint16_t* xgu = (uint16_t*)(ws + L.xgu);
+  moe_gather_kernel<<<dim3(slots, h->in / 128, 2), 64, 0, s>>>(
+      x, h->in, h->top_k, selected, pp.sorted_slot, pp.counts + 1, h->gu_suh, xgu);
+  if (int rc = check_launch("moe gather")) return rc;
+
+  MoeQmmParams q{};
+  q.experts = h->experts;
+  q.table = pp.table;
+  q.counts = pp.counts;
+  q.sorted_slot = pp.sorted_slot;
+  q.max_blocks = L.max_blocks;
+  q.slots_pad = slots;
+  q.selected = selected;
+  // gate/up: input width `in`, per-expert output `hidden`
+  q.trellis = (const uint32_t*)h->gu_trellis;
+  q.tn_total = 2 * h->experts * h->hidden / 16;
+  q.k_in = h->in;
+  q.width = h->hidden;
+  q.col_blocks = h->hidden / 128;
+  q.xgu = xgu;
+  q.gu_svh = h->gu_svh;
+  q.down_suh = h->down_suh;
+  q.xd = (uint16_t*)(ws + L.xd);
+  gateup<<<L.max_blocks * q.col_blocks, 256, 0, s>>>(q);
+  if (int rc = check_launch("moe gate/up")) return rc;
+
+  // down: input width `hidden`, per-expert output `in`
+  q.trellis = (const uint32_t*)h->down_trellis;
+  q.tn_total = h->experts * h->in / 16;
+  q.k_in = h->hidden;
+  q.width = h->in;
+  q.col_blocks = h->in / 128;
+  q.xin = q.xd;
+  q.down_svh = h->down_svh;
+  q.scores = scores;
+  q.z = (uint16_t*)(ws + L.z);
+  down<<<L.max_blocks * q.col_blocks, 256, 0, s>>>(q);
+  if (int rc = check_launch("moe down")) return rc;
+
+  moe_reduce_kernel<<<dim3((unsigned)rows, (h->in + 255) / 256), 256, 0, s>>>(
+      q.z, selected, h->experts, h->top_k, h->in, y);
+  return check_launch("moe reduce");
 }
+
+}  // extern "C"
+
+#endif  // __HIP_DEVICE_COMPILE__

@@ -86,3 +86,38 @@ def linear_layer(seed: int, base_id: int, in_features: int, out_features: int, k
     svh = signs_scales(seed, base_id + 2, out_features)
     b = signs_scales(seed, base_id + 3, out_features) if bias else None
     return t, suh, svh, b
+
+
+def moe_layer(seed: int, base_id: int, in_features: int, hidden: int, experts: int, k: int):
+    """SwitchGLU expert banks in the reference's layout (moe.rs:756-760, 835-870).
+
+    Returns (gu_trellis [in/16, 2*E*H/16, 16k], gu_suh [E, 2, in], gu_svh [E, 2, H],
+    down_trellis [H/16, E*in/16, 16k], down_suh [E, H], down_svh [E, in]); gate tiles
+    of expert e sit at tile columns [e*H/16, (e+1)*H/16), up tiles at [(E+e)*H/16, ...).
+    The output scales carry 1/sqrt(fan-in), as a quantized checkpoint's svh does, so the
+    SwiGLU product stays in f16 range: svh = f16(+-U(0.5, 1.5) / sqrt(fan_in)).
+    """
+    gu = trellis(seed, base_id, in_features, 2 * experts * hidden, k)
+    gu_suh = signs_scales(seed, base_id + 1, experts * 2 * in_features).reshape(experts, 2, in_features)
+    gu_svh = (signs_scales(seed, base_id + 2, experts * 2 * hidden).astype(np.float64)
+              / np.sqrt(in_features)).astype(np.float16).reshape(experts, 2, hidden)
+    down = trellis(seed, base_id + 3, hidden, experts * in_features, k)
+    down_suh = signs_scales(seed, base_id + 4, experts * hidden).reshape(experts, hidden)
+    down_svh = (signs_scales(seed, base_id + 5, experts * in_features).astype(np.float64)
+                / np.sqrt(hidden)).astype(np.float16).reshape(experts, in_features)
+    return gu, gu_suh, gu_svh, down, down_suh, down_svh
+
+
+def moe_routes(seed: int, tensor_id: int, rows: int, experts: int, top_k: int):
+    """Top-k routing from softmax(N(0,1) logits), probabilities renormalised over the top k.
+
+    Returns (selected uint32 [rows, top_k] in descending-probability order,
+    scores float16 [rows, top_k]).
+    """
+    logits = normal(seed, tensor_id, rows * experts).reshape(rows, experts).astype(np.float32)
+    p = np.exp(logits - logits.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    order = np.argsort(-p, axis=1, kind="stable")[:, :top_k]
+    top = np.take_along_axis(p, order, axis=1)
+    top /= top.sum(axis=1, keepdims=True)
+    return order.astype(np.uint32), top.astype(np.float16)

@@ -118,3 +118,51 @@ def test_group_rejects_mismatched_members():
     finally:
         lib.exl3_linear_destroy(a)
         lib.exl3_linear_destroy(b)
+
+
+def moe_create(n_in=256, hidden=256, experts=8, top_k=2, k=3, cb=0, ptr=FAKE):
+    lib = mlxl3_amd.load_library()
+    h = ctypes.c_void_p()
+    rc = lib.exl3_moe_create(ptr, ptr, ptr, ptr, ptr, ptr, n_in, hidden, experts, top_k, k, cb,
+                             ctypes.byref(h))
+    return rc, h, lib.exl3_last_error().decode()
+
+
+@pytest.mark.parametrize(
+    "kwargs,msg",
+    [
+        # switch_glu_layout (native/src/contracts.rs:4-28) and its unit test
+        (dict(k=7), "invalid or overflowing SwitchGLU dimensions"),
+        (dict(k=0), "invalid or overflowing SwitchGLU dimensions"),
+        (dict(k=9), "invalid or overflowing SwitchGLU dimensions"),
+        (dict(experts=2, top_k=3), "invalid or overflowing SwitchGLU dimensions"),
+        (dict(top_k=0), "invalid or overflowing SwitchGLU dimensions"),
+        (dict(n_in=127), "invalid or overflowing SwitchGLU dimensions"),
+        (dict(hidden=0), "invalid or overflowing SwitchGLU dimensions"),
+        (dict(experts=2**31 - 1, top_k=1), "invalid or overflowing SwitchGLU dimensions"),
+        (dict(cb=3), "invalid EXL3 codebook 3"),
+        (dict(ptr=None), "SwitchGLU trellis/scales disagree"),
+    ],
+)
+def test_moe_create_rejects_like_the_reference(kwargs, msg):
+    rc, h, err = moe_create(**kwargs)
+    assert rc == -1 and not h.value and msg in err
+
+
+def test_moe_create_workspace_and_forward_rejects():
+    lib = mlxl3_amd.load_library()
+    rc, h, err = moe_create()
+    assert rc == 0 and h.value, err
+    try:
+        one = lib.exl3_moe_workspace_bytes(h, 1)
+        many = lib.exl3_moe_workspace_bytes(h, 100)
+        assert 0 < one < many
+        assert lib.exl3_moe_workspace_bytes(h, 0) == 0
+        # rows < 1, null routes, short workspace: rejected before any launch
+        assert lib.exl3_moe_forward(h, FAKE, 0, FAKE, FAKE, FAKE, FAKE, one, None) == -1
+        assert lib.exl3_moe_forward(h, FAKE, 1, None, FAKE, FAKE, FAKE, one, None) == -1
+        assert "invalid SwitchGLU input/routes" in lib.exl3_last_error().decode()
+        assert lib.exl3_moe_forward(h, FAKE, 100, FAKE, FAKE, FAKE, FAKE, one, None) == -1
+        assert "workspace too small" in lib.exl3_last_error().decode()
+    finally:
+        lib.exl3_moe_destroy(h)

@@ -1,0 +1,131 @@
+"""Pins the CPU MoE oracle (oracle/exl3_oracle.c exl3o_moe_forward).
+
+The reference holds no MoE output vectors, so the oracle is checked against a
+second, structurally different composition built from parts that are pinned on
+their own (test_oracle.py): the dense expert matrices from ``reconstruct_inner``
+(golden real tiles and quantizer corpus), the f32 Hadamard (MLX fixture) and the
+staged f16 schedule.  The composition slices the dense banks by column instead of
+walking tiles, so a wrong bank offset, a swapped gate/up projection or a scale
+taken from the wrong expert fails it; each such mistake is planted in the
+composition below and must be detected.  Exact invariants: scaling every score by
+2 scales y by 2 bit-for-bit (f16 and f32 are exact under powers of two), and
+relabelling experts together with their banks leaves y bit-identical.
+Semantics followed: Exl3SwitchGlu::forward (native/src/moe.rs:905-975),
+routed_inputs (:184-250), glu_down_input (:435-563), finish_and_reduce (:586-609).
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from mlxl3_amd import synth
+
+F16 = np.float16
+
+
+def f16(v):
+    return np.asarray(v, np.float32).astype(F16).astype(np.float32)
+
+
+def dense_moe(x, sel, sc, layer, k, cb, mutant=None):
+    gu, gu_suh, gu_svh, down, down_suh, down_svh = layer
+    experts, _, n_in = gu_suh.shape
+    hidden = gu_svh.shape[-1]
+    w_gu = oracle.reconstruct_inner(gu, k, cb, n_in, 2 * experts * hidden).astype(np.float64)
+    w_d = oracle.reconstruct_inner(down, k, cb, hidden, experts * n_in).astype(np.float64)
+    rows, top_k = sel.shape
+    y = np.zeros((rows, n_in), np.float32)
+    for r in range(rows):
+        acc = np.zeros(n_in, np.float32)
+        for t in range(top_k):
+            e = int(sel[r, t])
+            proj = []
+            for p in range(2):
+                sp = 1 - p if mutant == "suh_projection" else p
+                xin = oracle.h128_staged(f16(x[r].astype(np.float32) * gu_suh[e, sp].astype(np.float32)))
+                col = (p * experts + e) * hidden
+                if mutant == "up_offset" and p == 1:
+                    col = (e + 1) % experts * hidden
+                raw = xin.astype(np.float64) @ w_gu[:, col:col + hidden]
+                sv = gu_svh[e, p].astype(np.float32)
+                proj.append(f16(oracle.h128_f32(f16(raw)) * sv))
+            g, u = proj
+            if mutant == "swap_glu":
+                g, u = u, g
+            act = f16((g / (np.float32(1) + np.exp(-g))) * u)
+            dsu = down_suh[(e + 1) % experts if mutant == "down_suh_expert" else e]
+            din = f16(oracle.h128_f32(f16(act * dsu.astype(np.float32))))
+            d = din.astype(np.float64) @ w_d[:, e * n_in:(e + 1) * n_in]
+            d = oracle.h128_staged(f16(d))
+            if mutant != "no_svh":
+                d = f16(d * down_svh[e].astype(np.float32))
+            acc += f16(d * np.float32(sc[r, t]))
+        y[r] = acc
+    return y.astype(F16)
+
+
+def case(in_f=256, hidden=256, experts=6, top_k=2, rows=5, k=3, seed=3):
+    layer = synth.moe_layer(seed, 500, in_f, hidden, experts, k)
+    x = synth.activations(seed, 510, rows, in_f)
+    sel, sc = synth.moe_routes(seed, 520, rows, experts, top_k)
+    return x, sel, sc, layer
+
+
+def rel_l2(a, b):
+    a = a.astype(np.float64)
+    b = b.astype(np.float64)
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+@pytest.mark.parametrize("k,cb", [(2, 0), (3, 0), (3, 1), (4, 2)])
+def test_oracle_moe_matches_dense_composition(k, cb):
+    x, sel, sc, layer = case(k=k)
+    got = oracle.moe_forward(x, sel, sc, *layer, k, cb)
+    want = dense_moe(x, sel, sc, layer, k, cb)
+    # f32 tile-order vs f64 dense accumulation: rare f16 flips before the glue
+    assert rel_l2(got, want) < 1e-3
+    rms = np.sqrt(np.mean(want.astype(np.float64) ** 2))
+    assert np.abs(got.astype(np.float64) - want).max() < 1e-2 * rms
+
+
+@pytest.mark.parametrize("mutant", ["swap_glu", "up_offset", "suh_projection", "down_suh_expert",
+                                    "no_svh"])
+def test_dense_composition_detects_planted_mistakes(mutant):
+    x, sel, sc, layer = case()
+    got = oracle.moe_forward(x, sel, sc, *layer, 3, 0)
+    wrong = dense_moe(x, sel, sc, layer, 3, 0, mutant=mutant)
+    assert rel_l2(wrong, got) > 0.05
+
+
+def test_oracle_moe_scores_scale_exactly():
+    x, sel, sc, layer = case()
+    y1 = oracle.moe_forward(x, sel, sc, *layer, 3, 0)
+    y2 = oracle.moe_forward(x, sel, (sc.astype(np.float32) * 2).astype(F16), *layer, 3, 0)
+    np.testing.assert_array_equal(y2, (y1.astype(np.float32) * 2).astype(F16))
+
+
+def test_oracle_moe_expert_relabelling_is_exact():
+    in_f, hidden, experts, k = 256, 128, 5, 2
+    x, sel, sc, layer = case(in_f=in_f, hidden=hidden, experts=experts, k=k, rows=6)
+    gu, gu_suh, gu_svh, down, down_suh, down_svh = layer
+    perm = np.array([3, 0, 4, 1, 2])  # new expert i is old expert perm[i]
+    inv = np.argsort(perm)
+    ht, it = hidden // 16, in_f // 16
+    gate = gu[:, :experts * ht].reshape(gu.shape[0], experts, ht, -1)[:, perm]
+    up = gu[:, experts * ht:].reshape(gu.shape[0], experts, ht, -1)[:, perm]
+    gu2 = np.concatenate([gate.reshape(gu.shape[0], experts * ht, -1),
+                          up.reshape(gu.shape[0], experts * ht, -1)], axis=1)
+    down2 = down.reshape(down.shape[0], experts, it, -1)[:, perm].reshape(down.shape)
+    layer2 = (gu2, gu_suh[perm], gu_svh[perm], down2, down_suh[perm], down_svh[perm])
+    sel2 = inv[sel].astype(np.uint32)
+    y1 = oracle.moe_forward(x, sel, sc, *layer, k, 0)
+    y2 = oracle.moe_forward(x, sel2, sc, *layer2, k, 0)
+    np.testing.assert_array_equal(y1, y2)
+
+
+def test_oracle_moe_rejects_out_of_bank_routes():
+    x, sel, sc, layer = case()
+    bad = sel.copy()
+    bad[0, 0] = 6
+    with pytest.raises(ValueError):
+        oracle.moe_forward(x, bad, sc, *layer, 3, 0)

@@ -23,7 +23,10 @@ SOURCES = ["exl3_api.hip", "exl3_qmv.hip", "exl3_qmm.hip", "exl3_moe.hip"]
 ARCH = "gfx950"
 
 # -ffp-contract=off: every f32 multiply/add in the glue is rounded separately,
-# as the reference's stages are; -packed-fp32-ops off: no v_pk_*_f32.
+# as the reference's stages are; -packed-fp32-ops off: no v_pk_*_f32;
+# -fma-mix-insts off: the backend selects f16(f32(a) * f32(b)) as
+# v_fma_mix*(a, b, +0), which turns an exact -0 product into +0 (f16 outputs
+# such as f16(+0 * svh) with svh < 0 must keep the sign).
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -34,6 +37,10 @@ HIPCC_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-fma-mix-insts",
     "-Wall",
     "-Wno-unused-function",
 ]

@@ -78,11 +78,62 @@ static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
   *kw_out = kw;
 }
 
+// QMM launch shape: rows per workgroup 64*MB and global K-splits.  One
+// workgroup of 8 waves fills a CU (two waves per SIMD), so the cost model
+// counts rounds of 256 workgroups times K-steps per split times the step
+// time, which is the larger of the consumers' MFMA time (16*MB MFMAs of 16
+// cycles) and the producers' decode time (~720 cycles), plus ~100 cycles of
+// barrier; a split adds its f32 partial traffic (written and read back at
+// ~5 TB/s, i.e. ~0.4 cycles per byte at 2.1 GHz).  Splits are only used while
+// the output tiles alone fill fewer than 192 CUs, so at most 256 tile
+// counters are ever needed.  EXL3_QMM_MB and EXL3_QMM_SPLITS override.
+static constexpr int kTileCounters = 256;
+
+struct QmmShape {
+  int mb, mtiles, splits;
+};
+
+static QmmShape choose_qmm_shape(int in, int out, int64_t rows) {
+  const int col_blocks = out / 128, nq = in / 64;
+  int force_mb = 0, force_splits = 0;
+  if (const char* env = getenv("EXL3_QMM_MB")) {
+    int v = atoi(env);
+    if (v == 1 || v == 2 || v == 4) force_mb = v;
+  }
+  if (const char* env = getenv("EXL3_QMM_SPLITS")) force_splits = std::max(0, atoi(env));
+  QmmShape best{4, 1, 1};
+  double best_cost = 1e300;
+  for (int mb : {4, 2, 1}) {
+    if (force_mb && mb != force_mb) continue;
+    const int64_t mt = (rows + 64 * mb - 1) / (64 * mb);
+    const int64_t base = mt * col_blocks;
+    int splits = 1;
+    if (base < 192) splits = (int)std::min<int64_t>((256 + base - 1) / base, 8);
+    if (force_splits) splits = force_splits;
+    splits = std::max(1, std::min(splits, std::max(1, nq / 4)));
+    if (splits > 1 && base > kTileCounters) splits = 1;
+    const int64_t rounds = (base * splits + 255) / 256;
+    const double step = std::max(256.0 * mb, 720.0) + 100.0;
+    double cost = (double)rounds * ((nq + splits - 1) / splits) * step;
+    if (splits > 1) cost += 0.4 * 2.0 * 4.0 * (double)splits * rows * out;
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = QmmShape{mb, (int)mt, splits};
+    }
+  }
+  return best;
+}
+
+// Workspace: [tile counters][QMV partials | QMM xhat, partials].  The counter
+// region has a fixed size, so one workspace serves QMV and QMM calls in any
+// order (every call leaves its counters at zero).
 static size_t linear_ws_bytes(const exl3_linear* h, int64_t rows) {
-  size_t counters = align_up(sizeof(uint32_t) * (size_t)(h->out / 128));
+  size_t counters = align_up(sizeof(uint32_t) * (size_t)std::max(h->out / 128, kTileCounters));
   if (rows <= kQmvMaxRows)
     return counters + align_up(sizeof(float) * (size_t)h->qmv_splits * rows * h->out);
-  return counters + align_up(sizeof(uint16_t) * (size_t)rows * h->in);
+  const QmmShape sh = choose_qmm_shape(h->in, h->out, rows);
+  size_t partials = sh.splits > 1 ? sizeof(float) * (size_t)sh.splits * rows * h->out : 0;
+  return counters + align_up(sizeof(uint16_t) * (size_t)rows * h->in) + align_up(partials);
 }
 
 // ---------------------------------------------------------------------------
@@ -101,7 +152,8 @@ static int linear_forward(const exl3_linear* h, const void* x, int x_type, int64
   if (!ws || ws_bytes < need)
     return fail(EXL3_EINVAL, "workspace too small: %zu bytes given, %zu needed", ws_bytes, need);
   uint32_t* counters = (uint32_t*)ws;
-  char* after = (char*)ws + align_up(sizeof(uint32_t) * (size_t)(h->out / 128));
+  char* after =
+      (char*)ws + align_up(sizeof(uint32_t) * (size_t)std::max(h->out / 128, kTileCounters));
   const int kidx = h->k - 1, cb = h->cb;
 
   if (rows <= kQmvMaxRows) {
@@ -133,22 +185,26 @@ static int linear_forward(const exl3_linear* h, const void* x, int x_type, int64
   uint16_t* xhat = (uint16_t*)after;
   launch_prologue(x, x_type, h->suh, h->in, (int)rows, xhat, stream);
   if (int rc = check_launch("EXL3 prologue launch")) return rc;
+  const QmmShape sh = choose_qmm_shape(h->in, h->out, rows);
   QmmParams q;
   q.trellis = (const uint32_t*)h->trellis;
   q.xhat = xhat;
   q.svh = h->svh;
   q.bias = h->bias;
   q.y = y;
+  q.partials = (float*)((char*)xhat + align_up(sizeof(uint16_t) * (size_t)rows * h->in));
+  q.counters = counters;
   q.in = h->in;
   q.out = h->out;
   q.M = (int)rows;
   q.y_dtype = y_type;
   q.col_blocks = h->out / 128;
-  const int mbw = rows >= 4096 ? 4 : 2;
-  const int bm = 64 * mbw;
-  const int mtiles = (int)((rows + bm - 1) / bm);
-  dim3 grid((unsigned)(mtiles * q.col_blocks));
-  (mbw == 4 ? kQmm4 : kQmm2)[kidx][cb](q, grid, stream);
+  q.mtiles = sh.mtiles;
+  q.splits = sh.splits;
+  const int mbi = sh.mb == 4 ? 2 : sh.mb == 2 ? 1 : 0;
+  const int64_t wgs = (int64_t)sh.mtiles * q.col_blocks * sh.splits;
+  if (wgs > INT32_MAX) return fail(EXL3_EINVAL, "EXL3 QMM grid too large");
+  kQmm[mbi][kidx][cb](q, dim3((unsigned)wgs), stream);
   return check_launch("EXL3 QMM launch");
 }
 

@@ -281,6 +281,35 @@ __device__ __forceinline__ float4v mfma16(half8 a, half8 b, float4v c) {
 }
 
 // ---------------------------------------------------------------------------
+// lane exchanges: value of lane (lane ^ S) within the wave
+// ---------------------------------------------------------------------------
+// S = 1, 2: DPP quad permutations; 4, 8: a DPP mirror composed with a quad
+// permutation or the half-row mirror (i^7^3 = i^4, i^15^7 = i^8); 16: a
+// ds_swizzle in bit-mask mode (xor 0x10 inside 32 lanes); 32: ds_bpermute.
+template <int S>
+__device__ __forceinline__ float xor_lanes(float v) {
+  const int b = __builtin_bit_cast(int, v);
+  int r;
+  if constexpr (S == 1) {
+    r = __builtin_amdgcn_update_dpp(0, b, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  } else if constexpr (S == 2) {
+    r = __builtin_amdgcn_update_dpp(0, b, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else if constexpr (S == 4) {
+    int t = __builtin_amdgcn_update_dpp(0, b, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    r = __builtin_amdgcn_update_dpp(0, t, 0x1B, 0xF, 0xF, false);       // quad_perm [3,2,1,0]
+  } else if constexpr (S == 8) {
+    int t = __builtin_amdgcn_update_dpp(0, b, 0x140, 0xF, 0xF, false);  // row_mirror
+    r = __builtin_amdgcn_update_dpp(0, t, 0x141, 0xF, 0xF, false);      // row_half_mirror
+  } else if constexpr (S == 16) {
+    r = __builtin_amdgcn_ds_swizzle(b, 0x401F);  // and 0x1f, or 0, xor 0x10
+  } else {
+    static_assert(S == 32, "lane exchange distance");
+    r = __builtin_amdgcn_ds_bpermute((int)((__lane_id() ^ 32) << 2), b);
+  }
+  return __builtin_bit_cast(float, r);
+}
+
+// ---------------------------------------------------------------------------
 // wave-level Hadamard-128: lane holds elements lane and lane+64
 // ---------------------------------------------------------------------------
 // Ascending radix-2 stages (the MLX butterfly order pinned by the reference's
@@ -288,10 +317,10 @@ __device__ __forceinline__ float4v mfma16(half8 a, half8 b, float4v c) {
 // stages (exl3.metal:156-170).  The 1/sqrt(128) scale is left to the caller.
 template <bool STAGED>
 __device__ __forceinline__ void h128_wave(float& v0, float& v1, int lane) {
-#pragma unroll
-  for (int stride = 1; stride < 64; stride <<= 1) {
-    float p0 = __shfl_xor(v0, stride, 64);
-    float p1 = __shfl_xor(v1, stride, 64);
+  static_for<6>([&](auto i_) {
+    constexpr int stride = 1 << decltype(i_)::value;
+    const float p0 = xor_lanes<stride>(v0);
+    const float p1 = xor_lanes<stride>(v1);
     if (lane & stride) {
       v0 = p0 - v0;
       v1 = p1 - v1;
@@ -303,7 +332,7 @@ __device__ __forceinline__ void h128_wave(float& v0, float& v1, int lane) {
       v0 = round_f16(v0);
       v1 = round_f16(v1);
     }
-  }
+  });
   float a = v0, b = v1;
   v0 = a + b;
   v1 = a - b;

@@ -17,8 +17,7 @@ typedef void (*DecodeFn)(const uint32_t*, int64_t, uint16_t*, uint16_t*, dim3, h
 // [K-1][codebook]
 extern const QmvFn kQmv[3][8][3];  // [log2 KW]: 1, 2 or 4 K-parts per column pair
 extern const DecodeFn kDecode[8][3];
-extern const QmmFn kQmm2[8][3];  // 128-row workgroup tile
-extern const QmmFn kQmm4[8][3];  // 256-row workgroup tile
+extern const QmmFn kQmm[3][8][3];  // [log2 MB]: 64, 128 or 256 rows per workgroup
 
 void launch_prologue(const void* x, int x_dtype, const uint16_t* suh, int in, int rows,
                      uint16_t* xhat, hipStream_t s);

@@ -24,8 +24,12 @@ struct QmmParams {
   const uint16_t* svh;      // [out]
   const uint16_t* bias;     // [out] or null
   void* y;                  // [M][out]
+  float* partials;          // [splits][M][out] f32 (splits > 1)
+  uint32_t* counters;       // [mtiles * col_blocks], zero between calls (splits > 1)
   int in, out, M, y_dtype;
   int col_blocks;           // out / 128
+  int mtiles;               // ceil(M / rows per workgroup)
+  int splits;               // K-ranges per output tile (global split-K)
 };
 
 }  // namespace exl3

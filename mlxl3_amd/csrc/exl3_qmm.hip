@@ -5,6 +5,7 @@
 namespace exl3 {
 
 #define EXL3_QMM_INST(K, CB)                                   \
+  template __global__ void qmm_kernel<K, CB, 1>(QmmParams); \
   template __global__ void qmm_kernel<K, CB, 2>(QmmParams); \
   template __global__ void qmm_kernel<K, CB, 4>(QmmParams);
 EXL3_INSTANTIATE(EXL3_QMM_INST)
@@ -17,22 +18,31 @@ __global__ void fill_zero_kernel(uint32_t* p, size_t words) {
 
 // Host-side launchers (not part of the device compilation pass).
 #ifndef __HIP_DEVICE_COMPILE__
+template <int K, int CB, int MB>
+static void run_qmm(const QmmParams& p, dim3 g, hipStream_t s) {
+  hipLaunchKernelGGL((qmm_kernel<K, CB, MB>), g, dim3(512), 0, s, p);
+}
+template <int K, int CB>
+static void run_qmm1(const QmmParams& p, dim3 g, hipStream_t s) {
+  run_qmm<K, CB, 1>(p, g, s);
+}
 template <int K, int CB>
 static void run_qmm2(const QmmParams& p, dim3 g, hipStream_t s) {
-  hipLaunchKernelGGL((qmm_kernel<K, CB, 2>), g, dim3(256), 0, s, p);
+  run_qmm<K, CB, 2>(p, g, s);
 }
 template <int K, int CB>
 static void run_qmm4(const QmmParams& p, dim3 g, hipStream_t s) {
-  hipLaunchKernelGGL((qmm_kernel<K, CB, 4>), g, dim3(256), 0, s, p);
+  run_qmm<K, CB, 4>(p, g, s);
 }
 
-const QmmFn kQmm2[8][3] = EXL3_TABLE(run_qmm2);
-const QmmFn kQmm4[8][3] = EXL3_TABLE(run_qmm4);
+const QmmFn kQmm[3][8][3] = {EXL3_TABLE(run_qmm1), EXL3_TABLE(run_qmm2), EXL3_TABLE(run_qmm4)};
 
 void launch_prologue(const void* x, int x_dtype, const uint16_t* suh, int in, int rows,
                      uint16_t* xhat, hipStream_t s) {
-  hipLaunchKernelGGL(prologue_kernel, dim3(in / 128, rows), dim3(64), 0, s, x, x_dtype, suh, in,
-                     xhat);
+  const int jobs = rows * (in / 128);
+  const int per_wg = 4 * kPrologueJobs;
+  hipLaunchKernelGGL(prologue_kernel, dim3((jobs + per_wg - 1) / per_wg), dim3(256), 0, s, x,
+                     x_dtype, suh, in, jobs, xhat);
 }
 
 void launch_fill_zero(uint32_t* p, size_t words, hipStream_t s) {

@@ -283,9 +283,9 @@ __device__ __forceinline__ float4v mfma16(half8 a, half8 b, float4v c) {
 // ---------------------------------------------------------------------------
 // lane exchanges: value of lane (lane ^ S) within the wave
 // ---------------------------------------------------------------------------
-// S = 1, 2: DPP quad permutations; 4, 8: a DPP mirror composed with a quad
-// permutation or the half-row mirror (i^7^3 = i^4, i^15^7 = i^8); 16: a
-// ds_swizzle in bit-mask mode (xor 0x10 inside 32 lanes); 32: ds_bpermute.
+// S = 1, 2: DPP quad permutations; 4: the half-row mirror composed with a
+// quad reversal (i^7^3 = i^4); 8: a rotation by 8 inside the 16-lane row; 16:
+// a ds_swizzle in bit-mask mode (xor 0x10 inside 32 lanes); 32: ds_bpermute.
 template <int S>
 __device__ __forceinline__ float xor_lanes(float v) {
   const int b = __builtin_bit_cast(int, v);
@@ -298,8 +298,7 @@ __device__ __forceinline__ float xor_lanes(float v) {
     int t = __builtin_amdgcn_update_dpp(0, b, 0x141, 0xF, 0xF, false);  // row_half_mirror
     r = __builtin_amdgcn_update_dpp(0, t, 0x1B, 0xF, 0xF, false);       // quad_perm [3,2,1,0]
   } else if constexpr (S == 8) {
-    int t = __builtin_amdgcn_update_dpp(0, b, 0x140, 0xF, 0xF, false);  // row_mirror
-    r = __builtin_amdgcn_update_dpp(0, t, 0x141, 0xF, 0xF, false);      // row_half_mirror
+    r = __builtin_amdgcn_update_dpp(0, b, 0x128, 0xF, 0xF, false);  // row_ror:8 = xor 8 in 16
   } else if constexpr (S == 16) {
     r = __builtin_amdgcn_ds_swizzle(b, 0x401F);  // and 0x1f, or 0, xor 0x10
   } else {

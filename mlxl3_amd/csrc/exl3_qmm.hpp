@@ -69,6 +69,30 @@ __device__ __forceinline__ float bfly_lane(float v, int lane) {
   return (lane & STRIDE) ? p - v : v + p;
 }
 
+// Rows of a finished tile pass through LDS as f16: Y[row][136] (128 columns
+// plus 8 halves of padding, so the 16-byte reads of one row never meet the
+// next row's banks).
+constexpr int kYStride = 136;
+
+// Consumer side: f16(acc) of one row into Y.  Register f of the lane holds
+// column 32*(f>>1) + 8*(f&1) + lanecol, lanecol = 16*(n>>3) + (n&7), n =
+// lane & 15.  Neighbouring lanes swap one value so that each lane writes two
+// 32-bit column pairs: an even lane columns (c, c+1) of register 2w, an odd
+// lane columns (c-1, c) of register 2w+1.
+__device__ __forceinline__ void qmm_stage_row(const float (&v)[8], int lane, uint16_t* yrow) {
+  const int n = lane & 15;
+  const bool odd = n & 1;
+  const int pcol = 16 * (n >> 3) + (n & 7) + (odd ? 7 : 0);
+  uint32_t* y32 = (uint32_t*)(yrow + pcol);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float mine = odd ? v[2 * w + 1] : v[2 * w];
+    const float other = xor_lanes<1>(odd ? v[2 * w] : v[2 * w + 1]);
+    const float lo = odd ? other : mine, hi = odd ? mine : other;
+    y32[16 * w] = (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
+  }
+}
+
 // 16-bit output bits of the linear epilogue's final cast (+ bias), as
 // store_out computes them.
 __device__ __forceinline__ uint32_t out16(float v16, float b, bool has_bias, int dt) {
@@ -78,75 +102,60 @@ __device__ __forceinline__ uint32_t out16(float v16, float b, bool has_bias, int
   return f2bf(v);
 }
 
-// One row of a 128-column block: v[f] holds column 32*(f>>1) + 16*(n>>3) +
-// 8*(f&1) + (n&7) of the row, n = lane & 15 (f32 sums).  svh and bias of the
-// block come from LDS (f32).  All lanes take part in the exchanges; only
-// `live` lanes store.  16-bit outputs leave as 32-bit pairs: for each
-// register pair (f, f+1) an even lane stores columns (c, c+1) of register f
-// and an odd lane columns (c-1, c) of register f+1, each taking the missing
-// value from its neighbour.
-__device__ __forceinline__ void qmm_finish_row(float (&v)[8], int lane, int colb, int row,
-                                               bool live, const QmmParams& p,
-                                               const float* s_svh, const float* s_bias) {
-  const int n = lane & 15;
+// Finishing side: each lane holds 8 consecutive columns 8*(lane&15)+j of one
+// row (four rows per wave pass): f16 values -> staged Hadamard-128 (strides
+// 1, 2, 4 inside the lane, 8..64 across lanes 1..8, f16 rounding after
+// strides 8 and 64) -> f16(* 1/sqrt 128) -> f16(* svh) -> cast (+ bias) ->
+// one 16-byte store (two for f32).  sv/bv: svh and bias of the lane's columns.
+__device__ __forceinline__ void qmm_finish_chunk(const u32x4 raw, const float (&sv)[8],
+                                                 const float (&bv)[8], int lane, bool live,
+                                                 const QmmParams& p, size_t yoff) {
+  float v[8];
 #pragma unroll
-  for (int f = 0; f < 8; ++f) v[f] = round_f16(v[f]);
-#pragma unroll
-  for (int f = 0; f < 8; ++f) {
-    v[f] = bfly_lane<1>(v[f], lane);
-    v[f] = bfly_lane<2>(v[f], lane);
-    v[f] = bfly_lane<4>(v[f], lane);
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = h2f((uint16_t)raw[i]);
+    v[2 * i + 1] = h2f((uint16_t)(raw[i] >> 16));
   }
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {  // stride 8: cg pair
-    float a0 = v[2 * w], b0 = v[2 * w + 1];
-    v[2 * w] = round_f16(a0 + b0);
-    v[2 * w + 1] = round_f16(a0 - b0);
+  for (int s = 1; s < 8; s <<= 1)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (!(j & s)) {
+        const float a0 = v[j], b0 = v[j + s];
+        v[j] = a0 + b0;
+        v[j + s] = a0 - b0;
+      }
+  // stride 8 = lane bit 0, then f16 rounding
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = round_f16(bfly_lane<1>(v[j], lane));
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    v[j] = bfly_lane<2>(v[j], lane);  // stride 16
+    v[j] = bfly_lane<4>(v[j], lane);  // stride 32
+    v[j] = round_f16(bfly_lane<8>(v[j], lane));  // stride 64
   }
 #pragma unroll
-  for (int f = 0; f < 8; ++f) v[f] = bfly_lane<8>(v[f], lane);  // column stride 16: lane bit 3
-#pragma unroll
-  for (int cg = 0; cg < 2; ++cg) {
-#pragma unroll
-    for (int wl = 0; wl < 4; wl += 2) {  // stride 32: w bit 0
-      float a0 = v[2 * wl + cg], b0 = v[2 * (wl + 1) + cg];
-      v[2 * wl + cg] = a0 + b0;
-      v[2 * (wl + 1) + cg] = a0 - b0;
-    }
-#pragma unroll
-    for (int wl = 0; wl < 2; ++wl) {  // stride 64: w bit 1
-      float a0 = v[2 * wl + cg], b0 = v[2 * (wl + 2) + cg];
-      v[2 * wl + cg] = round_f16(a0 + b0);
-      v[2 * (wl + 2) + cg] = round_f16(a0 - b0);
-    }
-  }
+  for (int j = 0; j < 8; ++j) v[j] = round_f16(round_f16(v[j] * kHadScale) * sv[j]);
+  if (!live) return;
   const bool has_bias = p.bias != nullptr;
-  int cl[8];
-#pragma unroll
-  for (int f = 0; f < 8; ++f) {
-    cl[f] = 32 * (f >> 1) + 16 * (n >> 3) + 8 * (f & 1) + (n & 7);
-    v[f] = round_f16(round_f16(v[f] * kHadScale) * s_svh[cl[f]]);
-  }
   if (p.y_dtype == DT_F32) {
-    if (live) {
+    float4v o0, o1;
 #pragma unroll
-      for (int f = 0; f < 8; ++f)
-        ((float*)p.y)[(size_t)row * p.out + colb + cl[f]] = has_bias ? v[f] + s_bias[cl[f]] : v[f];
+    for (int j = 0; j < 4; ++j) {
+      o0[j] = has_bias ? v[j] + bv[j] : v[j];
+      o1[j] = has_bias ? v[j + 4] + bv[j + 4] : v[j + 4];
     }
+    float4v* yp = (float4v*)((float*)p.y + yoff);
+    yp[0] = o0;
+    yp[1] = o1;
     return;
   }
-  const bool odd = n & 1;
+  u32x4 o;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const float mine = odd ? v[2 * w + 1] : v[2 * w];
-    const float other = xor_lanes<1>(odd ? v[2 * w] : v[2 * w + 1]);
-    const int c = cl[2 * w + (odd ? 1 : 0)];  // column of `mine`
-    const int c_lo = odd ? c - 1 : c;
-    const float lo = odd ? other : mine, hi = odd ? mine : other;
-    const uint32_t bits = out16(lo, s_bias[c_lo], has_bias, p.y_dtype) |
-                          (out16(hi, s_bias[c_lo + 1], has_bias, p.y_dtype) << 16);
-    if (live) *(uint32_t*)((uint16_t*)p.y + (size_t)row * p.out + colb + c_lo) = bits;
-  }
+  for (int i = 0; i < 4; ++i)
+    o[i] = out16(v[2 * i], bv[2 * i], has_bias, p.y_dtype) |
+           (out16(v[2 * i + 1], bv[2 * i + 1], has_bias, p.y_dtype) << 16);
+  *(u32x4*)((uint16_t*)p.y + yoff) = o;
 }
 
 // Decode one step's 8 tiles of a producer (B[0] = previous lane's last word,
@@ -163,9 +172,17 @@ __device__ __forceinline__ void qmm_produce(const uint32_t (&B)[K + 1], u32x4* d
 
 template <int K, int CB, int MB>
 __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
-  __shared__ u32x4 bsh[2][4][4][64];  // [buffer][producer][fragment h*2+cg][lane]
+  // LDS: three stages of B fragments (16 KB each) and of A rows (64*MB rows x
+  // 128 bytes each); after the K loop the same bytes hold the tile's f16 rows.
+  constexpr int kBStage = 16384, kAStage = 64 * MB * 128;
+  constexpr int kLoop = 3 * (kBStage + kAStage), kY = 64 * MB * kYStride * 2;
+  constexpr int kLdsBytes = kLoop > kY ? kLoop : kY;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+  uint16_t* ys = (uint16_t*)lds;  // [64*MB][kYStride] after the loop
   __shared__ float s_svh[128], s_bias[128];
   __shared__ int s_last;
+  auto bstage = [&](int st) { return (u32x4*)(lds + st * kBStage); };  // [producer][frag][lane]
+  auto astage = [&](int st) { return lds + 3 * kBStage + st * kAStage; };
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int role = wave & 3;
@@ -188,17 +205,24 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
   const int qlast = nq - 1;
   const int g = lane >> 4, n = lane & 15;
   const int tile = mtile * p.col_blocks + cblk;
+  const int row_base = mtile * 64 * MB + role * 16 * MB;  // first row of consumer `role`
 
-  // The two roles run separate loops with the same number of barriers (one
-  // per step), so their register live ranges do not overlap.
+  // A rows sit in LDS as [row][8 chunks of 16 bytes] with chunk c of row r at
+  // slot c ^ (r & 7): the producers' row-wise writes and the consumers'
+  // fragment reads (16 rows x one chunk) are both free of bank conflicts.
+
+  // Step s of the K loop uses stage s % 3.  In iteration q the producers fill
+  // stage (q+2) % 3 with step q+2 while the consumers multiply step q and,
+  // before the barrier, read the first fragments of step q+1 (written in
+  // iteration q-1).  One barrier per iteration orders both.
   if (wave < 4) {
-    // the block's svh and bias go to LDS for the consumers' epilogue
+    // ---- producer `role`: B tiles of output tiles 2*role, 2*role+1 and the
+    // A rows of consumer `role` ----
     if (threadIdx.x < 128) {
       s_svh[threadIdx.x] = h2f(p.svh[cblk * 128 + threadIdx.x]);
       s_bias[threadIdx.x] = p.bias ? h2f(p.bias[cblk * 128 + threadIdx.x]) : 0.f;
     }
-    // ---- producer: trellis slices of steps q+1..q+4 in flight ----
-    constexpr int PD = 4;
+    constexpr int PD = 4;  // trellis slices in flight
     const int hsel = (lane >> 3) & 1, j = lane & 7;
     const size_t qstride = (size_t)4 * TN * 8 * K;
     const uint32_t* tp = p.trellis +
@@ -209,19 +233,52 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
 #pragma unroll
     for (int d = 0; d < PD; ++d)
       load_slice_prev<K>(tp + (size_t)min(d, qlast) * qstride, prev_off, sl[d]);
-    qmm_produce<K, CB>(sl[0], &bsh[0][role][0][0], lane);
+    // A: row 8i + (lane >> 3) of the consumer's 16*MB rows, chunk lane & 7
+    const int ar = lane >> 3, ac = lane & 7;
+    const uint16_t* ap[2 * MB];
+#pragma unroll
+    for (int i = 0; i < 2 * MB; ++i) {
+      const int row = row_base + 8 * i + ar;
+      ap[i] = p.xhat + (size_t)(row < p.M ? row : 0) * p.in + (size_t)qa * 64 + ac * 8;
+    }
+    // A rows of steps q+2 and q+3 in flight (register sets alternate by step)
+    u32x4 areg[2][2 * MB];
+    auto load_a = [&](u32x4(&dst)[2 * MB], int step) {
+#pragma unroll
+      for (int i = 0; i < 2 * MB; ++i)
+        dst[i] = *(const u32x4*)(ap[i] + (size_t)min(step, qlast) * 64);
+    };
+    auto store_a = [&](const u32x4(&src)[2 * MB], int st) {
+      uint8_t* base = astage(st) + role * (16 * MB * 128);
+#pragma unroll
+      for (int i = 0; i < 2 * MB; ++i) {
+        const int r = 8 * i + ar;
+        *(u32x4*)(base + r * 128 + ((ac ^ (r & 7)) << 4)) = src[i];
+      }
+    };
+    // steps 0 and 1
+    load_a(areg[0], 0);
+    load_a(areg[1], 1);
+    qmm_produce<K, CB>(sl[0], bstage(0) + role * 256, lane);
     load_slice_prev<K>(tp + (size_t)min(PD, qlast) * qstride, prev_off, sl[0]);
+    qmm_produce<K, CB>(sl[1], bstage(1) + role * 256, lane);
+    load_slice_prev<K>(tp + (size_t)min(PD + 1, qlast) * qstride, prev_off, sl[1]);
+    store_a(areg[0], 0);
+    load_a(areg[0], 2);
+    store_a(areg[1], 1);
+    load_a(areg[1], 3);
     __syncthreads();
-    // step q (phase P = q % 4): decode step q+1 from slot (q+1) % 4 into
-    // buffer (q+1) & 1, refill the slot with step q+5.  Unconditional: at
-    // q = nq-1 the decode lands in the buffer no consumer reads again, and the
-    // loads are clamped, so the load count per step is static and the waits
-    // before each decode stay partial.
+    // iteration q (slot (q+2) % 4 and A set q % 2 hold step q+2):
+    // unconditional, so the load count per iteration is static (past-the-end
+    // steps re-read the last one into a stage no consumer reads)
     auto iter = [&](int q, auto phase) {
       constexpr int P = decltype(phase)::value;
-      qmm_produce<K, CB>(sl[(P + 1) % PD], &bsh[(q + 1) & 1][role][0][0], lane);
-      load_slice_prev<K>(tp + (size_t)min(q + 1 + PD, qlast) * qstride, prev_off,
-                         sl[(P + 1) % PD]);
+      const int st = (q + 2) % 3;
+      qmm_produce<K, CB>(sl[(P + 2) % PD], bstage(st) + role * 256, lane);
+      load_slice_prev<K>(tp + (size_t)min(q + 2 + PD, qlast) * qstride, prev_off,
+                         sl[(P + 2) % PD]);
+      store_a(areg[P & 1], st);
+      load_a(areg[P & 1], q + 4);
       __syncthreads();
     };
     const int nq4 = nq & ~3;
@@ -234,136 +291,158 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
     if (nq4 < nq) iter(nq4, std::integral_constant<int, 0>{});
     if (nq4 + 1 < nq) iter(nq4 + 1, std::integral_constant<int, 1>{});
     if (nq4 + 2 < nq) iter(nq4 + 2, std::integral_constant<int, 2>{});
-    if (p.splits > 1) {  // the arrival count of the split-K exchange below
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        uint32_t old = __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (old == (uint32_t)(p.splits - 1));
-      }
-      __syncthreads();
-    }
-    return;
-  }
-
-  // ---- consumer: A fragments of steps q and q+1 in flight ----
-  // Rows past M read row 0 (in bounds) and produce outputs that are never stored.
-  const int row_base = mtile * 64 * MB + role * 16 * MB;
-  const uint16_t* arow[MB];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const int row = row_base + 16 * mb + n;
-    arow[mb] = p.xhat + (size_t)(row < p.M ? row : 0) * p.in + (size_t)qa * 64 + g * 16;
-  }
-  half8 abuf[2][MB][2];
-  auto load_a = [&](half8(&dst)[MB][2], int q) {
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const half8* src = (const half8*)(arow[mb] + min(q, qlast) * 64);
-      dst[mb][0] = src[0];
-      dst[mb][1] = src[1];
-    }
-  };
-  float4v acc[MB][8];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int f = 0; f < 8; ++f) acc[mb][f] = float4v{0.f, 0.f, 0.f, 0.f};
-  load_a(abuf[0], 0);
-  load_a(abuf[1], 1);
-  __syncthreads();
-  // step q: multiply with A buffer q % 2, then refill it with step q+2.  The
-  // B fragments of producer w2+1 are read from LDS while those of w2 feed the
-  // MFMAs.
-  auto iter = [&](int q, auto phase) {
-    constexpr int P = decltype(phase)::value;
-    half8(&a)[MB][2] = abuf[P & 1];
-    const u32x4* bb = &bsh[q & 1][0][0][lane];
-    half8 bc[4], bn[4];
-#pragma unroll
-    for (int f = 0; f < 4; ++f) bc[f] = __builtin_bit_cast(half8, bb[f * 64]);
-#pragma unroll
-    for (int w2 = 0; w2 < 4; ++w2) {
-      if (w2 < 3) {
-#pragma unroll
-        for (int f = 0; f < 4; ++f) bn[f] = __builtin_bit_cast(half8, bb[((w2 + 1) * 4 + f) * 64]);
-      }
-      // keep the reads of the next group ahead of this group's MFMAs
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int cg = 0; cg < 2; ++cg)
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb)
-            acc[mb][w2 * 2 + cg] = mfma16(a[mb][h], bc[h * 2 + cg], acc[mb][w2 * 2 + cg]);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int f = 0; f < 4; ++f) bc[f] = bn[f];
-    }
-    load_a(a, q + 2);
-    __syncthreads();
-  };
-  const int nq2 = nq & ~1;
-  for (int q = 0; q < nq2; q += 2) {
-    iter(q, std::integral_constant<int, 0>{});
-    iter(q + 1, std::integral_constant<int, 1>{});
-  }
-  if (nq2 < nq) iter(nq2, std::integral_constant<int, 0>{});
-
-  const int colb = cblk * 128;
-  if (p.splits == 1) {
+  } else {
+    // ---- consumer `role`: 16*MB rows x 128 columns ----
+    float4v acc[MB][8];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = row_base + 16 * mb + 4 * g + r;
-        float v[8];
+      for (int f = 0; f < 8; ++f) acc[mb][f] = float4v{0.f, 0.f, 0.f, 0.f};
+    // fragment (mb, h): row 16mb + n of this consumer, chunk 2g + h
+    int aoff[MB][2];
 #pragma unroll
-        for (int f = 0; f < 8; ++f) v[f] = acc[mb][f][r];
-        qmm_finish_row(v, lane, colb, row, row < p.M, p, s_svh, s_bias);
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = role * 16 * MB + 16 * mb + n;
+        aoff[mb][h] = r * 128 + (((2 * g + h) ^ (r & 7)) << 4);
       }
-    return;
+    half8 a[2][MB][2], b[2][4];
+    auto read_a = [&](half8(&dst)[MB][2], int st) {
+      const uint8_t* base = astage(st);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) dst[mb][h] = *(const half8*)(base + aoff[mb][h]);
+    };
+    auto read_b = [&](half8(&dst)[4], int st, int w2) {
+      const u32x4* bb = bstage(st) + w2 * 256 + lane;
+#pragma unroll
+      for (int f = 0; f < 4; ++f) dst[f] = __builtin_bit_cast(half8, bb[f * 64]);
+    };
+    __syncthreads();
+    read_a(a[0], 0);
+    read_b(b[0], 0, 0);
+    // iteration q: A of step q in a[q&1], B groups alternate between b[0]
+    // and b[1]; the last group prefetches step q+1 (stage (q+1) % 3)
+    auto iter = [&](int q, auto phase) {
+      constexpr int P = decltype(phase)::value;
+      const int st = q % 3, st1 = (q + 1) % 3;
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) {
+        if (w2 < 3) {
+          read_b(b[(w2 + 1) & 1], st, w2 + 1);
+        } else {
+          read_a(a[(P + 1) & 1], st1);
+          read_b(b[0], st1, 0);
+        }
+        // keep the reads of the next group ahead of this group's MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int cg = 0; cg < 2; ++cg)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+              acc[mb][w2 * 2 + cg] =
+                  mfma16(a[P & 1][mb][h], b[w2 & 1][h * 2 + cg], acc[mb][w2 * 2 + cg]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      __syncthreads();
+    };
+    const int nq2 = nq & ~1;
+    for (int q = 0; q < nq2; q += 2) {
+      iter(q, std::integral_constant<int, 0>{});
+      iter(q + 1, std::integral_constant<int, 1>{});
+    }
+    if (nq2 < nq) iter(nq2, std::integral_constant<int, 0>{});
+    // the stages are free after the loop's last barrier
+    const int colb = cblk * 128;
+    if (p.splits == 1) {
+      // static_for: the accumulator index must stay a compile-time constant
+      static_for<MB>([&](auto mb_) {
+        constexpr int mb = decltype(mb_)::value;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v[8];
+#pragma unroll
+          for (int f = 0; f < 8; ++f) v[f] = round_f16(acc[mb][f][r]);
+          qmm_stage_row(v, lane, ys + (role * 16 * MB + 16 * mb + 4 * g + r) * kYStride);
+        }
+      });
+    } else {
+      // split-K: f32 partials out, through agent-scope relaxed atomics
+      float* part = p.partials + (size_t)split * p.M * p.out;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = row_base + 16 * mb + 4 * g + r;
+          if (row < p.M) {
+#pragma unroll
+            for (int f = 0; f < 8; ++f) {
+              const int c = colb + 32 * (f >> 1) + 16 * (n >> 3) + 8 * (f & 1) + (n & 7);
+              store_coherent(part + (size_t)row * p.out + c, acc[mb][f][r]);
+            }
+          }
+        }
+    }
   }
 
-  // split-K: store f32 partials; the producers' thread 0 counts arrivals
-  // between the two barriers; the last arriver finishes the tile
-  float* part = p.partials + (size_t)split * p.M * p.out;
+  // ---- split-K exchange: every wave takes part in the barriers ----
+  if (p.splits > 1) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t old = __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+      s_last = (old == (uint32_t)(p.splits - 1));
+    }
+    __syncthreads();
+    if (!s_last) return;  // uniform across the workgroup
+    if (threadIdx.x == 0)
+      __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the tile's rows: sum of every split's partial in split order (this
+    // workgroup's own included, read back from memory), f16 into LDS; each
+    // wave takes 8*MB rows, each lane 4 consecutive columns... as 2 pairs
+    const int colb = cblk * 128;
+    for (int i = 0; i < MB; ++i) {
+      const int rl = wave * 8 * MB + 8 * i + (lane >> 3);  // tile row
+      const int row = mtile * 64 * MB + rl;
+      const int lrow = row < p.M ? row : p.M - 1;  // in-bounds loads for padding rows
+      const int c0 = (lane & 7) * 16;
+      uint32_t* yw = (uint32_t*)(ys + rl * kYStride + c0);
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = row_base + 16 * mb + 4 * g + r;
-      if (row < p.M) {
-#pragma unroll
-        for (int f = 0; f < 8; ++f) {
-          const int c = colb + 32 * (f >> 1) + 16 * (n >> 3) + 8 * (f & 1) + (n & 7);
-          store_coherent(part + (size_t)row * p.out + c, acc[mb][f][r]);
+      for (int j = 0; j < 16; j += 2) {
+        float s0 = 0.f, s1 = 0.f;
+        for (int s = 0; s < p.splits; ++s) {
+          const float* ps = p.partials + ((size_t)s * p.M + lrow) * p.out + colb + c0 + j;
+          s0 += load_coherent(ps);
+          s1 += load_coherent(ps + 1);
         }
+        yw[j >> 1] = (uint32_t)f2h(s0) | ((uint32_t)f2h(s1) << 16);
       }
     }
-  __builtin_amdgcn_s_waitcnt(0);
+  }
   __syncthreads();
-  __syncthreads();
-  if (!s_last) return;  // uniform
-  if (threadIdx.x == 256)
-    __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // every split's partial, this workgroup's own included, is read back from
-  // memory and added in split order
-#pragma unroll 1
-  for (int i = 0; i < 4 * MB; ++i) {
-    const int row = row_base + 16 * (i >> 2) + 4 * g + (i & 3);
-    const int lrow = row < p.M ? row : p.M - 1;  // in-bounds loads for padding rows
-    float v[8];
+
+  // ---- epilogue: all 8 waves finish 8*MB rows each, 4 rows per pass ----
+  {
+    const int colb = cblk * 128;
+    const int chunk = lane & 15;
+    float sv[8], bv[8];
 #pragma unroll
-    for (int f = 0; f < 8; ++f) {
-      const int c = colb + 32 * (f >> 1) + 16 * (n >> 3) + 8 * (f & 1) + (n & 7);
-      float sum = 0.f;
-      for (int s = 0; s < p.splits; ++s)
-        sum += load_coherent(p.partials + ((size_t)s * p.M + lrow) * p.out + c);
-      v[f] = sum;
+    for (int j = 0; j < 8; ++j) {
+      sv[j] = s_svh[8 * chunk + j];
+      bv[j] = s_bias[8 * chunk + j];
     }
-    qmm_finish_row(v, lane, colb, row, row < p.M, p, s_svh, s_bias);
+#pragma unroll
+    for (int i = 0; i < 2 * MB; ++i) {
+      const int rl = wave * 8 * MB + 4 * i + (lane >> 4);
+      const int row = mtile * 64 * MB + rl;
+      const u32x4 raw = *(const u32x4*)(ys + rl * kYStride + 8 * chunk);
+      qmm_finish_chunk(raw, sv, bv, lane, row < p.M, p, (size_t)row * p.out + colb + 8 * chunk);
+    }
   }
 }
 

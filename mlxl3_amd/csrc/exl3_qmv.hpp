@@ -202,17 +202,19 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   // it finishes and leaves them to run alone at single-wave efficiency.
   __builtin_amdgcn_s_setprio(3);
 
-  // The first prologue job's activation loads go out first, then the weight
-  // stream's first set, so the Hadamard below waits only for the (shared,
-  // cache-resident) activations while the weight loads are in flight.
+  // The activation loads of the wave's first kPrologueEarly prologue jobs go
+  // out first, then the weight stream's first set, so the Hadamards below wait
+  // only for the (shared, cache-resident) activations, not behind the weights.
+  constexpr int kPrologueEarly = 2;
   const int nb = b1 - b0;
   const int njobs = M * nb;
-  PrologueIn first;
-  {
-    const int job = min(wave, njobs - 1);  // waves without a job load a valid one
+  PrologueIn first[kPrologueEarly];
+#pragma unroll
+  for (int t = 0; t < kPrologueEarly; ++t) {
+    const int job = min(wave + t * 4 * KW, njobs - 1);  // clamped: always a valid job
     const int m = job / nb, b = job - m * nb;
-    first = prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128, p.suh,
-                          row0 + b * 128, lane);
+    first[t] = prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128, p.suh,
+                             row0 + b * 128, lane);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -232,11 +234,21 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   __builtin_amdgcn_sched_barrier(0);
 
   // prologue into LDS
-  for (int job = wave; job < njobs; job += 4 * KW) {
+#pragma unroll
+  for (int t = 0; t < kPrologueEarly; ++t) {
+    const int job = wave + t * 4 * KW;
+    if (job < njobs) {
+      const int m = job / nb, b = job - m * nb;
+      float v0, v1;
+      prologue_finish(first[t], p.x_dtype, lane, v0, v1);
+      xs[m * nrows + b * 128 + lane] = (_Float16)v0;
+      xs[m * nrows + b * 128 + lane + 64] = (_Float16)v1;
+    }
+  }
+  for (int job = wave + kPrologueEarly * 4 * KW; job < njobs; job += 4 * KW) {
     const int m = job / nb, b = job - m * nb;
-    PrologueIn in = job == wave ? first
-                                : prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128,
-                                                p.suh, row0 + b * 128, lane);
+    const PrologueIn in = prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128,
+                                        p.suh, row0 + b * 128, lane);
     float v0, v1;
     prologue_finish(in, p.x_dtype, lane, v0, v1);
     xs[m * nrows + b * 128 + lane] = (_Float16)v0;

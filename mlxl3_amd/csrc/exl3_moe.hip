@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <new>
 
 #include "../../include/exl3_hip.h"
@@ -13,9 +14,11 @@
 #include "exl3_moe.hpp"
 
 namespace exl3 {
-#define EXL3_MOE_INST(K, CB)                                                  \
-  template __global__ void moe_gateup_kernel<K, CB>(MoeQmmParams);           \
-  template __global__ void moe_down_kernel<K, CB>(MoeQmmParams);
+#define EXL3_MOE_INST(K, CB)                                          \
+  template __global__ void moe_mm_kernel<K, CB, 2, 1>(MoeMmParams);  \
+  template __global__ void moe_mm_kernel<K, CB, 1, 1>(MoeMmParams);  \
+  template __global__ void moe_mm_kernel<K, CB, 2, 4>(MoeMmParams);  \
+  template __global__ void moe_mm_kernel<K, CB, 1, 4>(MoeMmParams);
 // K = 7 is not a SwitchGLU width (switch_glu_layout rejects it).
 EXL3_INST_CB(EXL3_MOE_INST, 1)
 EXL3_INST_CB(EXL3_MOE_INST, 2)
@@ -30,18 +33,22 @@ using namespace exl3;
 
 #ifndef __HIP_DEVICE_COMPILE__
 
-typedef void (*MoeKernel)(MoeQmmParams);
-#define EXL3_MOE_ROW(F, K) {F<K, 0>, F<K, 1>, F<K, 2>}
-#define EXL3_MOE_TABLE(F)                                                                 \
-  {EXL3_MOE_ROW(F, 1), EXL3_MOE_ROW(F, 2), EXL3_MOE_ROW(F, 3), EXL3_MOE_ROW(F, 4),        \
-   EXL3_MOE_ROW(F, 5), EXL3_MOE_ROW(F, 6), {nullptr, nullptr, nullptr}, EXL3_MOE_ROW(F, 8)}
-static const MoeKernel kGateUp[8][3] = EXL3_MOE_TABLE(moe_gateup_kernel);
-static const MoeKernel kDown[8][3] = EXL3_MOE_TABLE(moe_down_kernel);
+typedef void (*MoeKernel)(MoeMmParams);
+#define EXL3_MOE_ROW(N, MB, K) \
+  {moe_mm_kernel<K, 0, N, MB>, moe_mm_kernel<K, 1, N, MB>, moe_mm_kernel<K, 2, N, MB>}
+#define EXL3_MOE_TABLE(N, MB)                                                             \
+  {EXL3_MOE_ROW(N, MB, 1), EXL3_MOE_ROW(N, MB, 2), EXL3_MOE_ROW(N, MB, 3),               \
+   EXL3_MOE_ROW(N, MB, 4), EXL3_MOE_ROW(N, MB, 5), EXL3_MOE_ROW(N, MB, 6),               \
+   {nullptr, nullptr, nullptr}, EXL3_MOE_ROW(N, MB, 8)}
+// [MB == 4][K-1][codebook]
+static const MoeKernel kGateUp[2][8][3] = {EXL3_MOE_TABLE(2, 1), EXL3_MOE_TABLE(2, 4)};
+static const MoeKernel kDown[2][8][3] = {EXL3_MOE_TABLE(1, 1), EXL3_MOE_TABLE(1, 4)};
 
 struct exl3_moe {
   const uint16_t *gu_trellis, *gu_suh, *gu_svh;
   const uint16_t *down_trellis, *down_suh, *down_svh;
   int in, hidden, experts, top_k, k, cb;
+  int force_splits;  // EXL3_MOE_SPLITS at create (0: by slot count)
 };
 
 // The largest bank the plan kernel's LDS histogram holds (3 ints per expert).
@@ -50,18 +57,38 @@ static constexpr size_t kMoeAlign = 256;
 static size_t moe_align(size_t v) { return (v + kMoeAlign - 1) / kMoeAlign * kMoeAlign; }
 
 namespace {
+// K-splits of an expert QMM.  The block count is known only on the device;
+// min(slots, E) + slots/16 bounds it, and the split count aims at about 512
+// workgroups with at least two 64-row K-steps per split.
+int moe_splits(const exl3_moe* h, int64_t slots, int block_rows, int k_in, int col_blocks) {
+  if (h->force_splits > 0) return std::min(h->force_splits, k_in / 64);
+  const int64_t blocks = std::min<int64_t>(slots, h->experts) + slots / block_rows;
+  const int64_t base = std::max<int64_t>(1, blocks * col_blocks);
+  int s = (int)std::min<int64_t>((512 + base - 1) / base, 16);
+  return std::max(1, std::min(s, k_in / 128));
+}
+
 // Workspace layout for `slots` = rows * top_k routed slots.
 struct MoeLayout {
-  size_t counts, rank, sorted, expert_count, table, xgu, xd, z, total;
-  int max_blocks;
+  size_t counts, rank, sorted, expert_count, table, counters, xgu, xd, z, partials, total;
+  int max_blocks, ncounters, splits_gu, splits_down, block_rows;
 };
 
 bool moe_layout(const exl3_moe* h, int64_t rows, MoeLayout& L) {
   if (rows < 1) return false;
   const int64_t slots = rows * h->top_k;
   if (slots > (int64_t)1 << 24) return false;
-  // each expert's last block may be partial: sum ceil(c_e/64) <= slots/64 + E
-  L.max_blocks = (int)(slots / kMoeBlockRows + h->experts + 1);
+  // 64-row blocks once the average expert sees 8 or more rows
+  L.block_rows = slots >= 8 * (int64_t)h->experts ? kMoeMaxBlockRows : 16;
+  if (const char* env = getenv("EXL3_MOE_BLOCK_ROWS")) {
+    const int v = atoi(env);
+    if (v == 16 || v == 64) L.block_rows = v;
+  }
+  // each expert's last block may be partial: sum ceil(c_e/b) <= slots/b + E
+  L.max_blocks = (int)(slots / L.block_rows + h->experts + 1);
+  L.ncounters = L.max_blocks * std::max(h->hidden, h->in) / 128;
+  L.splits_gu = moe_splits(h, slots, L.block_rows, h->in, h->hidden / 128);
+  L.splits_down = moe_splits(h, slots, L.block_rows, h->hidden, h->in / 128);
   size_t off = 0;
   auto take = [&](size_t bytes) {
     size_t at = off;
@@ -73,9 +100,13 @@ bool moe_layout(const exl3_moe* h, int64_t rows, MoeLayout& L) {
   L.sorted = take((size_t)slots * sizeof(int));
   L.expert_count = take((size_t)h->experts * sizeof(int));
   L.table = take((size_t)L.max_blocks * sizeof(int4));
+  L.counters = take((size_t)L.ncounters * sizeof(uint32_t));
   L.xgu = take((size_t)2 * slots * h->in * sizeof(uint16_t));
   L.xd = take((size_t)slots * h->hidden * sizeof(uint16_t));
   L.z = take((size_t)slots * h->in * sizeof(uint16_t));
+  const size_t pgu = L.splits_gu > 1 ? (size_t)L.splits_gu * 2 * slots * h->hidden : 0;
+  const size_t pdn = L.splits_down > 1 ? (size_t)L.splits_down * slots * h->in : 0;
+  L.partials = take(std::max(pgu, pdn) * sizeof(float));
   L.total = off;
   return true;
 }
@@ -102,7 +133,8 @@ int exl3_moe_create(const uint16_t* gu_trellis, const uint16_t* gu_suh, const ui
   exl3_moe* h = new (std::nothrow) exl3_moe;
   if (!h) return fail(EXL3_ENOMEM, "out of host memory");
   *h = exl3_moe{gu_trellis, gu_suh, gu_svh, down_trellis, down_suh, down_svh,
-                in,         hidden, experts, top_k,       k,        cb};
+                in,         hidden, experts, top_k,       k,        cb,       0};
+  if (const char* env = getenv("EXL3_MOE_SPLITS")) h->force_splits = std::max(0, atoi(env));
   *out_handle = h;
   return EXL3_OK;
 }
@@ -126,10 +158,12 @@ int exl3_moe_forward(const exl3_moe* h, const uint16_t* x, int64_t rows,
   if (!workspace || workspace_bytes < L.total)
     return fail(EXL3_EINVAL, "workspace too small: need %zu bytes, got %zu", L.total,
                 workspace_bytes);
-  const MoeKernel gateup = kGateUp[h->k - 1][h->cb], down = kDown[h->k - 1][h->cb];
+  const int mbi = L.block_rows == kMoeMaxBlockRows ? 1 : 0;
+  const MoeKernel gateup = kGateUp[mbi][h->k - 1][h->cb], down = kDown[mbi][h->k - 1][h->cb];
   if (!gateup || !down) return fail(EXL3_EUNSUPPORTED, "no SwitchGLU kernel for K=%d", h->k);
-  const int64_t wide = (int64_t)L.max_blocks * (std::max(h->in, h->hidden) / 128);
-  if (wide * 256 >= ((int64_t)1 << 31))
+  const int64_t wide = (int64_t)L.max_blocks * (std::max(h->in, h->hidden) / 128) *
+                       std::max(L.splits_gu, L.splits_down);
+  if (wide * 512 >= ((int64_t)1 << 31))
     return fail(EXL3_EUNSUPPORTED, "SwitchGLU launch of %lld rows is too large", (long long)rows);
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
@@ -144,33 +178,37 @@ int exl3_moe_forward(const exl3_moe* h, const uint16_t* x, int64_t rows,
   pp.table = (int4*)(ws + L.table);
   pp.counts = (int*)(ws + L.counts);
   pp.expert_count = (int*)(ws + L.expert_count);
+  pp.counters = (uint32_t*)(ws + L.counters);
+  pp.ncounters = L.ncounters;
+  pp.block_rows = L.block_rows;
   moe_plan_kernel<<<1, 1024, (3 * h->experts + 1) * sizeof(int), s>>>(pp);
   if (int rc = check_launch("moe plan")) return rc;
 
   uint16_t* xgu = (uint16_t*)(ws + L.xgu);
-  moe_gather_kernel<<<dim3(slots, h->in / 128, 2), 64, 0, s>>>(
-      x, h->in, h->top_k, selected, pp.sorted_slot, pp.counts + 1, h->gu_suh, xgu);
+  moe_gather_kernel<<<(unsigned)((2 * (int64_t)slots + 3) / 4), 256, 0, s>>>(
+      x, h->in, h->top_k, selected, pp.sorted_slot, pp.counts + 1, slots, h->gu_suh, xgu);
   if (int rc = check_launch("moe gather")) return rc;
 
-  MoeQmmParams q{};
+  MoeMmParams q{};
   q.experts = h->experts;
   q.table = pp.table;
   q.counts = pp.counts;
   q.sorted_slot = pp.sorted_slot;
-  q.max_blocks = L.max_blocks;
   q.slots_pad = slots;
-  q.selected = selected;
+  q.partials = (float*)(ws + L.partials);
+  q.counters = pp.counters;
   // gate/up: input width `in`, per-expert output `hidden`
   q.trellis = (const uint32_t*)h->gu_trellis;
   q.tn_total = 2 * h->experts * h->hidden / 16;
   q.k_in = h->in;
   q.width = h->hidden;
   q.col_blocks = h->hidden / 128;
-  q.xgu = xgu;
+  q.splits = L.splits_gu;
+  q.xa = xgu;
   q.gu_svh = h->gu_svh;
   q.down_suh = h->down_suh;
   q.xd = (uint16_t*)(ws + L.xd);
-  gateup<<<L.max_blocks * q.col_blocks, 256, 0, s>>>(q);
+  gateup<<<L.max_blocks * q.col_blocks * q.splits, 512, 0, s>>>(q);
   if (int rc = check_launch("moe gate/up")) return rc;
 
   // down: input width `hidden`, per-expert output `in`
@@ -179,11 +217,12 @@ int exl3_moe_forward(const exl3_moe* h, const uint16_t* x, int64_t rows,
   q.k_in = h->hidden;
   q.width = h->in;
   q.col_blocks = h->in / 128;
-  q.xin = q.xd;
+  q.splits = L.splits_down;
+  q.xa = q.xd;
   q.down_svh = h->down_svh;
   q.scores = scores;
   q.z = (uint16_t*)(ws + L.z);
-  down<<<L.max_blocks * q.col_blocks, 256, 0, s>>>(q);
+  down<<<L.max_blocks * q.col_blocks * q.splits, 256, 0, s>>>(q);
   if (int rc = check_launch("moe down")) return rc;
 
   moe_reduce_kernel<<<dim3((unsigned)rows, (h->in + 255) / 256), 256, 0, s>>>(

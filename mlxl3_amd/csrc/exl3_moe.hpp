@@ -2,21 +2,27 @@
 // (native/src/moe.rs:611-1085) -- route plan, routed inputs, expert QMMs,
 // SwiGLU glue, down projection, weighted top-k reduction -- re-designed for
 // gfx950 as five launches:
-//   1. plan:    one workgroup counting-sorts the rows*top_k slots by expert and
-//               cuts each expert's run into <= 64-row blocks (block table);
+//   1. plan:    one workgroup counting-sorts the rows*top_k slots by expert,
+//               cuts each expert's run into blocks of <= 16 or 64 rows (block
+//               table) and clears the tile arrival counters of the two expert
+//               QMMs;
 //   2. gather:  f16(x[token] * gu_suh[e][p]) -> staged Hadamard-128 for the gate
 //               (p = 0) and up (p = 1) inputs, in expert-sorted order;
-//   3. gate/up: per (block, 128 hidden columns) a workgroup decodes the expert's
-//               gate AND up tiles of those columns in registers (waves own column
-//               pairs, as in the QMV) and multiplies them with the block's rows;
-//               the epilogue is the whole of glu_down_input (moe.rs:435-563): f16,
+//   3. gate/up: per (block, 128 hidden columns, K-range) a workgroup of 8 waves
+//               decodes the expert's gate (waves 0-3) and up (waves 4-7) tiles of
+//               those columns in registers -- each wave owns a column pair, as in
+//               the QMV -- and multiplies them with the block's rows; the
+//               epilogue is the whole of glu_down_input (moe.rs:435-563): f16,
 //               f32 Hadamard, *scale*svh, SiLU(g)*u, *down_suh, f32 Hadamard,
 //               *scale -> the down projection's xhat;
-//   4. down:    same kernel shape over the down bank; the epilogue is
+//   4. down:    the same kernel with 4 waves over the down bank; the epilogue is
 //               finish_and_reduce's per-slot part (moe.rs:586-609): f16, staged
 //               Hadamard, *svh, *score, stored per slot;
 //   5. reduce:  y[row] = f16(sum over top_k in slot order, f32).
-// Each row's arithmetic is independent of the other rows of its block, so the
+// Small inputs (decode: a handful of slots) split K over several workgroups
+// whose f32 partials meet in the last arriving one (agent-scope relaxed
+// atomics, as in the QMV), which adds them in split order.  Each row's
+// arithmetic is independent of the other rows of its block, so the
 // (atomics-ordered) placement of slots inside an expert's run cannot change any
 // result.
 #pragma once
@@ -26,7 +32,10 @@
 
 namespace exl3 {
 
-constexpr int kMoeBlockRows = 64;  // rows per block-table entry (moe.rs:80-83)
+// Rows per block-table entry: up to 4 MFMA row blocks; the plan cuts 16-row
+// blocks for small inputs (more workgroups) and 64-row blocks otherwise (each
+// decoded weight serves more rows), as moe.rs:80-83 cuts 64.
+constexpr int kMoeMaxBlockRows = 64;
 
 struct MoePlanParams {
   const uint32_t* selected;  // [slots] expert ids (rows * top_k)
@@ -36,6 +45,9 @@ struct MoePlanParams {
   int4* table;               // [max_blocks] (expert, first sorted position, rows, 0)
   int* counts;               // [2]: block-table entries, routed slots
   int* expert_count;         // [experts] (rows routed to each expert)
+  uint32_t* counters;        // [ncounters] tile arrival counters, cleared here
+  int ncounters;
+  int block_rows;            // 16 or 64
 };
 
 // One workgroup of 1024 threads.  Slots with an expert id >= experts are left
@@ -46,6 +58,7 @@ __global__ __launch_bounds__(1024) void moe_plan_kernel(MoePlanParams p) {
   int* off = lds + p.experts;
   int* boff = lds + 2 * p.experts;
   const int tid = threadIdx.x;
+  for (int i = tid; i < p.ncounters; i += 1024) p.counters[i] = 0u;
   for (int e = tid; e < p.experts; e += 1024) cnt[e] = 0;
   __syncthreads();
   for (int s = tid; s < p.slots; s += 1024) {
@@ -53,17 +66,39 @@ __global__ __launch_bounds__(1024) void moe_plan_kernel(MoePlanParams p) {
     p.rank[s] = e < (uint32_t)p.experts ? atomicAdd(&cnt[e], 1) : -1;
   }
   __syncthreads();
-  if (tid == 0) {
-    int acc = 0, bacc = 0;
-    for (int e = 0; e < p.experts; ++e) {
-      off[e] = acc;
-      boff[e] = bacc;
-      acc += cnt[e];
-      bacc += (cnt[e] + kMoeBlockRows - 1) / kMoeBlockRows;
-    }
-    boff[p.experts] = bacc;
-    p.counts[0] = bacc;
-    p.counts[1] = acc;
+  // exclusive scans of the counts and block counts: each thread sums a run of
+  // experts, the 1024 run totals are scanned (waves, then wave totals), and
+  // each thread writes its run's offsets
+  __shared__ int wsum[2][16];
+  const int per = (p.experts + 1023) / 1024;
+  const int e0 = min(tid * per, p.experts), e1 = min(e0 + per, p.experts);
+  int lc = 0, lb = 0;
+  for (int e = e0; e < e1; ++e) {
+    lc += cnt[e];
+    lb += (cnt[e] + p.block_rows - 1) / p.block_rows;
+  }
+  int ic = lc, ib = lb;  // inclusive scan inside the wave
+  const int lane = tid & 63, wv = tid >> 6;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int tc = __shfl_up(ic, d, 64), tb = __shfl_up(ib, d, 64);
+    if (lane >= d) ic += tc, ib += tb;
+  }
+  if (lane == 63) wsum[0][wv] = ic, wsum[1][wv] = ib;
+  __syncthreads();
+  int bc = 0, bb = 0;
+  for (int w = 0; w < wv; ++w) bc += wsum[0][w], bb += wsum[1][w];
+  int rc = bc + ic - lc, rb = bb + ib - lb;  // exclusive prefix of this run
+  for (int e = e0; e < e1; ++e) {
+    off[e] = rc;
+    boff[e] = rb;
+    rc += cnt[e];
+    rb += (cnt[e] + p.block_rows - 1) / p.block_rows;
+  }
+  if (tid == 1023) {
+    boff[p.experts] = rb;
+    p.counts[0] = rb;
+    p.counts[1] = rc;
   }
   __syncthreads();
   for (int s = tid; s < p.slots; s += 1024) {
@@ -73,36 +108,34 @@ __global__ __launch_bounds__(1024) void moe_plan_kernel(MoePlanParams p) {
   for (int e = tid; e < p.experts; e += 1024) {
     p.expert_count[e] = cnt[e];
     for (int b = boff[e]; b < boff[e + 1]; ++b) {
-      const int first = off[e] + (b - boff[e]) * kMoeBlockRows;
-      p.table[b] = make_int4(e, first, min(kMoeBlockRows, off[e] + cnt[e] - first), 0);
+      const int first = off[e] + (b - boff[e]) * p.block_rows;
+      p.table[b] = make_int4(e, first, min(p.block_rows, off[e] + cnt[e] - first), 0);
     }
   }
 }
 
 // Gate/up inputs in sorted order: xgu[proj][pos][in] with proj 0 = gate,
-// 1 = up (routed_inputs, moe.rs:184-250).  grid (slots, in/128, 2), one wave
-// per (block, position, projection); positions past the routed count idle.
-__global__ __launch_bounds__(64) void moe_gather_kernel(const uint16_t* __restrict__ x, int in,
-                                                        int top_k, const uint32_t* selected,
-                                                        const int* sorted_slot,
-                                                        const int* routed,
-                                                        const uint16_t* __restrict__ gu_suh,
-                                                        uint16_t* __restrict__ xgu) {
-  const int lane = threadIdx.x, pos = blockIdx.x, b = blockIdx.y, proj = blockIdx.z;
-  if (pos >= *routed) return;
+// 1 = up (routed_inputs, moe.rs:184-250).  One wave per (position,
+// projection): the slot and expert lookups once, then the row's blocks with
+// eight blocks' loads in flight.  grid ceil(2 * slots / 4), 256 threads;
+// positions past the routed count idle.
+__global__ __launch_bounds__(256) void moe_gather_kernel(const uint16_t* __restrict__ x, int in,
+                                                         int top_k, const uint32_t* selected,
+                                                         const int* sorted_slot,
+                                                         const int* routed, int slots_pad,
+                                                         const uint16_t* __restrict__ gu_suh,
+                                                         uint16_t* __restrict__ xgu) {
+  const int job = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int pos = job >> 1, proj = job & 1;
+  if (pos >= *routed) return;  // uniform per wave
   const int slot = sorted_slot[pos];
-  const int token = slot / top_k;
-  const uint32_t e = selected[slot];
-  const uint16_t* suh = gu_suh + ((size_t)e * 2 + proj) * in;
-  float v0, v1;
-  prepare_row128(x, DT_F16, (size_t)token * in + b * 128, suh, b * 128, lane, v0, v1);
-  uint16_t* dst = xgu + ((size_t)proj * gridDim.x + pos) * in + b * 128;
-  dst[lane] = f2h(v0);
-  dst[lane + 64] = f2h(v1);
+  const uint16_t* suh = gu_suh + ((size_t)selected[slot] * 2 + proj) * in;
+  pair_prologue_row(x, DT_F16, (size_t)(slot / top_k) * in, suh, 0, in >> 7, threadIdx.x & 63,
+                    xgu + ((size_t)proj * slots_pad + pos) * in);
 }
 
-struct MoeQmmParams {
-  const uint32_t* trellis;  // bank, [K_in/16][tn_total][8K] u32
+struct MoeMmParams {
+  const uint32_t* trellis;  // bank, [k_in/16][tn_total][8K] u32
   int tn_total;             // tile columns of the bank
   int k_in;                 // input width of the projection (rows of the trellis)
   int width;                // output width of one expert's projection
@@ -110,218 +143,258 @@ struct MoeQmmParams {
   const int4* table;
   const int* counts;        // [0] = block-table entries
   const int* sorted_slot;
-  int max_blocks;
   int col_blocks;           // width / 128
-  int slots_pad;            // position stride of xgu
-  // gate/up
-  const uint16_t* xgu;      // [2][slots_pad][k_in]
+  int splits;               // K-ranges per (block, column block)
+  int slots_pad;            // position stride of xa / partials
+  const uint16_t* xa;       // A rows [nproj][slots_pad][k_in] (f16, rotated)
+  float* partials;          // [splits][nproj][slots_pad][width] (splits > 1)
+  uint32_t* counters;       // [blocks][col_blocks], cleared by the plan
+  // gate/up epilogue
   const uint16_t* gu_svh;   // [E][2][width]
   const uint16_t* down_suh; // [E][width]
   uint16_t* xd;             // [slots_pad][width]
-  // down
-  const uint16_t* xin;      // [slots_pad][k_in]
+  // down epilogue
   const uint16_t* down_svh; // [E][width]
   const uint16_t* scores;   // [slots]
   uint16_t* z;              // [slots][width]
-  const uint32_t* selected;
 };
 
-// One weight step of a grouped QMM: decode the wave's 8 tiles (2 output tiles x
-// 4 tile rows) of `B` and run MBLK 16-row MFMA blocks against A fragments read
-// from `arow` rows (row stride `k_in`), rows >= nrows contributing zero.
-template <int K, int CB, int MBLK>
-__device__ __forceinline__ void moe_step(const uint32_t (&B)[K + 1],
-                                         const uint16_t* const (&arow)[MBLK],
-                                         const bool (&aval)[MBLK], int mblocks, int q,
-                                         float4v (&acc0)[MBLK], float4v (&acc1)[MBLK]) {
-  uint32_t src[32];
-  extract_states<K>(B, src);
-  const half8 b00 = decode_fragment<CB, K, 0, 0>(src);
-  const half8 b01 = decode_fragment<CB, K, 0, 1>(src);
-  const half8 b10 = decode_fragment<CB, K, 1, 0>(src);
-  const half8 b11 = decode_fragment<CB, K, 1, 1>(src);
-  const half8 zero8 = {};
-#pragma unroll
-  for (int mb = 0; mb < MBLK; ++mb) {
-    if (mb < mblocks) {
-      // rows past the block's end read a valid row and are zeroed afterwards
-      const half8* src8 = (const half8*)(arow[mb] + q * 64);
-      half8 a0 = src8[0], a1 = src8[1];
-      a0 = aval[mb] ? a0 : zero8;
-      a1 = aval[mb] ? a1 : zero8;
-      acc0[mb] = mfma16(a0, b00, acc0[mb]);
-      acc1[mb] = mfma16(a0, b01, acc1[mb]);
-      acc0[mb] = mfma16(a1, b10, acc0[mb]);
-      acc1[mb] = mfma16(a1, b11, acc1[mb]);
-    }
+// Epilogue of one routed row of a 128-column block: (g0, g1) and (u0, u1) are
+// the f32 sums of columns (lane, lane+64) of the first and last projection.
+template <bool GLU>
+__device__ __forceinline__ void moe_finish_row(const MoeMmParams& p, int e, int pos, int cblk,
+                                               float g0, float g1, float u0, float u1,
+                                               int lane) {
+  const int col0 = cblk * 128;
+  if constexpr (GLU) {
+    // gate and up: f16(raw) -> f32 Hadamard -> f16(v * scale * svh)
+    g0 = round_f16(g0), g1 = round_f16(g1), u0 = round_f16(u0), u1 = round_f16(u1);
+    h128_wave<false>(g0, g1, lane);
+    h128_wave<false>(u0, u1, lane);
+    const uint16_t* gsv = p.gu_svh + ((size_t)e * 2) * p.width + col0;
+    const uint16_t* usv = gsv + p.width;
+    g0 = round_f16(g0 * kHadScale * h2f(gsv[lane]));
+    g1 = round_f16(g1 * kHadScale * h2f(gsv[lane + 64]));
+    u0 = round_f16(u0 * kHadScale * h2f(usv[lane]));
+    u1 = round_f16(u1 * kHadScale * h2f(usv[lane + 64]));
+    // SiLU(g) * u, then * down_suh, f32 Hadamard, f16(v * scale)
+    const float a0 = round_f16((g0 / (1.0f + expf(-g0))) * u0);
+    const float a1 = round_f16((g1 / (1.0f + expf(-g1))) * u1);
+    const uint16_t* dsu = p.down_suh + (size_t)e * p.width + col0;
+    float d0 = round_f16(a0 * h2f(dsu[lane])), d1 = round_f16(a1 * h2f(dsu[lane + 64]));
+    h128_wave<false>(d0, d1, lane);
+    uint16_t* dst = p.xd + (size_t)pos * p.width + col0;
+    dst[lane] = f2h(d0 * kHadScale);
+    dst[lane + 64] = f2h(d1 * kHadScale);
+  } else {
+    // f16(raw) -> staged Hadamard -> f16(* scale) -> f16(* svh) -> f16(* score)
+    (void)u0, (void)u1;
+    const int slot = p.sorted_slot[pos];
+    float v0 = round_f16(g0), v1 = round_f16(g1);
+    h128_wave<true>(v0, v1, lane);
+    v0 = round_f16(v0 * kHadScale);
+    v1 = round_f16(v1 * kHadScale);
+    const uint16_t* sv = p.down_svh + (size_t)e * p.width + col0;
+    const float sc = h2f(p.scores[slot]);
+    v0 = round_f16(round_f16(v0 * h2f(sv[lane])) * sc);
+    v1 = round_f16(round_f16(v1 * h2f(sv[lane + 64])) * sc);
+    uint16_t* dst = p.z + (size_t)slot * p.width + col0;
+    dst[lane] = f2h(v0);
+    dst[lane + 64] = f2h(v1);
   }
 }
 
-// Accumulators of a wave -> LDS rows [16*mb + row][32*wave + col] (f32).
-template <int MBLK>
-__device__ __forceinline__ void moe_park(float* red, int wave, int lane, int mb,
-                                         const float4v (&acc0)[MBLK],
-                                         const float4v (&acc1)[MBLK]) {
-  const int g = lane >> 4, n = lane & 15;
-  const int col = 32 * wave + 16 * (n >> 3) + (n & 7);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    red[(4 * g + r) * 128 + col] = acc0[mb][r];
-    red[(4 * g + r) * 128 + col + 8] = acc1[mb][r];
-  }
-}
-
-// Gate/up grouped QMM with the fused SwiGLU / down-prologue epilogue.
-template <int K, int CB>
-__global__ __launch_bounds__(256) void moe_gateup_kernel(MoeQmmParams p) {
-  constexpr int MBLK = kMoeBlockRows / 16;
-  __shared__ float red[2][16 * 128];  // gate, up rows of one 16-row block
-  const int blk = blockIdx.x / p.col_blocks, cblk = blockIdx.x % p.col_blocks;
+// Grouped expert QMM over one block of up to 16*MB rows, one 128-column block
+// and one K-range.  NPROJ = 2 (gate/up, GLU epilogue) or 1 (down).  Wave w
+// serves projection w / 4 and the column pair w % 4 with the QMV's loop: D
+// trellis slices and the matching A fragments of every row group in flight
+// per set, two sets in ping-pong, unconditional (clamped) loads.  Each decoded
+// step feeds the block's ceil(rows/16) row groups.
+template <int K, int CB, int NPROJ, int MB>
+__global__ __launch_bounds__(256 * NPROJ) void moe_mm_kernel(MoeMmParams p) {
+  // A rows of the block pass through LDS, three steps deep: [stage][proj][row]
+  // [8 chunks of 16 bytes], chunk c of row r at slot c ^ (r & 7) so that both
+  // the row-wise stores and the 16-row fragment reads are conflict-free.
+  constexpr int kRows = 16 * MB, kStage = NPROJ * kRows * 128;
+  __shared__ __attribute__((aligned(16))) uint8_t as[3][kStage];
+  __shared__ float red[NPROJ][16][128];  // f32 sums of one row group (one K-range)
+  __shared__ int s_last;
+  constexpr bool GLU = NPROJ == 2;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int proj = wave >> 2, pair = wave & 3;
+  // workgroup -> (block, column block, split), split fastest
+  const int split = blockIdx.x % p.splits;
+  const int bc = blockIdx.x / p.splits;
+  const int blk = bc / p.col_blocks, cblk = bc % p.col_blocks;
   if (blk >= p.counts[0]) return;  // uniform
   const int4 ent = p.table[blk];
   const int e = ent.x, pos0 = ent.y, nrows = ent.z;
-  const int mblocks = (nrows + 15) / 16;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int groups = (nrows + 15) >> 4;
+  const int nq_all = p.k_in >> 6;
+  const int qa = split * nq_all / p.splits, nq = (split + 1) * nq_all / p.splits - qa;
+
   const int g = lane >> 4, hsel = (lane >> 3) & 1, j = lane & 7, am = lane & 15;
-  const int nq = p.k_in >> 6;
+  const int tpe = p.width / 16;  // tile columns per expert
   const size_t qstride = (size_t)4 * p.tn_total * 8 * K;
-  const int tiles_per_expert = p.width / 16;
-  const int tcol = cblk * 8 + 2 * wave + hsel;
-  const uint32_t* tg = p.trellis + ((size_t)g * p.tn_total + (size_t)e * tiles_per_expert + tcol) *
-                                       (8 * K) + (size_t)j * K;
-  const uint32_t* tu = tg + (size_t)p.experts * tiles_per_expert * (8 * K);
+  const int tcol = (proj * p.experts + e) * tpe + cblk * 8 + 2 * pair + hsel;
+  const uint32_t* tp =
+      p.trellis + ((size_t)(4 * qa + g) * p.tn_total + tcol) * (8 * K) + (size_t)j * K;
   const int prev_off = j == 0 ? 8 * K - 1 : -1;
-
-  const uint16_t* ag[MBLK];
-  const uint16_t* au[MBLK];
-  bool aval[MBLK];
+  // A loader: each thread moves kPer 16-byte chunks of a step (rows past the
+  // block's end repeat its last row; their sums are never used)
+  constexpr int kThreads = 256 * NPROJ, kChunks = NPROJ * kRows * 8;
+  constexpr int kPer = (kChunks + kThreads - 1) / kThreads;
+  const uint16_t* lsrc[kPer];
+  int ldst[kPer];
+  bool lact[kPer];
 #pragma unroll
-  for (int mb = 0; mb < MBLK; ++mb) {
-    const int r = 16 * mb + am;
-    aval[mb] = r < nrows;
-    const int pos = pos0 + (aval[mb] ? r : 0);
-    ag[mb] = p.xgu + (size_t)pos * p.k_in + g * 16;
-    au[mb] = p.xgu + ((size_t)p.slots_pad + pos) * p.k_in + g * 16;
+  for (int i = 0; i < kPer; ++i) {
+    const int c = threadIdx.x + i * kThreads;
+    lact[i] = c < kChunks;
+    const int cc = lact[i] ? c : 0;
+    const int pj = cc / (kRows * 8), row = (cc / 8) % kRows, ch = cc & 7;
+    lsrc[i] = p.xa + ((size_t)pj * p.slots_pad + pos0 + min(row, nrows - 1)) * p.k_in +
+              (size_t)qa * 64 + ch * 8;
+    ldst[i] = (pj * kRows + row) * 128 + ((ch ^ (row & 7)) << 4);
   }
-  float4v gacc0[MBLK], gacc1[MBLK], uacc0[MBLK], uacc1[MBLK];
+  const int qlast = nq - 1;
+  u32x4 areg[2][kPer];
+  auto load_a = [&](u32x4(&dst)[kPer], int q) {
 #pragma unroll
-  for (int mb = 0; mb < MBLK; ++mb)
-    gacc0[mb] = gacc1[mb] = uacc0[mb] = uacc1[mb] = float4v{0.f, 0.f, 0.f, 0.f};
-
-  uint32_t wg[K + 1], wu[K + 1];
-  load_slice_prev<K>(tg, prev_off, wg);
-  load_slice_prev<K>(tu, prev_off, wu);
-  for (int q = 0; q < nq; ++q) {
-    uint32_t cg[K + 1], cu[K + 1];
+    for (int i = 0; i < kPer; ++i)
+      if (lact[i]) dst[i] = *(const u32x4*)(lsrc[i] + (size_t)min(q, qlast) * 64);
+  };
+  auto store_a = [&](const u32x4(&src)[kPer], int st) {
 #pragma unroll
-    for (int i = 0; i <= K; ++i) cg[i] = wg[i], cu[i] = wu[i];
-    const int qn = min(q + 1, nq - 1);
-    load_slice_prev<K>(tg + (size_t)qn * qstride, prev_off, wg);
-    load_slice_prev<K>(tu + (size_t)qn * qstride, prev_off, wu);
-    moe_step<K, CB, MBLK>(cg, ag, aval, mblocks, q, gacc0, gacc1);
-    moe_step<K, CB, MBLK>(cu, au, aval, mblocks, q, uacc0, uacc1);
-  }
-
-  // epilogue, one 16-row block at a time through LDS
-  const int col0 = cblk * 128;
-  for (int mb = 0; mb < MBLK; ++mb) {
-    if (mb >= mblocks) break;  // uniform
-    __syncthreads();
-    moe_park<MBLK>(red[0], wave, lane, mb, gacc0, gacc1);
-    moe_park<MBLK>(red[1], wave, lane, mb, uacc0, uacc1);
-    __syncthreads();
-    for (int r = wave; r < 16; r += 4) {
-      const int row = 16 * mb + r;
-      if (row >= nrows) break;
-      const int pos = pos0 + row;
-      // gate and up: f16(raw) -> f32 Hadamard -> f16(v * scale * svh)
-      float g0 = round_f16(red[0][r * 128 + lane]), g1 = round_f16(red[0][r * 128 + lane + 64]);
-      float u0 = round_f16(red[1][r * 128 + lane]), u1 = round_f16(red[1][r * 128 + lane + 64]);
-      h128_wave<false>(g0, g1, lane);
-      h128_wave<false>(u0, u1, lane);
-      const uint16_t* gsv = p.gu_svh + ((size_t)e * 2) * p.width + col0;
-      const uint16_t* usv = gsv + p.width;
-      g0 = round_f16(g0 * kHadScale * h2f(gsv[lane]));
-      g1 = round_f16(g1 * kHadScale * h2f(gsv[lane + 64]));
-      u0 = round_f16(u0 * kHadScale * h2f(usv[lane]));
-      u1 = round_f16(u1 * kHadScale * h2f(usv[lane + 64]));
-      // SiLU(g) * u, then * down_suh, f32 Hadamard, f16(v * scale)
-      const float a0 = round_f16((g0 / (1.0f + expf(-g0))) * u0);
-      const float a1 = round_f16((g1 / (1.0f + expf(-g1))) * u1);
-      const uint16_t* dsu = p.down_suh + (size_t)e * p.width + col0;
-      float d0 = round_f16(a0 * h2f(dsu[lane])), d1 = round_f16(a1 * h2f(dsu[lane + 64]));
-      h128_wave<false>(d0, d1, lane);
-      uint16_t* dst = p.xd + (size_t)pos * p.width + col0;
-      dst[lane] = f2h(d0 * kHadScale);
-      dst[lane + 64] = f2h(d1 * kHadScale);
+    for (int i = 0; i < kPer; ++i)
+      if (lact[i]) *(u32x4*)(&as[st][0] + ldst[i]) = src[i];
+  };
+  // fragment (mb, h) of this lane: row 16mb + am of the wave's projection, chunk 2g + h
+  int aoff[MB][2];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int row = 16 * mb + am;
+      aoff[mb][h] = (proj * kRows + row) * 128 + (((2 * g + h) ^ (row & 7)) << 4);
     }
-  }
-}
 
-// Down grouped QMM with finish_and_reduce's per-slot epilogue.
-template <int K, int CB>
-__global__ __launch_bounds__(256) void moe_down_kernel(MoeQmmParams p) {
-  constexpr int MBLK = kMoeBlockRows / 16;
-  __shared__ float red[16 * 128];
-  const int blk = blockIdx.x / p.col_blocks, cblk = blockIdx.x % p.col_blocks;
-  if (blk >= p.counts[0]) return;  // uniform
-  const int4 ent = p.table[blk];
-  const int e = ent.x, pos0 = ent.y, nrows = ent.z;
-  const int mblocks = (nrows + 15) / 16;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = lane >> 4, hsel = (lane >> 3) & 1, j = lane & 7, am = lane & 15;
-  const int nq = p.k_in >> 6;
-  const size_t qstride = (size_t)4 * p.tn_total * 8 * K;
-  const int tiles_per_expert = p.width / 16;
-  const int tcol = cblk * 8 + 2 * wave + hsel;
-  const uint32_t* tp = p.trellis + ((size_t)g * p.tn_total + (size_t)e * tiles_per_expert + tcol) *
-                                       (8 * K) + (size_t)j * K;
-  const int prev_off = j == 0 ? 8 * K - 1 : -1;
-
-  const uint16_t* ar[MBLK];
-  bool aval[MBLK];
+  constexpr int D = kQmvDepth<K>;
+  uint32_t setA[D][K + 1], setB[D][K + 1];
+  auto fetch = [&](uint32_t(&set)[D][K + 1], int qbase) {
 #pragma unroll
-  for (int mb = 0; mb < MBLK; ++mb) {
-    const int r = 16 * mb + am;
-    aval[mb] = r < nrows;
-    ar[mb] = p.xin + (size_t)(pos0 + (aval[mb] ? r : 0)) * p.k_in + g * 16;
-  }
-  float4v acc0[MBLK], acc1[MBLK];
+    for (int d = 0; d < D; ++d)
+      load_slice_prev<K>(tp + (size_t)min(qbase + d, qlast) * qstride, prev_off, set[d]);
+  };
+  float4v acc0[MB], acc1[MB];
 #pragma unroll
-  for (int mb = 0; mb < MBLK; ++mb) acc0[mb] = acc1[mb] = float4v{0.f, 0.f, 0.f, 0.f};
-
-  uint32_t w[K + 1];
-  load_slice_prev<K>(tp, prev_off, w);
-  for (int q = 0; q < nq; ++q) {
-    uint32_t c[K + 1];
+  for (int mb = 0; mb < MB; ++mb) acc0[mb] = acc1[mb] = float4v{0.f, 0.f, 0.f, 0.f};
+  // step q: A of step q+1 (loaded two steps earlier) goes to stage (q+1) % 3,
+  // step q+3 is loaded in its place, step q is multiplied from stage q % 3;
+  // one barrier per step orders the stages
+  auto compute = [&](uint32_t(&set)[D][K + 1], int qbase) {
 #pragma unroll
-    for (int i = 0; i <= K; ++i) c[i] = w[i];
-    load_slice_prev<K>(tp + (size_t)min(q + 1, nq - 1) * qstride, prev_off, w);
-    moe_step<K, CB, MBLK>(c, ar, aval, mblocks, q, acc0, acc1);
-  }
-
-  const int col0 = cblk * 128;
-  for (int mb = 0; mb < MBLK; ++mb) {
-    if (mb >= mblocks) break;  // uniform
-    __syncthreads();
-    moe_park<MBLK>(red, wave, lane, mb, acc0, acc1);
-    __syncthreads();
-    for (int r = wave; r < 16; r += 4) {
-      const int row = 16 * mb + r;
-      if (row >= nrows) break;
-      const int slot = p.sorted_slot[pos0 + row];
-      float v0 = round_f16(red[r * 128 + lane]), v1 = round_f16(red[r * 128 + lane + 64]);
-      h128_wave<true>(v0, v1, lane);
-      v0 = round_f16(v0 * kHadScale);
-      v1 = round_f16(v1 * kHadScale);
-      const uint16_t* sv = p.down_svh + (size_t)e * p.width + col0;
-      const float sc = h2f(p.scores[slot]);
-      v0 = round_f16(round_f16(v0 * h2f(sv[lane])) * sc);
-      v1 = round_f16(round_f16(v1 * h2f(sv[lane + 64])) * sc);
-      uint16_t* dst = p.z + (size_t)slot * p.width + col0;
-      dst[lane] = f2h(v0);
-      dst[lane + 64] = f2h(v1);
+    for (int d = 0; d < D; ++d) {
+      const int q = qbase + d;
+      if (q < nq) {  // uniform
+        store_a(areg[(q + 1) & 1], (q + 1) % 3);
+        load_a(areg[(q + 1) & 1], q + 3);
+        uint32_t src[32];
+        extract_states<K>(set[d], src);
+        const half8 b00 = decode_fragment<CB, K, 0, 0>(src);
+        const half8 b01 = decode_fragment<CB, K, 0, 1>(src);
+        const half8 b10 = decode_fragment<CB, K, 1, 0>(src);
+        const half8 b11 = decode_fragment<CB, K, 1, 1>(src);
+        const uint8_t* st = &as[q % 3][0];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          if (mb < groups) {
+            const half8 a0 = *(const half8*)(st + aoff[mb][0]);
+            const half8 a1 = *(const half8*)(st + aoff[mb][1]);
+            acc0[mb] = mfma16(a0, b00, acc0[mb]);
+            acc1[mb] = mfma16(a0, b01, acc1[mb]);
+            acc0[mb] = mfma16(a1, b10, acc0[mb]);
+            acc1[mb] = mfma16(a1, b11, acc1[mb]);
+          }
+        __syncthreads();
+      }
     }
+  };
+  // steps 0..2 of A: step 0 into stage 0, steps 1 and 2 in registers
+  load_a(areg[0], 0);
+  load_a(areg[1], 1);
+  fetch(setA, 0);
+  store_a(areg[0], 0);
+  load_a(areg[0], 2);
+  __syncthreads();
+  for (int q0 = 0; q0 < nq; q0 += 2 * D) {
+    fetch(setB, q0 + D);
+    compute(setA, q0);
+    fetch(setA, q0 + 2 * D);
+    compute(setB, q0 + D);
+  }
+
+  // accumulator lane l: rows 4*(l/16)+r, column 32*pair + 16*(n/8) + n%8 + 8*cg
+  const int n = lane & 15;
+  const int col = 32 * pair + 16 * (n >> 3) + (n & 7);
+  if (p.splits == 1) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      if (mb >= groups) break;  // uniform
+      if (mb > 0) __syncthreads();  // the previous group's rows are read
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        red[proj][4 * g + r][col] = acc0[mb][r];
+        red[proj][4 * g + r][col + 8] = acc1[mb][r];
+      }
+      __syncthreads();
+      const int rows = min(16, nrows - 16 * mb);
+      for (int m = wave; m < rows; m += 4 * NPROJ)
+        moe_finish_row<GLU>(p, e, pos0 + 16 * mb + m, cblk, red[0][m][lane],
+                            red[0][m][lane + 64], red[NPROJ - 1][m][lane],
+                            red[NPROJ - 1][m][lane + 64], lane);
+    }
+    return;
+  }
+
+  // split-K: partials out, count arrivals, the last arriver adds them up
+  float* part = p.partials + ((size_t)split * NPROJ + proj) * p.slots_pad * p.width;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 16 * mb + 4 * g + r;
+      if (m < nrows) {
+        float* dst = part + (size_t)(pos0 + m) * p.width + cblk * 128 + col;
+        store_coherent(dst, acc0[mb][r]);
+        store_coherent(dst + 8, acc1[mb][r]);
+      }
+    }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  uint32_t* counter = p.counters + (size_t)blk * p.col_blocks + cblk;
+  if (threadIdx.x == 0) {
+    const uint32_t old =
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = old == (uint32_t)(p.splits - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;  // uniform
+  if (threadIdx.x == 0)
+    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int m = wave; m < nrows; m += 4 * NPROJ) {
+    float v[NPROJ][2] = {};
+    for (int s = 0; s < p.splits; ++s)
+#pragma unroll
+      for (int pj = 0; pj < NPROJ; ++pj) {
+        const float* src = p.partials +
+                           ((size_t)(s * NPROJ + pj) * p.slots_pad + pos0 + m) * p.width +
+                           cblk * 128;
+        v[pj][0] += load_coherent(src + lane);
+        v[pj][1] += load_coherent(src + lane + 64);
+      }
+    moe_finish_row<GLU>(p, e, pos0 + m, cblk, v[0][0], v[0][1], v[NPROJ - 1][0],
+                        v[NPROJ - 1][1], lane);
   }
 }
 

@@ -39,10 +39,9 @@ const QmmFn kQmm[3][8][3] = {EXL3_TABLE(run_qmm1), EXL3_TABLE(run_qmm2), EXL3_TA
 
 void launch_prologue(const void* x, int x_dtype, const uint16_t* suh, int in, int rows,
                      uint16_t* xhat, hipStream_t s) {
-  const int jobs = rows * (in / 128);
-  const int per_wg = 4 * kPrologueJobs;
-  hipLaunchKernelGGL(prologue_kernel, dim3((jobs + per_wg - 1) / per_wg), dim3(256), 0, s, x,
-                     x_dtype, suh, in, jobs, xhat);
+  const int64_t waves = (int64_t)rows * ((in / 128 + 7) / 8);
+  hipLaunchKernelGGL(prologue_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, x,
+                     x_dtype, suh, in, rows, xhat);
 }
 
 void launch_fill_zero(uint32_t* p, size_t words, hipStream_t s) {

@@ -32,35 +32,18 @@
 namespace exl3 {
 
 
-// xhat = prologue(x) for all rows.  A job is one (row, 128-input block); a
-// wave takes kPrologueJobs jobs spaced by the grid, issues all their loads,
-// then runs the Hadamards, so several jobs' memory latencies overlap.
-constexpr int kPrologueJobs = 4;
+// xhat = prologue(x) for all rows: one wave per (row, run of eight 128-input
+// blocks), pair layout with the run's loads in flight together.
+// grid ceil(rows * runs / 4), 256 threads.
 __global__ __launch_bounds__(256) void prologue_kernel(const void* __restrict__ x, int x_dtype,
                                                        const uint16_t* __restrict__ suh, int in,
-                                                       int jobs, uint16_t* __restrict__ xhat) {
-  const int lane = threadIdx.x & 63;
-  const int nb = in >> 7;
-  const int stride = gridDim.x * 4;
-  const int first = blockIdx.x * 4 + (threadIdx.x >> 6);
-  PrologueIn pin[kPrologueJobs];
-#pragma unroll
-  for (int t = 0; t < kPrologueJobs; ++t) {
-    const int job = min(first + t * stride, jobs - 1);  // clamped: loads stay in bounds
-    const int m = job / nb, b = job - m * nb;
-    pin[t] = prologue_load(x, x_dtype, (size_t)m * in + b * 128, suh, b * 128, lane);
-  }
-#pragma unroll
-  for (int t = 0; t < kPrologueJobs; ++t) {
-    const int job = first + t * stride;
-    float v0, v1;
-    prologue_finish(pin[t], x_dtype, lane, v0, v1);
-    if (job < jobs) {
-      const int m = job / nb, b = job - m * nb;
-      xhat[(size_t)m * in + b * 128 + lane] = f2h(v0);
-      xhat[(size_t)m * in + b * 128 + lane + 64] = f2h(v1);
-    }
-  }
+                                                       int rows, uint16_t* __restrict__ xhat) {
+  const int nb = in >> 7, runs = (nb + 7) >> 3;
+  const int job = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = job / runs, run = job - row * runs;
+  if (row >= rows) return;  // uniform per wave
+  pair_prologue_row(x, x_dtype, (size_t)row * in, suh, 8 * run, min(8 * run + 8, nb),
+                    threadIdx.x & 63, xhat + (size_t)row * in);
 }
 
 template <int STRIDE>

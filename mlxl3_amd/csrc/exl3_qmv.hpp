@@ -179,6 +179,85 @@ __device__ __forceinline__ void prepare_row128(const void* x, int x_dtype, size_
   prologue_finish(prologue_load(x, x_dtype, off, suh, e0, lane), x_dtype, lane, v0, v1);
 }
 
+// Prologue in the pair layout (lane holds elements 2*lane and 2*lane+1 of a
+// 128-input block): one 32-bit (64-bit for f32) activation load and one 32-bit
+// suh load per lane.  The butterflies run in the same ascending order with the
+// same roundings as h128_wave: stride 1 inside the lane, strides 2..64 across
+// lanes 1..32, f16 rounding after strides 8 and 64.
+struct PairIn {
+  uint32_t x0, x1;  // raw activation bits (x1: high word of the second f32)
+  uint32_t s;       // two suh halves
+};
+__device__ __forceinline__ PairIn pair_load(const void* x, int x_dtype, size_t off,
+                                            const uint16_t* __restrict__ suh, int e0, int lane) {
+  PairIn in;
+  if (x_dtype == DT_F32) {
+    const uint2 v = ((const uint2*)((const float*)x + off))[lane];
+    in.x0 = v.x;
+    in.x1 = v.y;
+  } else {
+    in.x0 = ((const uint32_t*)((const uint16_t*)x + off))[lane];
+    in.x1 = 0;
+  }
+  in.s = ((const uint32_t*)(suh + e0))[lane];
+  return in;
+}
+// xhat bits of the lane's two elements, packed (element 2*lane low).
+__device__ __forceinline__ uint32_t pair_finish(const PairIn& in, int x_dtype, int lane) {
+  float a, b;
+  if (x_dtype == DT_F32) {
+    a = __builtin_bit_cast(float, in.x0);
+    b = __builtin_bit_cast(float, in.x1);
+  } else {
+    a = raw_act(in.x0 & 0xffffu, x_dtype);
+    b = raw_act(in.x0 >> 16, x_dtype);
+  }
+  float v0 = round_f16(round_f16(a) * h2f((uint16_t)in.s));
+  float v1 = round_f16(round_f16(b) * h2f((uint16_t)(in.s >> 16)));
+  {  // stride 1
+    const float t = v0;
+    v0 = t + v1;
+    v1 = t - v1;
+  }
+  static_for<6>([&](auto i_) {
+    constexpr int ls = 1 << decltype(i_)::value;  // element stride 2*ls
+    const float p0 = xor_lanes<ls>(v0), p1 = xor_lanes<ls>(v1);
+    if (lane & ls) {
+      v0 = p0 - v0;
+      v1 = p1 - v1;
+    } else {
+      v0 = v0 + p0;
+      v1 = v1 + p1;
+    }
+    if (ls == 4 || ls == 32) {  // after element strides 8 and 64
+      v0 = round_f16(v0);
+      v1 = round_f16(v1);
+    }
+  });
+  return (uint32_t)f2h(v0 * kHadScale) | ((uint32_t)f2h(v1 * kHadScale) << 16);
+}
+
+// Prologue of 128-input blocks [b_begin, b_end) of a row by one wave in the
+// pair layout: the loads of up to eight blocks are in flight together.
+// dst: xhat row (f16).
+__device__ __forceinline__ void pair_prologue_row(const void* x, int x_dtype, size_t xoff,
+                                                  const uint16_t* __restrict__ suh, int b_begin,
+                                                  int b_end, int lane, uint16_t* __restrict__ dst) {
+  for (int b0 = b_begin; b0 < b_end; b0 += 8) {
+    PairIn in[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int b = min(b0 + t, b_end - 1);  // clamped: loads stay in bounds
+      in[t] = pair_load(x, x_dtype, xoff + b * 128, suh, b * 128, lane);
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const uint32_t bits = pair_finish(in[t], x_dtype, lane);
+      if (b0 + t < b_end) ((uint32_t*)(dst + (b0 + t) * 128))[lane] = bits;
+    }
+  }
+}
+
 // KW waves share each column pair and split the workgroup's K-range between
 // them (reduced through LDS in a fixed order), so a workgroup of 4*KW waves
 // amortises one prologue over KW times more weight stream.

@@ -80,10 +80,12 @@ def test_moe_small_all_k_cb(k, cb):
     check(y, oracle.moe_forward(x, sel, sc, *layer, k, cb), f"moe k={k} cb={cb}")
 
 
-def test_moe_multi_block_segments_and_idle_experts():
+@pytest.mark.parametrize("block_rows", ["16", "64"])
+def test_moe_multi_block_segments_and_idle_experts(block_rows, monkeypatch):
     # 160 rows x top-2 over experts 0..2 of 5: about 107 slots per routed
-    # expert (two 64-row blocks each, the second partial), experts 3 and 4 idle
-    print("moe multi-block", flush=True)
+    # expert (several blocks each, the last partial), experts 3 and 4 idle
+    print(f"moe multi-block, {block_rows}-row blocks", flush=True)
+    monkeypatch.setenv("EXL3_MOE_BLOCK_ROWS", block_rows)
     in_f, hidden, experts, top_k, rows, k = 256, 384, 5, 2, 160, 3
     layer, x, _, _ = case(in_f, hidden, experts, top_k, rows, k, 77)
     sel, sc = synth.moe_routes(77, 530, rows, 3, top_k)
@@ -100,15 +102,32 @@ def test_moe_decode_single_token():
     check(y, oracle.moe_forward(x, sel, sc, *layer, 3, 0), "moe decode")
 
 
-def test_moe_rows_independent_and_deterministic():
+def test_moe_rows_independent_and_deterministic(monkeypatch):
+    # The K-split count follows the slot count, and splits change the f32
+    # summation order; with the split count pinned, a row's result does not
+    # depend on the other rows of the call.
     print("moe batch == serial", flush=True)
     layer, x, sel, sc = case(256, 256, 8, 4, 40, 4, 123)
+    monkeypatch.setenv("EXL3_MOE_SPLITS", "2")
     moe = make_moe(layer, 4, 4, 1)
     y = run(moe, x, sel, sc)
     np.testing.assert_array_equal(run(moe, x, sel, sc), y)
     for r in (0, 17, 39):
         np.testing.assert_array_equal(run(moe, x[r:r + 1], sel[r:r + 1], sc[r:r + 1]), y[r:r + 1])
     np.testing.assert_array_equal(run(moe, x[5:23], sel[5:23], sc[5:23]), y[5:23])
+    monkeypatch.delenv("EXL3_MOE_SPLITS")
+    moe = make_moe(layer, 4, 4, 1)
+    check(run(moe, x[:1], sel[:1], sc[:1]), oracle.moe_forward(x[:1], sel[:1], sc[:1], *layer, 4, 1),
+          "moe single row, default splits")
+
+
+@pytest.mark.parametrize("splits", [1, 3, 8])
+def test_moe_split_k_schedules(splits, monkeypatch):
+    print(f"moe splits={splits}", flush=True)
+    monkeypatch.setenv("EXL3_MOE_SPLITS", str(splits))
+    layer, x, sel, sc = case(1024, 256, 8, 2, 24, 3, 321)
+    moe = make_moe(layer, 2, 3, 0)
+    check(run(moe, x, sel, sc), oracle.moe_forward(x, sel, sc, *layer, 3, 0), f"moe splits={splits}")
 
 
 def test_moe_c4_full_shape():

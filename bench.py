@@ -145,6 +145,90 @@ def cpu_baseline(n_in, n_out, k, cb, rows, budget_s=12.0):
     }
 
 
+def moe_leg(steps, warmup):
+    """C4 expert block (hidden 2048, 128 experts x 768, top-8, 256 tokens, K=3
+    3INST): one SwitchGLU forward per step through the C ABI, graph replays
+    rotating over copies of the 226 MB bank so each step streams it from HBM."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    import mlxl3_amd
+    from mlxl3_amd import synth
+
+    in_f, hidden, experts, top_k, k, rows = 2048, 768, 128, 8, 3, 256
+    layer = synth.moe_layer(4, 500, in_f, hidden, experts, k)
+
+    def dev(a):
+        if a.dtype == np.uint16:
+            a = a.view(np.int16)
+        elif a.dtype == np.uint32:
+            a = a.astype(np.int32)
+        return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+    bank = [dev(a) for a in layer]
+    bank_bytes = (bank[0].numel() + bank[3].numel()) * 2
+    copies = max(2, math.ceil(ROTATE_BYTES / bank_bytes))
+    trellises = [(bank[0], bank[3])] + [(bank[0].clone(), bank[3].clone()) for _ in range(copies - 1)]
+    moes = [mlxl3_amd.Exl3SwitchGlu(g, bank[1], bank[2], d, bank[4], bank[5], top_k=top_k, k=k, cb=0)
+            for g, d in trellises]
+    x = dev(synth.activations(4, 510, rows, in_f))
+    sel, sc = synth.moe_routes(4, 520, rows, experts, top_k)
+    sel, sc = dev(sel), dev(sc)
+    y = torch.empty_like(x)
+    lib = mlxl3_amd.load_library()
+    nws = int(lib.exl3_moe_workspace_bytes(moes[0]._handle, rows))
+    ws = torch.zeros(nws + 4096, dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def call(m):  # on the current stream (the capture stream inside torch.cuda.graph)
+        rc = lib.exl3_moe_forward(m._handle, x.data_ptr(), rows, sel.data_ptr(), sc.data_ptr(),
+                                  y.data_ptr(), ws.data_ptr(), ws.numel(),
+                                  ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc:
+            raise RuntimeError(lib.exl3_last_error().decode())
+
+    for m in moes:
+        call(m)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for m in moes:
+            call(m)
+    reps = max(1, warmup // len(moes))
+    for _ in range(reps):
+        g.replay()
+    torch.cuda.synchronize()
+    reps = max(1, math.ceil(steps / len(moes)))
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        g.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / (reps * len(moes))
+    nbytes = bank_bytes + rows * in_f * 2 * 2 + (experts * 2 * in_f + experts * 2 * hidden
+                                                  + experts * hidden + experts * in_f) * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {
+        "workload": f"moe_switchglu_{in_f}x{hidden}_e{experts}_top{top_k}_rows{rows}_k{k}_3inst",
+        "ms_per_step": round(ms, 6),
+        "steps": reps * len(moes),
+        "bank_copies_rotated": copies,
+        "bytes_per_step": nbytes,
+        "gflop_per_step": round(2.0 * rows * top_k * 3 * in_f * hidden / 1e9, 3),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -152,6 +236,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-qmm", action="store_true", help="skip the QMM M=512 leg")
+    ap.add_argument("--no-moe", action="store_true", help="skip the MoE SwitchGLU leg")
     ap.add_argument("--k", type=int, default=4)
     ap.add_argument("--cb", type=int, default=0)
     ap.add_argument("--in-features", type=int, default=4096)
@@ -244,6 +329,9 @@ def main():
             },
         }
         del qlins, _qw
+
+    if not args.no_moe:
+        result["moe"] = moe_leg(max(8, args.steps // 40), max(2, args.warmup // 40))
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(n_in, n_out, k, cb, rows)

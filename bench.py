@@ -224,7 +224,8 @@ def moe_leg(steps, warmup):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(
+                f"moe_switchglu_{in_f}x{hidden}_e{experts}_top{top_k}_rows{rows}_k{k}_3inst"),
         },
     }
 
@@ -325,7 +326,7 @@ def main():
                 "peak": FP16_MFMA_PEAK_TFLOPS,
                 "unit": "TFLOP/s",
                 "frac": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4),
-                "traffic": None,
+                "traffic": measured_traffic(f"qmm_{n_in}x{n_out}_k{k}_m{m}"),
             },
         }
         del qlins, _qw

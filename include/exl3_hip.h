@@ -124,6 +124,77 @@ int exl3_moe_forward(const exl3_moe* handle, const uint16_t* x, int64_t rows,
 int exl3_decode_tiles(const uint16_t* packed, int64_t tiles, int32_t k, int32_t cb,
                       uint16_t* states, uint16_t* values, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Checkpoints (safetensors EXL3 model directories).
+ *
+ * exl3_checkpoint_open replaces checkpoint::inspect
+ * (native/src/checkpoint.rs:197-330, with read_header :38-93): it reads
+ * config.json, quantization_config.json (quant_method "exl3",
+ * tensor_storage) and the header of every model*.safetensors shard, and
+ * validates them with the reference's checks and messages (payload tiled by
+ * the tensors exactly, no duplicate tensors, tokenizer files present,
+ * stored_tensors shapes, every exl3 module's trellis and suh/svh (or legacy
+ * su/sv), the shard index).  No payload is read; shards stay open until
+ * exl3_checkpoint_close.  A checkpoint handle is immutable and may be shared
+ * between threads.
+ * ------------------------------------------------------------------------ */
+typedef struct exl3_checkpoint exl3_checkpoint;
+
+/* TensorInfo (checkpoint.rs:15-26) of one tensor. */
+typedef struct {
+  char dtype[8];      /* safetensors dtype, e.g. "I16", "F16" */
+  int32_t ndim;       /* at most 8 */
+  int64_t shape[8];
+  uint64_t offset;    /* absolute byte offset of the payload in its shard */
+  uint64_t bytes;     /* payload size */
+  const char* shard;  /* shard path, valid until the checkpoint is closed */
+} exl3_tensor_info;
+
+int exl3_checkpoint_open(const char* dir, exl3_checkpoint** out_handle);
+void exl3_checkpoint_close(exl3_checkpoint* ckpt);
+
+/* Checkpoint fields (checkpoint.rs:129-137): canonical path, config
+ * model_type ("unknown" if absent), quantization bits (NaN if absent), total
+ * size of the directory's files, sorted exl3 module prefixes. */
+const char* exl3_checkpoint_path(const exl3_checkpoint* ckpt);
+const char* exl3_checkpoint_model_type(const exl3_checkpoint* ckpt);
+double exl3_checkpoint_bits(const exl3_checkpoint* ckpt);
+uint64_t exl3_checkpoint_size_bytes(const exl3_checkpoint* ckpt);
+int32_t exl3_checkpoint_module_count(const exl3_checkpoint* ckpt);
+const char* exl3_checkpoint_module(const exl3_checkpoint* ckpt, int32_t index);
+
+/* Tensor names in sorted order, and one tensor's record. */
+int64_t exl3_checkpoint_tensor_count(const exl3_checkpoint* ckpt);
+const char* exl3_checkpoint_tensor_name(const exl3_checkpoint* ckpt, int64_t index);
+int exl3_checkpoint_tensor(const exl3_checkpoint* ckpt, const char* name, exl3_tensor_info* info);
+
+/* TensorInfo::read_bytes (checkpoint.rs:113-125): copies the raw payload
+ * into host memory `dst` of exactly info.bytes bytes. */
+int exl3_checkpoint_read(const exl3_checkpoint* ckpt, const char* name, void* dst, size_t bytes);
+
+/* A float tensor (F16, BF16 or F32) as `count` f16 values, rounded to nearest
+ * even as MLX astype(Float16) rounds (the conversion exl3_linear_load applies
+ * to scales and bias, linear.rs:527, :857, :993). */
+int exl3_checkpoint_read_f16(const exl3_checkpoint* ckpt, const char* name, uint16_t* dst,
+                             size_t count);
+
+/* Exl3Linear::from_checkpoint (linear.rs:454-575): {prefix}.trellis (U16 or
+ * I16), {prefix}.suh or .su, {prefix}.svh or .sv, optional {prefix}.bias;
+ * codebook MUL1 if {prefix}.mul1 exists, else MCG if {prefix}.mcg exists,
+ * else 3INST; K = last trellis dimension / 16.  Scales and bias are rounded
+ * to f16 (F16, BF16 or F32 on disk).  The weights are uploaded to the current
+ * HIP device; the handle owns them and exl3_linear_destroy frees them. */
+int exl3_linear_load(const exl3_checkpoint* ckpt, const char* prefix, exl3_linear** out_handle);
+
+/* Exl3SwitchGlu::from_checkpoint / from_lfm_checkpoint (moe.rs:629-660,
+ * :681-800): experts {prefix}.{e}.{gate|up|down} for e < experts, projection
+ * names "gate_proj"/"up_proj"/"down_proj" when NULL (LFM: "w1", "w3", "w2").
+ * Every expert must share K, codebook and shapes; scales must be F16.  The
+ * assembled bank is uploaded to the current HIP device and owned by the
+ * handle. */
+int exl3_moe_load(const exl3_checkpoint* ckpt, const char* prefix, int32_t experts, int32_t top_k,
+                  const char* gate, const char* up, const char* down, exl3_moe** out_handle);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,6 +9,8 @@ behaviour:
 * :class:`Exl3Group`    -- ``Exl3Group::forward`` (linear.rs:2285-2382)
 * :class:`Exl3SwitchGlu` -- ``Exl3SwitchGlu::new`` / ``forward`` (native/src/moe.rs:809-975)
 * :func:`decode_tiles`  -- the ``metal-decode`` codec op (exl3.metal:102-109)
+* :class:`Checkpoint`   -- ``checkpoint::inspect`` / ``TensorInfo`` (native/src/checkpoint.rs),
+  with ``Exl3Linear.from_checkpoint`` and ``Exl3SwitchGlu.from_checkpoint``
 
 PyTorch is used only to own device memory and to name the current stream.
 There is no CPU fallback: without the built library every entry point raises.
@@ -24,6 +26,8 @@ from typing import Optional, Sequence
 LIB_PATH = Path(__file__).resolve().parent / "libexl3_hip.so"
 
 __all__ = [
+    "Checkpoint",
+    "TensorInfo",
     "Codebook",
     "Exl3Error",
     "Exl3Linear",
@@ -78,6 +82,25 @@ _SIGNATURES = {
     "exl3_moe_workspace_bytes": (_sz, [_vp, _i64]),
     "exl3_moe_forward": (_i32, [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
     "exl3_decode_tiles": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _vp]),
+    "exl3_checkpoint_open": (_i32, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "exl3_checkpoint_close": (None, [_vp]),
+    "exl3_checkpoint_path": (ctypes.c_char_p, [_vp]),
+    "exl3_checkpoint_model_type": (ctypes.c_char_p, [_vp]),
+    "exl3_checkpoint_bits": (ctypes.c_double, [_vp]),
+    "exl3_checkpoint_size_bytes": (ctypes.c_uint64, [_vp]),
+    "exl3_checkpoint_module_count": (_i32, [_vp]),
+    "exl3_checkpoint_module": (ctypes.c_char_p, [_vp, _i32]),
+    "exl3_checkpoint_tensor_count": (_i64, [_vp]),
+    "exl3_checkpoint_tensor_name": (ctypes.c_char_p, [_vp, _i64]),
+    "exl3_checkpoint_tensor": (_i32, [_vp, ctypes.c_char_p, _vp]),
+    "exl3_checkpoint_read": (_i32, [_vp, ctypes.c_char_p, _vp, _sz]),
+    "exl3_checkpoint_read_f16": (_i32, [_vp, ctypes.c_char_p, _vp, _sz]),
+    "exl3_linear_load": (_i32, [_vp, ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "exl3_moe_load": (
+        _i32,
+        [_vp, ctypes.c_char_p, _i32, _i32, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
+         ctypes.POINTER(_vp)],
+    ),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
@@ -159,6 +182,125 @@ class _Workspace:
         return self.buf
 
 
+class _TensorInfoC(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_char * 8),
+        ("ndim", ctypes.c_int32),
+        ("shape", ctypes.c_int64 * 8),
+        ("offset", ctypes.c_uint64),
+        ("bytes", ctypes.c_uint64),
+        ("shard", ctypes.c_char_p),
+    ]
+
+
+class TensorInfo:
+    """TensorInfo (native/src/checkpoint.rs:15-26): dtype, shape, shard file and
+    the absolute byte range of the payload in it."""
+
+    __slots__ = ("name", "dtype", "shape", "shard", "offset", "nbytes")
+
+    def __init__(self, name, dtype, shape, shard, offset, nbytes):
+        self.name, self.dtype, self.shape = name, dtype, shape
+        self.shard, self.offset, self.nbytes = shard, offset, nbytes
+
+    def __repr__(self):
+        return f"TensorInfo({self.name!r}, {self.dtype}, {list(self.shape)}, {self.shard!r}@{self.offset})"
+
+
+# safetensors dtype -> numpy dtype string for Checkpoint.read
+_NP_DTYPES = {
+    "BOOL": "?", "U8": "u1", "I8": "i1", "F8_E4M3": "u1", "F8_E5M2": "u1", "U16": "<u2",
+    "I16": "<i2", "F16": "<f2", "BF16": "<u2", "U32": "<u4", "I32": "<i4", "F32": "<f4",
+    "U64": "<u8", "I64": "<i8", "F64": "<f8",
+}
+
+
+class Checkpoint:
+    """An inspected EXL3 model directory (``checkpoint::inspect``,
+    native/src/checkpoint.rs:197-330): headers validated, no payload read.
+
+    ``modules`` lists the exl3 projection prefixes; ``tensors`` maps every
+    tensor name to its :class:`TensorInfo`; :meth:`read` returns one payload
+    as a numpy array (BF16 as its raw uint16 bits).
+    """
+
+    def __init__(self, path):
+        lib = load_library()
+        h = _vp()
+        _check(lib.exl3_checkpoint_open(str(path).encode(), ctypes.byref(h)))
+        self._handle = h
+        self.path = lib.exl3_checkpoint_path(h).decode()
+        self.model_type = lib.exl3_checkpoint_model_type(h).decode()
+        bits = lib.exl3_checkpoint_bits(h)
+        self.bits = None if bits != bits else float(bits)
+        self.size_bytes = int(lib.exl3_checkpoint_size_bytes(h))
+        self.modules = [lib.exl3_checkpoint_module(h, i).decode()
+                        for i in range(lib.exl3_checkpoint_module_count(h))]
+        self._names = [lib.exl3_checkpoint_tensor_name(h, i).decode()
+                       for i in range(lib.exl3_checkpoint_tensor_count(h))]
+        self._infos = {}
+
+    @property
+    def handle(self):
+        return self._handle
+
+    def close(self):
+        h = getattr(self, "_handle", None)
+        if h is not None and h.value and _lib is not None:
+            _lib.exl3_checkpoint_close(h)
+        self._handle = None
+
+    __del__ = close
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __contains__(self, name) -> bool:
+        return self.info(name, missing_ok=True) is not None
+
+    @property
+    def tensor_names(self):
+        return list(self._names)
+
+    def info(self, name: str, missing_ok: bool = False) -> Optional[TensorInfo]:
+        if name in self._infos:
+            return self._infos[name]
+        rec = _TensorInfoC()
+        status = load_library().exl3_checkpoint_tensor(self._handle, name.encode(), ctypes.byref(rec))
+        if status != 0:
+            if missing_ok and status == -1:
+                return None
+            _check(status)
+        info = TensorInfo(name, rec.dtype.decode(), tuple(rec.shape[: rec.ndim]), rec.shard.decode(),
+                          int(rec.offset), int(rec.bytes))
+        self._infos[name] = info
+        return info
+
+    def read(self, name: str):
+        """TensorInfo::read_bytes (checkpoint.rs:113-125) as a numpy array."""
+        import numpy as np
+
+        info = self.info(name)
+        out = np.empty(info.nbytes, dtype=np.uint8)
+        _check(load_library().exl3_checkpoint_read(self._handle, name.encode(),
+                                                   out.ctypes.data_as(_vp), info.nbytes))
+        return out.view(np.dtype(_NP_DTYPES[info.dtype])).reshape(info.shape)
+
+    def read_f16(self, name: str):
+        """A float tensor rounded to f16 (astype(Float16)) as a numpy float16 array."""
+        import numpy as np
+
+        info = self.info(name)
+        count = int(np.prod(info.shape, dtype=np.int64))
+        out = np.empty(count, dtype=np.float16)
+        _check(load_library().exl3_checkpoint_read_f16(self._handle, name.encode(),
+                                                       out.ctypes.data_as(_vp), count))
+        return out.reshape(info.shape)
+
+
 class Exl3Linear:
     """Exl3Linear (native/src/linear.rs:424-998) on one MI355X.
 
@@ -198,6 +340,29 @@ class Exl3Linear:
         )
         self._handle = h
         self._ws = _Workspace()
+
+    @classmethod
+    def from_checkpoint(cls, checkpoint: "Checkpoint", prefix: str, device=None) -> "Exl3Linear":
+        """Exl3Linear::from_checkpoint (linear.rs:454-575): loads {prefix}.trellis,
+        suh/su, svh/sv and an optional bias to `device` (default: the current one);
+        the codebook follows the {prefix}.mul1 / .mcg flags."""
+        torch = _torch()
+        device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+        h = _vp()
+        with torch.cuda.device(device):
+            _check(load_library().exl3_linear_load(checkpoint.handle, prefix.encode(), ctypes.byref(h)))
+        self = cls.__new__(cls)
+        self._handle = h
+        self._ws = _Workspace()
+        self.trellis = self.suh = self.svh = self.bias = None  # owned by the handle
+        lib = load_library()
+        self.in_features = int(lib.exl3_linear_in_features(h))
+        self.out_features = int(lib.exl3_linear_out_features(h))
+        self.k = checkpoint.info(prefix + ".trellis").shape[-1] // 16
+        self.cb = (Codebook.MUL1 if prefix + ".mul1" in checkpoint
+                   else Codebook.MCG if prefix + ".mcg" in checkpoint else Codebook.DEFAULT)
+        self.device = device
+        return self
 
     def __del__(self):
         h = getattr(self, "_handle", None)
@@ -301,6 +466,37 @@ class Exl3SwitchGlu:
         )
         self._handle = h
         self._ws = _Workspace()
+
+    @classmethod
+    def from_checkpoint(cls, checkpoint: "Checkpoint", prefix: str, experts: int, top_k: int,
+                        names=("gate_proj", "up_proj", "down_proj"), device=None) -> "Exl3SwitchGlu":
+        """Exl3SwitchGlu::from_checkpoint (moe.rs:629-645, :681-800): experts
+        {prefix}.{e}.{gate,up,down}, assembled into one bank on `device`."""
+        torch = _torch()
+        device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+        gate, up, down = (n.encode() for n in names)
+        h = _vp()
+        with torch.cuda.device(device):
+            _check(load_library().exl3_moe_load(checkpoint.handle, prefix.encode(), int(experts),
+                                                 int(top_k), gate, up, down, ctypes.byref(h)))
+        self = cls.__new__(cls)
+        self._handle = h
+        self._ws = _Workspace()
+        self.tensors = []  # owned by the handle
+        first = checkpoint.info(f"{prefix}.0.{names[0]}.trellis")
+        self.input, self.hidden = first.shape[0] * 16, first.shape[1] * 16
+        self.experts, self.top_k = int(experts), int(top_k)
+        self.k = first.shape[-1] // 16
+        base = f"{prefix}.0.{names[0]}"
+        self.cb = (Codebook.MUL1 if base + ".mul1" in checkpoint
+                   else Codebook.MCG if base + ".mcg" in checkpoint else Codebook.DEFAULT)
+        return self
+
+    @classmethod
+    def from_lfm_checkpoint(cls, checkpoint: "Checkpoint", prefix: str, experts: int, top_k: int,
+                            device=None) -> "Exl3SwitchGlu":
+        """Exl3SwitchGlu::from_lfm_checkpoint (moe.rs:647-661): w1/w3/w2 experts."""
+        return cls.from_checkpoint(checkpoint, prefix, experts, top_k, ("w1", "w3", "w2"), device)
 
     def __del__(self):
         h = getattr(self, "_handle", None)

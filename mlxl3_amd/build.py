@@ -19,7 +19,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libexl3_hip.so"
-SOURCES = ["exl3_api.hip", "exl3_qmv.hip", "exl3_qmm.hip", "exl3_moe.hip"]
+SOURCES = ["exl3_api.hip", "exl3_qmv.hip", "exl3_qmm.hip", "exl3_moe.hip", "exl3_checkpoint.cpp"]
 ARCH = "gfx950"
 
 # -ffp-contract=off: every f32 multiply/add in the glue is rounded separately,

@@ -47,7 +47,10 @@ struct exl3_linear {
   int in, out, k, cb;
   int qmv_splits;
   int qmv_kw;  // K-parts per column pair inside a workgroup (1, 2, 4)
+  void* owned;  // device memory freed with the handle (checkpoint loads), or null
 };
+
+void exl3::adopt_device_memory(exl3_linear* h, void* mem) { h->owned = mem; }
 
 static constexpr int kQmvMaxRows = 16;
 static constexpr size_t kAlign = 256;
@@ -239,11 +242,15 @@ int exl3_linear_create(const uint16_t* trellis, int32_t in, int32_t out, int32_t
   h->k = k;
   h->cb = cb;
   choose_qmv_shape(in, out, &h->qmv_splits, &h->qmv_kw);
+  h->owned = nullptr;
   *out_handle = h;
   return EXL3_OK;
 }
 
-void exl3_linear_destroy(exl3_linear* handle) { delete handle; }
+void exl3_linear_destroy(exl3_linear* handle) {
+  if (handle && handle->owned) (void)hipFree(handle->owned);
+  delete handle;
+}
 
 int32_t exl3_linear_in_features(const exl3_linear* h) { return h ? h->in : 0; }
 int32_t exl3_linear_out_features(const exl3_linear* h) { return h ? h->out : 0; }

@@ -8,6 +8,9 @@
 
 #include "exl3_params.hpp"
 
+struct exl3_linear;
+struct exl3_moe;
+
 namespace exl3 {
 
 typedef void (*QmvFn)(const QmvParams&, dim3, size_t, hipStream_t);
@@ -27,6 +30,11 @@ void launch_fill_zero(uint32_t* p, size_t words, hipStream_t s);
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // Converts a pending launch error into EXL3_EDEVICE.
 int check_launch(const char* what);
+
+// Hands a device allocation (hipMalloc) to a handle, which frees it when it is
+// destroyed: the checkpoint loaders own the weights they upload.
+void adopt_device_memory(exl3_linear* h, void* mem);
+void adopt_device_memory(exl3_moe* h, void* mem);
 
 }  // namespace exl3
 

@@ -49,7 +49,10 @@ struct exl3_moe {
   const uint16_t *down_trellis, *down_suh, *down_svh;
   int in, hidden, experts, top_k, k, cb;
   int force_splits;  // EXL3_MOE_SPLITS at create (0: by slot count)
+  void* owned;       // device memory freed with the handle (checkpoint loads), or null
 };
+
+void exl3::adopt_device_memory(exl3_moe* h, void* mem) { h->owned = mem; }
 
 // The largest bank the plan kernel's LDS histogram holds (3 ints per expert).
 static constexpr int kMoeMaxExperts = 4096;
@@ -133,13 +136,16 @@ int exl3_moe_create(const uint16_t* gu_trellis, const uint16_t* gu_suh, const ui
   exl3_moe* h = new (std::nothrow) exl3_moe;
   if (!h) return fail(EXL3_ENOMEM, "out of host memory");
   *h = exl3_moe{gu_trellis, gu_suh, gu_svh, down_trellis, down_suh, down_svh,
-                in,         hidden, experts, top_k,       k,        cb,       0};
+                in,         hidden, experts, top_k,       k,        cb,       0, nullptr};
   if (const char* env = getenv("EXL3_MOE_SPLITS")) h->force_splits = std::max(0, atoi(env));
   *out_handle = h;
   return EXL3_OK;
 }
 
-void exl3_moe_destroy(exl3_moe* h) { delete h; }
+void exl3_moe_destroy(exl3_moe* h) {
+  if (h && h->owned) (void)hipFree(h->owned);
+  delete h;
+}
 
 size_t exl3_moe_workspace_bytes(const exl3_moe* h, int64_t rows) {
   MoeLayout L;

@@ -12,6 +12,9 @@ is reproducible on any host and independent of generation order.
 
 from __future__ import annotations
 
+import json
+from pathlib import Path
+
 import numpy as np
 
 _GOLD = np.uint64(0x9E3779B97F4A7C15)
@@ -121,3 +124,89 @@ def moe_routes(seed: int, tensor_id: int, rows: int, experts: int, top_k: int):
     top = np.take_along_axis(p, order, axis=1)
     top /= top.sum(axis=1, keepdims=True)
     return order.astype(np.uint32), top.astype(np.float16)
+
+
+# ---------------------------------------------------------------------------
+# safetensors / checkpoint writers (synthetic EXL3 model directories)
+# ---------------------------------------------------------------------------
+_ST_DTYPES = {
+    np.dtype("bool"): "BOOL", np.dtype("uint8"): "U8", np.dtype("int8"): "I8",
+    np.dtype("uint16"): "U16", np.dtype("int16"): "I16", np.dtype("float16"): "F16",
+    np.dtype("uint32"): "U32", np.dtype("int32"): "I32", np.dtype("float32"): "F32",
+    np.dtype("uint64"): "U64", np.dtype("int64"): "I64", np.dtype("float64"): "F64",
+}
+
+
+def safetensors_bytes(tensors: dict, metadata: dict | None = None, pad_to: int = 8) -> bytes:
+    """One safetensors file: 8-byte little-endian header length, JSON header,
+    payloads packed in insertion order.  A value is a numpy array or a
+    (dtype string, array) pair whose bytes are stored as given (e.g.
+    ("BF16", uint16 bits))."""
+    header, blobs, offset = {}, [], 0
+    if metadata is not None:
+        header["__metadata__"] = metadata
+    for name, value in tensors.items():
+        dtype, arr = value if isinstance(value, tuple) else (_ST_DTYPES[value.dtype], value)
+        arr = np.asarray(arr, order="C")  # keeps 0-d scalars 0-d
+        raw = arr.astype(arr.dtype.newbyteorder("<"), copy=False).tobytes()
+        header[name] = {"dtype": dtype, "shape": list(arr.shape),
+                        "data_offsets": [offset, offset + len(raw)]}
+        blobs.append(raw)
+        offset += len(raw)
+    text = json.dumps(header, separators=(",", ":")).encode()
+    text += b" " * (-len(text) % pad_to)
+    return len(text).to_bytes(8, "little") + text + b"".join(blobs)
+
+
+def write_checkpoint(root, shards: list, storage: dict, model_type: str = "llama",
+                     bits: float | None = 4.0, index: bool = True, tokenizer: bool = True) -> Path:
+    """An EXL3 model directory: config.json, quantization_config.json
+    (quant_method "exl3", tensor_storage = storage), tokenizer.json, shards
+    model-0000i-of-0000n.safetensors and their weight-map index."""
+    root = Path(root)
+    root.mkdir(parents=True, exist_ok=True)
+    (root / "config.json").write_text(json.dumps({"model_type": model_type}))
+    quant = {"quant_method": "exl3", "tensor_storage": storage}
+    if bits is not None:
+        quant["bits"] = bits
+    (root / "quantization_config.json").write_text(json.dumps(quant))
+    if tokenizer:
+        (root / "tokenizer.json").write_text("{}")
+    weight_map = {}
+    n = len(shards)
+    for i, tensors in enumerate(shards):
+        name = "model.safetensors" if n == 1 else f"model-{i + 1:05d}-of-{n:05d}.safetensors"
+        (root / name).write_bytes(safetensors_bytes(tensors))
+        weight_map.update({t: name for t in tensors})
+    if index:
+        (root / "model.safetensors.index.json").write_text(json.dumps({"weight_map": weight_map}))
+    return root
+
+
+def exl3_tensors(prefix: str, trellis_u16: np.ndarray, suh: np.ndarray, svh: np.ndarray,
+                 bias: np.ndarray | None = None, cb: int = 0, legacy_names: bool = False,
+                 scale_dtype: str = "F16", signed: bool = True) -> dict:
+    """The tensors of one EXL3 projection as a checkpoint stores them:
+    {prefix}.trellis (I16 or U16), .suh/.svh (or legacy .su/.sv) as F16, BF16
+    or F32, optional .bias (F16), and a .mcg / .mul1 flag tensor for the MCG /
+    MUL1 codebooks."""
+    def scale(v):
+        v32 = np.asarray(v, dtype=np.float32)
+        if scale_dtype == "F32":
+            return v32
+        if scale_dtype == "BF16":
+            bits = v32.view(np.uint32)
+            # round to nearest even into bfloat16 bits
+            rounded = (bits + np.uint32(0x7FFF) + ((bits >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)
+            return ("BF16", rounded.astype(np.uint16))
+        return v32.astype(np.float16)
+    su, sv = ("su", "sv") if legacy_names else ("suh", "svh")
+    t = trellis_u16.view(np.int16) if signed else trellis_u16
+    out = {f"{prefix}.trellis": t, f"{prefix}.{su}": scale(suh), f"{prefix}.{sv}": scale(svh)}
+    if bias is not None:
+        out[f"{prefix}.bias"] = np.asarray(bias, dtype=np.float16)
+    if cb == 1:
+        out[f"{prefix}.mcg"] = np.array(0xCBAC1FED, dtype=np.uint32).view(np.int32).reshape(())
+    elif cb == 2:
+        out[f"{prefix}.mul1"] = np.array(0x83DCD12D, dtype=np.uint32).view(np.int32).reshape(())
+    return out

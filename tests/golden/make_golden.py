@@ -12,7 +12,8 @@ records for them:
                (K = 2..8, cb = 0..2, 4 tiles each; sha256 from reference.json).  Used by
                tests/test_native_quantizer.py:299-336.  The only 3INST vectors.
 * real_tiles/  docs/native-coverage/baselines/exl3/{flash,qwen-dense,qwen-moe,lfm-moe}.json
-               (3 real checkpoint tiles each: packed, states, f16 bits).  Used by
+               (3 real checkpoint tiles each: packed, states, f16 bits, and the
+               byte offset of each tile in its shard).  Used by
                native/tests/contracts.rs:617-669.
 * hadamard/    tests/fixtures/native-converter-host/hadamard.{npz,json} (MLX 0.32.2 f32
                hadamard_transform outputs; sha256 in hadamard.json).  Used by
@@ -59,9 +60,13 @@ def main(ref: Path) -> None:
     t_dst.mkdir(exist_ok=True)
     for name in ("flash", "qwen-dense", "qwen-moe", "lfm-moe"):
         data = json.loads((t_src / f"{name}.json").read_text())
-        keep = {k: data[k] for k in ("checkpoint", "tensor", "dtype", "shape", "k", "mode")}
+        keep = {
+            k: data[k]
+            for k in ("checkpoint", "shard", "header_sha256", "tensor", "dtype", "shape", "k", "mode")
+        }
         keep["tiles"] = [
-            {k: t[k] for k in ("tile", "packed", "states", "f16_bits")} for t in data["tiles"]
+            {k: t[k] for k in ("tile", "shard_offset_bytes", "packed", "states", "f16_bits")}
+            for t in data["tiles"]
         ]
         (t_dst / f"{name}.json").write_text(json.dumps(keep))
 

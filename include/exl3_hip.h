@@ -24,7 +24,9 @@
  * Workspace: forward calls take a caller-owned device workspace of at least
  * *_workspace_bytes(rows) bytes.  A workspace must be zero-filled once before
  * its first use (exl3_workspace_init does that on a stream); every call leaves
- * it reusable.  Calls that share one workspace must not run concurrently.
+ * it reusable by any entry point (its first 64 KiB hold counters that every
+ * call leaves at zero).  Calls that share one workspace must not run
+ * concurrently.
  *
  * Threading: handles are immutable after creation and may be used from any
  * thread; error messages are per thread.
@@ -92,12 +94,35 @@ int exl3_linear_forward(const exl3_linear* handle, const void* x, int32_t x_type
                         void* y, int32_t y_type, void* workspace, size_t workspace_bytes,
                         void* stream);
 
-/* Exl3Group::forward, linear.rs:2313-2382: several projections with the same
- * input width applied to one x; ys[i] receives parts[i]'s output (dtype of
- * x).  Workspace: the maximum of the parts' requirements. */
+/* Exl3Group::new/forward, linear.rs:2285-2382: up to 8 projections with the
+ * same input width, K and codebook applied to one x (q/k/v, gate/up); ys[i]
+ * receives parts[i]'s output (dtype of x).  One launch covers every member's
+ * column blocks (rows <= 16), or one prologue launch and one QMM launch (rows
+ * > 16); each member's output is bit-identical to its own exl3_linear_forward.
+ * Workspace: exl3_group_workspace_bytes. */
+size_t exl3_group_workspace_bytes(const exl3_linear* const* parts, int32_t count, int64_t rows);
 int exl3_group_forward(const exl3_linear* const* parts, int32_t count, const void* x,
                        int32_t x_type, int64_t rows, void* const* ys, void* workspace,
                        size_t workspace_bytes, void* stream);
+
+/* Array::swiglu, native/ffi/mlx_bridge.cpp:745-749: out[i] =
+ * (g * sigmoid(g)) * u of f16 gate[i], up[i], every operation rounded to f16
+ * (sigmoid as MLX: y = 1 / (1 + exp(-|g|)), g < 0 ? 1 - y : y). */
+int exl3_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t count,
+                void* stream);
+
+/* Dense SwiGLU MLP of a decoder layer, qwen35.rs:303-307 (Exl3Group of
+ * gate/up, Array::swiglu, down Exl3Linear::forward): y[rows][down.out] =
+ * down(swiglu(gate(x), up(x))), f16 x and y; gate and up share in, out, K and
+ * codebook, down.in = gate.out.  The SwiGLU (and, for rows > 16, the down
+ * projection's input prologue) runs in the epilogue of the (gate, up) launch;
+ * the result is bit-identical to exl3_group_forward + exl3_swiglu +
+ * exl3_linear_forward.  Workspace: exl3_mlp_workspace_bytes. */
+size_t exl3_mlp_workspace_bytes(const exl3_linear* gate, const exl3_linear* up,
+                                const exl3_linear* down, int64_t rows);
+int exl3_mlp_forward(const exl3_linear* gate, const exl3_linear* up, const exl3_linear* down,
+                     const uint16_t* x, int64_t rows, uint16_t* y, void* workspace,
+                     size_t workspace_bytes, void* stream);
 
 /* Exl3SwitchGlu::new, moe.rs:809-900 (SiLU).  gu_trellis
  * [in/16][2*E*H/16][16k] (gate tiles of expert e at columns [e*H/16,

@@ -6,7 +6,9 @@ operator types on top of that ABI, with the same argument meaning and error
 behaviour:
 
 * :class:`Exl3Linear`   -- ``Exl3Linear::new`` / ``forward`` (native/src/linear.rs:577-998)
-* :class:`Exl3Group`    -- ``Exl3Group::forward`` (linear.rs:2285-2382)
+* :class:`Exl3Group`    -- ``Exl3Group::forward`` (linear.rs:2285-2382), one launch
+* :func:`swiglu`, :class:`Exl3Mlp` -- ``Array::swiglu`` (mlx_bridge.cpp:745-749) and the
+  dense SwiGLU MLP (qwen35.rs:303-307) with the SwiGLU fused into the gate/up epilogue
 * :class:`Exl3SwitchGlu` -- ``Exl3SwitchGlu::new`` / ``forward`` (native/src/moe.rs:809-975)
 * :func:`decode_tiles`  -- the ``metal-decode`` codec op (exl3.metal:102-109)
 * :class:`Checkpoint`   -- ``checkpoint::inspect`` / ``TensorInfo`` (native/src/checkpoint.rs),
@@ -26,6 +28,8 @@ from typing import Optional, Sequence
 LIB_PATH = Path(__file__).resolve().parent / "libexl3_hip.so"
 
 __all__ = [
+    "Exl3Mlp",
+    "swiglu",
     "Checkpoint",
     "TensorInfo",
     "Codebook",
@@ -73,7 +77,11 @@ _SIGNATURES = {
     "exl3_linear_workspace_bytes": (_sz, [_vp, _i64]),
     "exl3_workspace_init": (_i32, [_vp, _sz, _vp]),
     "exl3_linear_forward": (_i32, [_vp, _vp, _i32, _i64, _vp, _i32, _vp, _sz, _vp]),
+    "exl3_group_workspace_bytes": (_sz, [_vp, _i32, _i64]),
     "exl3_group_forward": (_i32, [_vp, _i32, _vp, _i32, _i64, _vp, _vp, _sz, _vp]),
+    "exl3_swiglu": (_i32, [_vp, _vp, _vp, _i64, _vp]),
+    "exl3_mlp_workspace_bytes": (_sz, [_vp, _vp, _vp, _i64]),
+    "exl3_mlp_forward": (_i32, [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _sz, _vp]),
     "exl3_moe_create": (
         _i32,
         [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_vp)],
@@ -402,7 +410,9 @@ class Exl3Linear:
 
 
 class Exl3Group:
-    """Exl3Group (linear.rs:2285-2815): projections sharing x, one output each."""
+    """Exl3Group (linear.rs:2285-2815): up to 8 projections sharing x (same input
+    width, K and codebook), one output each, computed in one launch (rows <= 16)
+    or one prologue + one QMM launch."""
 
     def __init__(self, linears: Sequence[Exl3Linear]):
         if not linears:
@@ -412,27 +422,80 @@ class Exl3Group:
             if (lin.in_features, lin.k, lin.cb) != (first.in_features, first.k, first.cb):
                 raise Exl3Error(-1, "EXL3 group members need the same input width, K and codebook")
         self.linears = list(linears)
+        self._handles = (_vp * len(self.linears))(*[l.handle.value for l in self.linears])
         self._ws = _Workspace()
+
+    def workspace_bytes(self, rows: int) -> int:
+        return int(load_library().exl3_group_workspace_bytes(self._handles, len(self.linears), int(rows)))
 
     def forward(self, x):
         torch = _torch()
         x = _require_device(x, "x", (torch.float16, torch.bfloat16, torch.float32))
         n_in = self.linears[0].in_features
-        if x.shape[-1] != n_in:
-            raise Exl3Error(-1, f"invalid EXL3 linear input for {n_in} inputs")
+        if x.shape[-1] != n_in or x.numel() % n_in:
+            raise Exl3Error(-1, "invalid grouped EXL3 input")
         rows = x.numel() // n_in
+        if rows == 0:
+            raise Exl3Error(-1, "grouped EXL3 input cannot be empty")
         ys = [torch.empty(*x.shape[:-1], l.out_features, dtype=x.dtype, device=x.device) for l in self.linears]
-        need = max(l.workspace_bytes(rows) for l in self.linears)
-        ws = self._ws.get(need, x.device)
-        handles = (_vp * len(self.linears))(*[l.handle.value for l in self.linears])
+        ws = self._ws.get(self.workspace_bytes(rows), x.device)
         outs = (_vp * len(ys))(*[y.data_ptr() for y in ys])
         _check(
             load_library().exl3_group_forward(
-                handles, len(self.linears), _ptr(x), _dtype_code(x.dtype), rows, outs, _ptr(ws),
+                self._handles, len(self.linears), _ptr(x), _dtype_code(x.dtype), rows, outs, _ptr(ws),
                 ws.numel(), _stream_ptr(x.device),
             )
         )
         return ys
+
+    __call__ = forward
+
+
+def swiglu(gate, up):
+    """Array::swiglu (native/ffi/mlx_bridge.cpp:745-749): (g * sigmoid(g)) * u in
+    f16 arithmetic, for f16 device tensors of one shape."""
+    torch = _torch()
+    gate = _require_device(gate, "gate", (torch.float16,))
+    up = _require_device(up, "up", (torch.float16,))
+    if gate.shape != up.shape:
+        raise Exl3Error(-1, "SwiGLU operands differ in shape")
+    out = torch.empty_like(gate)
+    _check(load_library().exl3_swiglu(_ptr(gate), _ptr(up), _ptr(out), gate.numel(),
+                                      _stream_ptr(gate.device)))
+    return out
+
+
+class Exl3Mlp:
+    """The dense SwiGLU MLP of a decoder layer (qwen35.rs:303-307: an Exl3Group
+    of gate/up, Array::swiglu, the down Exl3Linear), with the SwiGLU and the
+    down projection's input prologue fused into the gate/up launch."""
+
+    def __init__(self, gate: Exl3Linear, up: Exl3Linear, down: Exl3Linear):
+        if (gate.in_features, gate.out_features, gate.k, gate.cb) != \
+                (up.in_features, up.out_features, up.k, up.cb):
+            raise Exl3Error(-1, "incompatible grouped projections")
+        if down.in_features != gate.out_features:
+            raise Exl3Error(-1, f"EXL3 MLP down projection expects {down.in_features} inputs, "
+                                f"gate/up give {gate.out_features}")
+        self.gate, self.up, self.down = gate, up, down
+        self._ws = _Workspace()
+
+    def workspace_bytes(self, rows: int) -> int:
+        return int(load_library().exl3_mlp_workspace_bytes(self.gate.handle, self.up.handle,
+                                                           self.down.handle, int(rows)))
+
+    def forward(self, x):
+        torch = _torch()
+        x = _require_device(x, "x", (torch.float16,))
+        if x.shape[-1] != self.gate.in_features or x.numel() == 0:
+            raise Exl3Error(-1, f"invalid EXL3 MLP input for {self.gate.in_features} inputs")
+        rows = x.numel() // self.gate.in_features
+        y = torch.empty(*x.shape[:-1], self.down.out_features, dtype=torch.float16, device=x.device)
+        ws = self._ws.get(self.workspace_bytes(rows), x.device)
+        _check(load_library().exl3_mlp_forward(self.gate.handle, self.up.handle, self.down.handle,
+                                               _ptr(x), rows, _ptr(y), _ptr(ws), ws.numel(),
+                                               _stream_ptr(x.device)))
+        return y
 
     __call__ = forward
 

@@ -127,88 +127,293 @@ static QmmShape choose_qmm_shape(int in, int out, int64_t rows) {
   return best;
 }
 
-// Workspace: [tile counters][QMV partials | QMM xhat, partials].  The counter
-// region has a fixed size, so one workspace serves QMV and QMM calls in any
-// order (every call leaves its counters at zero).
-static size_t linear_ws_bytes(const exl3_linear* h, int64_t rows) {
-  size_t counters = align_up(sizeof(uint32_t) * (size_t)std::max(h->out / 128, kTileCounters));
-  if (rows <= kQmvMaxRows)
-    return counters + align_up(sizeof(float) * (size_t)h->qmv_splits * rows * h->out);
-  const QmmShape sh = choose_qmm_shape(h->in, h->out, rows);
-  size_t partials = sh.splits > 1 ? sizeof(float) * (size_t)sh.splits * rows * h->out : 0;
-  return counters + align_up(sizeof(uint16_t) * (size_t)rows * h->in) + align_up(partials);
+// Workspace: the first kWorkspaceCounterBytes hold counters that are zero
+// between calls (every call leaves them zero, so one workspace serves every
+// entry point in any order): split-K counters from word 0, the SwiGLU pair
+// counters of a (gate, up) QMM from word kPairCounterBase.  The rest is
+// per-call scratch: QMV partials, or QMM xhat rows (one set per member) and
+// partials.
+static constexpr int kCounterWords = (int)(kWorkspaceCounterBytes / sizeof(uint32_t));
+static constexpr int kPairCounterBase = kCounterWords / 2;
+
+// A launch over 1..kMaxMembers projections sharing one input.
+struct Group {
+  const exl3_linear* parts[kMaxMembers];
+  int count, in, total_out, k, cb;
+};
+
+static int make_group(const exl3_linear* const* parts, int count, Group& g) {
+  if (!parts || count < 1) return fail(EXL3_EINVAL, "empty EXL3 group");
+  if (count > kMaxMembers)
+    return fail(EXL3_EUNSUPPORTED, "EXL3 groups of more than %d projections are not supported",
+                kMaxMembers);
+  int64_t total = 0;
+  for (int i = 0; i < count; ++i) {
+    if (!parts[i]) return fail(EXL3_EINVAL, "null EXL3 group member %d", i);
+    if (parts[i]->in != parts[0]->in || parts[i]->k != parts[0]->k ||
+        parts[i]->cb != parts[0]->cb)
+      return fail(EXL3_EINVAL, "EXL3 group members need the same input width, K and codebook");
+    g.parts[i] = parts[i];
+    total += parts[i]->out;
+  }
+  if (total > INT32_MAX || total / 128 > kPairCounterBase)
+    return fail(EXL3_EUNSUPPORTED, "EXL3 group too wide: %lld columns", (long long)total);
+  g.count = count;
+  g.in = parts[0]->in;
+  g.total_out = (int)total;
+  g.k = parts[0]->k;
+  g.cb = parts[0]->cb;
+  return EXL3_OK;
 }
 
-// ---------------------------------------------------------------------------
-// forward
-// ---------------------------------------------------------------------------
-static int linear_forward(const exl3_linear* h, const void* x, int x_type, int64_t rows, void* y,
-                          int y_type, void* ws, size_t ws_bytes, hipStream_t stream) {
-  if (!h) return fail(EXL3_EINVAL, "null EXL3 linear handle");
-  if (!x || !y) return fail(EXL3_EINVAL, "null activation pointer");
-  if (!valid_dtype(x_type) || !valid_dtype(y_type))
-    return fail(EXL3_EINVAL, "unsupported dtype codes %d -> %d", x_type, y_type);
-  if (rows < 1) return fail(EXL3_EINVAL, "EXL3 linear input cannot be empty");
-  if (rows > (int64_t)INT32_MAX / std::max(h->in, h->out))
-    return fail(EXL3_EINVAL, "EXL3 linear input too large: %lld rows", (long long)rows);
-  size_t need = linear_ws_bytes(h, rows);
-  if (!ws || ws_bytes < need)
-    return fail(EXL3_EINVAL, "workspace too small: %zu bytes given, %zu needed", ws_bytes, need);
-  uint32_t* counters = (uint32_t*)ws;
-  char* after =
-      (char*)ws + align_up(sizeof(uint32_t) * (size_t)std::max(h->out / 128, kTileCounters));
-  const int kidx = h->k - 1, cb = h->cb;
-
-  if (rows <= kQmvMaxRows) {
-    QmvParams p;
-    p.trellis = (const uint32_t*)h->trellis;
-    p.x = x;
-    p.suh = h->suh;
-    p.svh = h->svh;
-    p.bias = h->bias;
-    p.y = y;
-    p.partials = (float*)after;
-    p.counters = counters;
-    p.in = h->in;
-    p.out = h->out;
-    p.M = (int)rows;
-    p.splits = h->qmv_splits;
-    p.x_dtype = x_type;
-    p.y_dtype = y_type;
-    const int nb = h->in / 128;
-    int max_blocks = 0;
-    for (int s = 0; s < p.splits; ++s)
-      max_blocks = std::max(max_blocks, (s + 1) * nb / p.splits - s * nb / p.splits);
-    size_t lds = sizeof(uint16_t) * (size_t)rows * max_blocks * 128;
-    const int kwi = h->qmv_kw == 4 ? 2 : h->qmv_kw == 2 ? 1 : 0;
-    kQmv[kwi][kidx][cb](p, dim3(h->out / 128, p.splits), lds, stream);
-    return check_launch("EXL3 QMV launch");
+static void group_qmv_shape(const Group& g, int* splits, int* kw) {
+  if (g.count == 1) {
+    *splits = g.parts[0]->qmv_splits;
+    *kw = g.parts[0]->qmv_kw;
+  } else {
+    choose_qmv_shape(g.in, g.total_out, splits, kw);
   }
+}
 
-  uint16_t* xhat = (uint16_t*)after;
-  launch_prologue(x, x_type, h->suh, h->in, (int)rows, xhat, stream);
-  if (int rc = check_launch("EXL3 prologue launch")) return rc;
-  const QmmShape sh = choose_qmm_shape(h->in, h->out, rows);
-  QmmParams q;
-  q.trellis = (const uint32_t*)h->trellis;
-  q.xhat = xhat;
-  q.svh = h->svh;
-  q.bias = h->bias;
-  q.y = y;
-  q.partials = (float*)((char*)xhat + align_up(sizeof(uint16_t) * (size_t)rows * h->in));
+// Scratch bytes (after the counter region) of one group launch.
+static size_t group_scratch_bytes(const Group& g, int64_t rows) {
+  if (rows <= kQmvMaxRows) {
+    int splits, kw;
+    group_qmv_shape(g, &splits, &kw);
+    return align_up(sizeof(float) * (size_t)splits * rows * g.total_out);
+  }
+  const QmmShape sh = choose_qmm_shape(g.in, g.total_out, rows);
+  size_t partials = sh.splits > 1 ? sizeof(float) * (size_t)sh.splits * rows * g.total_out : 0;
+  return (size_t)g.count * align_up(sizeof(uint16_t) * (size_t)rows * g.in) + align_up(partials);
+}
+
+static int check_rows(const Group& g, int64_t rows) {
+  if (rows < 1) return fail(EXL3_EINVAL, "EXL3 linear input cannot be empty");
+  if (rows > (int64_t)INT32_MAX / std::max(g.in, g.total_out))
+    return fail(EXL3_EINVAL, "EXL3 linear input too large: %lld rows", (long long)rows);
+  return EXL3_OK;
+}
+
+static Member member_of(const exl3_linear* h, void* y, int cblk0) {
+  Member m;
+  m.trellis = (const uint32_t*)h->trellis;
+  m.suh = h->suh;
+  m.xhat = nullptr;
+  m.svh = h->svh;
+  m.bias = h->bias;
+  m.y = y;
+  m.out = h->out;
+  m.cblk0 = cblk0;
+  return m;
+}
+
+// One QMV launch (rows <= 16) over the group; `glu` for a (gate, up) pair.
+static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows,
+                         void* const* ys, int y_type, uint32_t* counters, char* scratch,
+                         const Glu& glu, hipStream_t stream) {
+  QmvParams p{};
+  int cblk0 = 0;
+  for (int i = 0; i < g.count; ++i) {
+    p.mem[i] = member_of(g.parts[i], ys[i], cblk0);
+    cblk0 += g.parts[i]->out / 128;
+  }
+  p.members = g.count;
+  p.x = x;
+  p.partials = (float*)scratch;
+  p.counters = counters;
+  p.in = g.in;
+  p.total_out = g.total_out;
+  p.M = (int)rows;
+  int kw;
+  group_qmv_shape(g, &p.splits, &kw);
+  p.x_dtype = x_type;
+  p.y_dtype = y_type;
+  p.glu = glu;
+  const int nb = g.in / 128;
+  int max_blocks = 0;
+  for (int s = 0; s < p.splits; ++s)
+    max_blocks = std::max(max_blocks, (s + 1) * nb / p.splits - s * nb / p.splits);
+  size_t lds = sizeof(uint16_t) * (size_t)rows * max_blocks * 128;
+  const int kwi = kw == 4 ? 2 : kw == 2 ? 1 : 0;
+  kQmv[kwi][g.k - 1][g.cb](p, dim3(g.total_out / 128, p.splits), lds, stream);
+  return check_launch("EXL3 QMV launch");
+}
+
+// Prologue (one launch for all members) and one QMM launch over the group.
+// xhats: per member, null to run the prologue into the scratch.
+static int run_group_qmm(const Group& g, const void* x, int x_type, int64_t rows,
+                         void* const* ys, int y_type, uint32_t* counters, char* scratch,
+                         const uint16_t* given_xhat, const Glu& glu, hipStream_t stream) {
+  const size_t xbytes = align_up(sizeof(uint16_t) * (size_t)rows * g.in);
+  QmmParams q{};
+  if (!given_xhat) {
+    PrologueParams pp{};
+    pp.x = x;
+    pp.x_dtype = x_type;
+    pp.in = g.in;
+    pp.rows = (int)rows;
+    for (int i = 0; i < g.count; ++i) {
+      pp.suh[i] = g.parts[i]->suh;
+      pp.xhat[i] = (uint16_t*)(scratch + i * xbytes);
+    }
+    launch_prologue(pp, g.count, stream);
+    if (int rc = check_launch("EXL3 prologue launch")) return rc;
+  }
+  int cblk0 = 0;
+  for (int i = 0; i < g.count; ++i) {
+    q.mem[i] = member_of(g.parts[i], ys[i], cblk0);
+    q.mem[i].xhat = given_xhat ? given_xhat : (const uint16_t*)(scratch + i * xbytes);
+    cblk0 += g.parts[i]->out / 128;
+  }
+  const QmmShape sh = choose_qmm_shape(g.in, g.total_out, rows);
+  q.members = g.count;
+  q.partials = (float*)(scratch + (given_xhat ? 0 : g.count * xbytes));
   q.counters = counters;
-  q.in = h->in;
-  q.out = h->out;
+  q.in = g.in;
+  q.total_out = g.total_out;
   q.M = (int)rows;
   q.y_dtype = y_type;
-  q.col_blocks = h->out / 128;
+  q.col_blocks = g.total_out / 128;
   q.mtiles = sh.mtiles;
   q.splits = sh.splits;
+  q.glu = glu;
   const int mbi = sh.mb == 4 ? 2 : sh.mb == 2 ? 1 : 0;
   const int64_t wgs = (int64_t)sh.mtiles * q.col_blocks * sh.splits;
   if (wgs > INT32_MAX) return fail(EXL3_EINVAL, "EXL3 QMM grid too large");
-  kQmm[mbi][kidx][cb](q, dim3((unsigned)wgs), stream);
+  kQmm[mbi][g.k - 1][g.cb](q, dim3((unsigned)wgs), stream);
   return check_launch("EXL3 QMM launch");
+}
+
+static int group_forward(const Group& g, const void* x, int x_type, int64_t rows,
+                         void* const* ys, int y_type, void* ws, size_t ws_bytes,
+                         hipStream_t stream) {
+  if (!x) return fail(EXL3_EINVAL, "null activation pointer");
+  for (int i = 0; i < g.count; ++i)
+    if (!ys[i]) return fail(EXL3_EINVAL, "null activation pointer");
+  if (!valid_dtype(x_type) || !valid_dtype(y_type))
+    return fail(EXL3_EINVAL, "unsupported dtype codes %d -> %d", x_type, y_type);
+  if (int rc = check_rows(g, rows)) return rc;
+  const size_t need = kWorkspaceCounterBytes + group_scratch_bytes(g, rows);
+  if (!ws || ws_bytes < need)
+    return fail(EXL3_EINVAL, "workspace too small: %zu bytes given, %zu needed", ws_bytes, need);
+  uint32_t* counters = (uint32_t*)ws;
+  char* scratch = (char*)ws + kWorkspaceCounterBytes;
+  const Glu none{};
+  if (rows <= kQmvMaxRows)
+    return run_group_qmv(g, x, x_type, rows, ys, y_type, counters, scratch, none, stream);
+  return run_group_qmm(g, x, x_type, rows, ys, y_type, counters, scratch, nullptr, none, stream);
+}
+
+// ---------------------------------------------------------------------------
+// SwiGLU MLP: y = down(swiglu(gate(x), up(x))), f16 activations.
+// rows <= 16: (gate, up) QMV with the SwiGLU edge -> act, then the down QMV
+// (its prologue fused as for any linear).  rows > 16: prologue of gate and up,
+// the (gate, up) QMM whose edge writes the down projection's xhat, then the
+// down QMM.  Rows are processed in chunks whose tile count fits the pair
+// counters.
+// ---------------------------------------------------------------------------
+static int mlp_check(const exl3_linear* gate, const exl3_linear* up, const exl3_linear* down) {
+  if (!gate || !up || !down) return fail(EXL3_EINVAL, "null EXL3 MLP projection");
+  if (gate->in != up->in || gate->out != up->out || gate->k != up->k || gate->cb != up->cb)
+    return fail(EXL3_EINVAL, "incompatible grouped projections");
+  if (down->in != gate->out)
+    return fail(EXL3_EINVAL, "EXL3 MLP down projection expects %d inputs, gate/up give %d",
+                down->in, gate->out);
+  return EXL3_OK;
+}
+
+// Rows per MLP chunk: the QMM pair counters hold mtiles * H/128 entries.
+static int64_t mlp_chunk_rows(const exl3_linear* gate) {
+  const int64_t tiles_per_mtile = gate->out / 128;
+  const int64_t mtiles = (kCounterWords - kPairCounterBase) / std::max<int64_t>(1, tiles_per_mtile);
+  return std::max<int64_t>(kQmvMaxRows + 1, mtiles * 64);  // 64-row tiles at the smallest
+}
+
+// Workspace of one MLP chunk of `rows` rows.
+static size_t mlp_chunk_ws(const Group& g, const exl3_linear* down, int64_t rows) {
+  const size_t act = align_up(sizeof(uint16_t) * (size_t)rows * g.parts[0]->out);
+  if (rows <= kQmvMaxRows) {
+    const size_t stage2 = align_up(sizeof(float) * (size_t)down->qmv_splits * rows * down->out);
+    return act + std::max(group_scratch_bytes(g, rows), stage2);
+  }
+  const QmmShape sh = choose_qmm_shape(down->in, down->out, rows);
+  const size_t stage2 =
+      sh.splits > 1 ? align_up(sizeof(float) * (size_t)sh.splits * rows * down->out) : 0;
+  // act (the down xhat) + gate and up outputs exchanged between workgroups
+  return 3 * act + std::max(group_scratch_bytes(g, rows), stage2);
+}
+
+static size_t mlp_ws_bytes(const exl3_linear* gate, const exl3_linear* up,
+                           const exl3_linear* down, int64_t rows) {
+  const exl3_linear* gu[2] = {gate, up};
+  Group g;
+  if (make_group(gu, 2, g)) return 0;
+  size_t need;
+  if (rows <= kQmvMaxRows) {
+    need = mlp_chunk_ws(g, down, rows);
+  } else {
+    // full chunks, and a last chunk that may fall to the QMV path
+    need = std::max(mlp_chunk_ws(g, down, std::min(rows, mlp_chunk_rows(gate))),
+                    mlp_chunk_ws(g, down, kQmvMaxRows));
+  }
+  return kWorkspaceCounterBytes + need;
+}
+
+static int mlp_forward(const exl3_linear* gate, const exl3_linear* up, const exl3_linear* down,
+                       const void* x, int x_type, int64_t rows, void* y, void* ws,
+                       size_t ws_bytes, hipStream_t stream) {
+  if (int rc = mlp_check(gate, up, down)) return rc;
+  if (!x || !y) return fail(EXL3_EINVAL, "null activation pointer");
+  if (x_type != EXL3_F16)
+    return fail(EXL3_EUNSUPPORTED, "the fused SwiGLU MLP takes f16 activations (dtype %d)",
+                x_type);
+  const exl3_linear* gu[2] = {gate, up};
+  Group g, d;
+  if (int rc = make_group(gu, 2, g)) return rc;
+  if (int rc = make_group(&down, 1, d)) return rc;
+  if (int rc = check_rows(g, rows)) return rc;
+  if (int rc = check_rows(d, rows)) return rc;
+  const size_t need = mlp_ws_bytes(gate, up, down, rows);
+  if (!ws || ws_bytes < need)
+    return fail(EXL3_EINVAL, "workspace too small: %zu bytes given, %zu needed", ws_bytes, need);
+  uint32_t* counters = (uint32_t*)ws;
+  const int64_t chunk = rows <= kQmvMaxRows ? rows : mlp_chunk_rows(gate);
+  const size_t H = (size_t)gate->out;
+  for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
+    const int64_t n = std::min(chunk, rows - r0);
+    const uint16_t* xr = (const uint16_t*)x + (size_t)r0 * gate->in;
+    uint16_t* yr = (uint16_t*)y + (size_t)r0 * down->out;
+    char* base = (char*)ws + kWorkspaceCounterBytes;
+    uint16_t* act = (uint16_t*)base;
+    const size_t act_bytes = align_up(sizeof(uint16_t) * (size_t)n * H);
+    Glu glu{};
+    glu.on = 1;
+    glu.out = act;
+    if (n <= kQmvMaxRows) {
+      // the pair counters of the QMV are its split counters (one per block pair)
+      void* gu_y[2] = {nullptr, nullptr};  // not written: the edge consumes the partials
+      if (int rc = run_group_qmv(g, xr, EXL3_F16, n, gu_y, EXL3_F16, counters,
+                                 base + act_bytes, glu, stream))
+        return rc;
+      void* dy[1] = {yr};
+      if (int rc = run_group_qmv(d, act, EXL3_F16, n, dy, EXL3_F16, counters, base + act_bytes,
+                                 Glu{}, stream))
+        return rc;
+    } else {
+      void* gu_y[2] = {base + act_bytes, base + 2 * act_bytes};
+      char* scratch = base + 3 * act_bytes;
+      glu.down_suh = down->suh;
+      glu.pair_counters = counters + kPairCounterBase;
+      if (int rc = run_group_qmm(g, xr, EXL3_F16, n, gu_y, EXL3_F16, counters, scratch, nullptr,
+                                 glu, stream))
+        return rc;
+      void* dy[1] = {yr};
+      if (int rc = run_group_qmm(d, nullptr, EXL3_F16, n, dy, EXL3_F16, counters, scratch, act,
+                                 Glu{}, stream))
+        return rc;
+    }
+  }
+  return EXL3_OK;
 }
 
 // ---------------------------------------------------------------------------
@@ -256,8 +461,21 @@ int32_t exl3_linear_in_features(const exl3_linear* h) { return h ? h->in : 0; }
 int32_t exl3_linear_out_features(const exl3_linear* h) { return h ? h->out : 0; }
 
 size_t exl3_linear_workspace_bytes(const exl3_linear* h, int64_t rows) {
-  if (!h || rows < 1) return 0;
-  return linear_ws_bytes(h, rows);
+  Group g;
+  if (!h || rows < 1 || make_group(&h, 1, g)) return 0;
+  return kWorkspaceCounterBytes + group_scratch_bytes(g, rows);
+}
+
+size_t exl3_group_workspace_bytes(const exl3_linear* const* parts, int32_t count, int64_t rows) {
+  Group g;
+  if (rows < 1 || make_group(parts, count, g)) return 0;
+  return kWorkspaceCounterBytes + group_scratch_bytes(g, rows);
+}
+
+size_t exl3_mlp_workspace_bytes(const exl3_linear* gate, const exl3_linear* up,
+                                const exl3_linear* down, int64_t rows) {
+  if (rows < 1 || mlp_check(gate, up, down)) return 0;
+  return mlp_ws_bytes(gate, up, down, rows);
 }
 
 int exl3_workspace_init(void* workspace, size_t bytes, void* stream) {
@@ -272,26 +490,37 @@ int exl3_workspace_init(void* workspace, size_t bytes, void* stream) {
 
 int exl3_linear_forward(const exl3_linear* h, const void* x, int32_t x_type, int64_t rows, void* y,
                         int32_t y_type, void* workspace, size_t workspace_bytes, void* stream) {
-  return linear_forward(h, x, x_type, rows, y, y_type, workspace, workspace_bytes,
-                        (hipStream_t)stream);
+  if (!h) return fail(EXL3_EINVAL, "null EXL3 linear handle");
+  Group g;
+  if (int rc = make_group(&h, 1, g)) return rc;
+  return group_forward(g, x, x_type, rows, &y, y_type, workspace, workspace_bytes,
+                       (hipStream_t)stream);
 }
 
 int exl3_group_forward(const exl3_linear* const* parts, int32_t count, const void* x,
                        int32_t x_type, int64_t rows, void* const* ys, void* workspace,
                        size_t workspace_bytes, void* stream) {
-  if (!parts || !ys || count < 1) return fail(EXL3_EINVAL, "empty EXL3 group");
-  for (int i = 0; i < count; ++i) {
-    if (!parts[i]) return fail(EXL3_EINVAL, "null EXL3 group member %d", i);
-    if (parts[i]->in != parts[0]->in || parts[i]->k != parts[0]->k ||
-        parts[i]->cb != parts[0]->cb)
-      return fail(EXL3_EINVAL, "EXL3 group members need the same input width, K and codebook");
-  }
-  for (int i = 0; i < count; ++i) {
-    int rc = linear_forward(parts[i], x, x_type, rows, ys[i], x_type, workspace, workspace_bytes,
-                            (hipStream_t)stream);
-    if (rc) return rc;
-  }
-  return EXL3_OK;
+  if (!ys) return fail(EXL3_EINVAL, "empty EXL3 group");
+  Group g;
+  if (int rc = make_group(parts, count, g)) return rc;
+  return group_forward(g, x, x_type, rows, ys, x_type, workspace, workspace_bytes,
+                       (hipStream_t)stream);
+}
+
+int exl3_mlp_forward(const exl3_linear* gate, const exl3_linear* up, const exl3_linear* down,
+                     const uint16_t* x, int64_t rows, uint16_t* y, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  return mlp_forward(gate, up, down, x, EXL3_F16, rows, y, workspace, workspace_bytes,
+                     (hipStream_t)stream);
+}
+
+int exl3_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t count,
+                void* stream) {
+  if (count < 0) return fail(EXL3_EINVAL, "negative element count");
+  if (count == 0) return EXL3_OK;
+  if (!gate || !up || !out) return fail(EXL3_EINVAL, "null SwiGLU buffer");
+  launch_swiglu(gate, up, out, count, (hipStream_t)stream);
+  return check_launch("SwiGLU launch");
 }
 
 int exl3_decode_tiles(const uint16_t* packed, int64_t tiles, int32_t k, int32_t cb,

@@ -17,13 +17,20 @@ typedef void (*QmvFn)(const QmvParams&, dim3, size_t, hipStream_t);
 typedef void (*QmmFn)(const QmmParams&, dim3, hipStream_t);
 typedef void (*DecodeFn)(const uint32_t*, int64_t, uint16_t*, uint16_t*, dim3, hipStream_t);
 
+// Every workspace starts with this many bytes of counters that are zero
+// between calls; each entry point's scratch follows them.
+constexpr size_t kWorkspaceCounterBytes = 65536;
+
 // [K-1][codebook]
 extern const QmvFn kQmv[3][8][3];  // [log2 KW]: 1, 2 or 4 K-parts per column pair
 extern const DecodeFn kDecode[8][3];
 extern const QmmFn kQmm[3][8][3];  // [log2 MB]: 64, 128 or 256 rows per workgroup
 
-void launch_prologue(const void* x, int x_dtype, const uint16_t* suh, int in, int rows,
-                     uint16_t* xhat, hipStream_t s);
+// xhat of `members` (suh, xhat) pairs of p in one launch.
+void launch_prologue(const PrologueParams& p, int members, hipStream_t s);
+// out[i] = swiglu(gate[i], up[i]) in f16 (Array::swiglu).
+void launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,
+                   hipStream_t s);
 void launch_fill_zero(uint32_t* p, size_t words, hipStream_t s);
 
 // Records the thread-local error message and returns `code`.

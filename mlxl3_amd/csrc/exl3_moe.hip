@@ -92,7 +92,7 @@ bool moe_layout(const exl3_moe* h, int64_t rows, MoeLayout& L) {
   L.ncounters = L.max_blocks * std::max(h->hidden, h->in) / 128;
   L.splits_gu = moe_splits(h, slots, L.block_rows, h->in, h->hidden / 128);
   L.splits_down = moe_splits(h, slots, L.block_rows, h->hidden, h->in / 128);
-  size_t off = 0;
+  size_t off = kWorkspaceCounterBytes;  // the shared counter region stays untouched
   auto take = [&](size_t bytes) {
     size_t at = off;
     off = moe_align(off + bytes);

@@ -5,31 +5,74 @@
 
 namespace exl3 {
 
-struct QmvParams {
+// A launch covers up to kMaxMembers projections that share one input (a
+// single linear is a group of one): their 128-column blocks are numbered
+// consecutively, member i owning global blocks [cblk0, cblk0 + out/128).
+constexpr int kMaxMembers = 8;
+
+struct Member {
   const uint32_t* trellis;  // [in/16][out/16][8K] u32
-  const void* x;            // [M][in] of x_dtype
-  const uint16_t* suh;      // [in] f16
+  const uint16_t* suh;      // [in] f16 (QMV: fused prologue)
+  const uint16_t* xhat;     // [M][in] f16 (QMM: prologue output of this member)
   const uint16_t* svh;      // [out] f16
   const uint16_t* bias;     // [out] f16 or null
   void* y;                  // [M][out] of y_dtype
-  float* partials;          // [splits][M][out]
-  uint32_t* counters;       // [out/128], zero between calls
-  int in, out, M, splits;
+  int out;                  // columns
+  int cblk0;                // first global column block
+};
+
+// SwiGLU edge of a (gate, up) group: members 0 and 1 have equal widths; the
+// last workgroup to finish a 128-column block of both computes
+// act = f16((g * sigmoid(g)) * u) for it and writes either act [M][out] or,
+// with down_suh set, the down projection's xhat [M][out]
+// (f16(H128(f16(act * down_suh)) / sqrt(128))).
+struct Glu {
+  int on;
+  uint16_t* out;             // act or down xhat, [M][out] f16
+  const uint16_t* down_suh;  // null: write act
+  uint32_t* pair_counters;   // QMM: [mtiles][out/128]; QMV uses the split counters
+};
+
+struct QmvParams {
+  Member mem[kMaxMembers];
+  int members;
+  const void* x;       // [M][in] of x_dtype
+  float* partials;     // [splits][M][total_out]
+  uint32_t* counters;  // [total_out/128] (GLU: [out/128]), zero between calls
+  int in, total_out, M, splits;
   int x_dtype, y_dtype;
+  Glu glu;
 };
 
 struct QmmParams {
-  const uint32_t* trellis;  // [in/16][out/16][8K] u32
-  const uint16_t* xhat;     // [M][in] f16 (prologue output)
-  const uint16_t* svh;      // [out]
-  const uint16_t* bias;     // [out] or null
-  void* y;                  // [M][out]
-  float* partials;          // [splits][M][out] f32 (splits > 1)
-  uint32_t* counters;       // [mtiles * col_blocks], zero between calls (splits > 1)
-  int in, out, M, y_dtype;
-  int col_blocks;           // out / 128
-  int mtiles;               // ceil(M / rows per workgroup)
-  int splits;               // K-ranges per output tile (global split-K)
+  Member mem[kMaxMembers];
+  int members;
+  float* partials;     // [splits][M][total_out] f32 (splits > 1)
+  uint32_t* counters;  // [mtiles * col_blocks], zero between calls (splits > 1)
+  int in, total_out, M, y_dtype;
+  int col_blocks;      // total_out / 128
+  int mtiles;          // ceil(M / rows per workgroup)
+  int splits;          // K-ranges per output tile (global split-K)
+  Glu glu;
 };
+
+struct PrologueParams {
+  const void* x;  // [rows][in] of x_dtype
+  int x_dtype, in, rows;
+  const uint16_t* suh[kMaxMembers];
+  uint16_t* xhat[kMaxMembers];  // [rows][in] f16 each
+};
+
+// The member owning global column block `cblk`, chosen with compile-time
+// indices only (a dynamically indexed parameter array would be copied to
+// scratch memory).
+template <typename P>
+__device__ __forceinline__ Member select_member(const P& p, int cblk) {
+  Member m = p.mem[0];
+#pragma unroll
+  for (int i = 1; i < kMaxMembers; ++i)
+    if (i < p.members && cblk >= p.mem[i].cblk0) m = p.mem[i];
+  return m;
+}
 
 }  // namespace exl3

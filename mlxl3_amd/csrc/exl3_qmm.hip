@@ -1,4 +1,6 @@
 // Instantiations of the prologue and the QMM over K x codebook x row tile.
+#include <algorithm>
+
 #include "exl3_launch.hpp"
 #include "exl3_qmm.hpp"
 
@@ -9,6 +11,31 @@ namespace exl3 {
   template __global__ void qmm_kernel<K, CB, 2>(QmmParams); \
   template __global__ void qmm_kernel<K, CB, 4>(QmmParams);
 EXL3_INSTANTIATE(EXL3_QMM_INST)
+
+// out = swiglu(gate, up) elementwise in f16, eight elements per thread
+// where the buffers allow 16-byte access.
+__global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict__ g,
+                                                     const uint16_t* __restrict__ u,
+                                                     uint16_t* __restrict__ o, int64_t n,
+                                                     int vec) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (vec) {
+    for (; i < n / 8; i += stride) {
+      const u32x4 gv = ((const u32x4*)g)[i], uv = ((const u32x4*)u)[i];
+      u32x4 ov;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = swiglu_f16(h2f((uint16_t)gv[j]), h2f((uint16_t)uv[j]));
+        const float hi = swiglu_f16(h2f((uint16_t)(gv[j] >> 16)), h2f((uint16_t)(uv[j] >> 16)));
+        ov[j] = (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
+      }
+      ((u32x4*)o)[i] = ov;
+    }
+    i = n / 8 * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  }
+  for (; i < n; i += stride) o[i] = f2h(swiglu_f16(h2f(g[i]), h2f(u[i])));
+}
 
 __global__ void fill_zero_kernel(uint32_t* p, size_t words) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -37,11 +64,18 @@ static void run_qmm4(const QmmParams& p, dim3 g, hipStream_t s) {
 
 const QmmFn kQmm[3][8][3] = {EXL3_TABLE(run_qmm1), EXL3_TABLE(run_qmm2), EXL3_TABLE(run_qmm4)};
 
-void launch_prologue(const void* x, int x_dtype, const uint16_t* suh, int in, int rows,
-                     uint16_t* xhat, hipStream_t s) {
-  const int64_t waves = (int64_t)rows * ((in / 128 + 7) / 8);
-  hipLaunchKernelGGL(prologue_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, x,
-                     x_dtype, suh, in, rows, xhat);
+void launch_prologue(const PrologueParams& p, int members, hipStream_t s) {
+  const int64_t waves = (int64_t)p.rows * ((p.in / 128 + 7) / 8);
+  hipLaunchKernelGGL(prologue_kernel, dim3((unsigned)((waves + 3) / 4), (unsigned)members),
+                     dim3(256), 0, s, p);
+}
+
+void launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,
+                   hipStream_t s) {
+  const int vec = ((((uintptr_t)gate | (uintptr_t)up | (uintptr_t)out) & 15) == 0) ? 1 : 0;
+  const int64_t work = vec ? n / 8 + 8 : n;
+  const unsigned blocks = (unsigned)std::min<int64_t>((work + 255) / 256, 4096);
+  hipLaunchKernelGGL(swiglu_kernel, dim3(blocks), dim3(256), 0, s, gate, up, out, n, vec);
 }
 
 void launch_fill_zero(uint32_t* p, size_t words, hipStream_t s) {

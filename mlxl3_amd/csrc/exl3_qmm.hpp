@@ -32,18 +32,24 @@
 namespace exl3 {
 
 
-// xhat = prologue(x) for all rows: one wave per (row, run of eight 128-input
-// blocks), pair layout with the run's loads in flight together.
-// grid ceil(rows * runs / 4), 256 threads.
-__global__ __launch_bounds__(256) void prologue_kernel(const void* __restrict__ x, int x_dtype,
-                                                       const uint16_t* __restrict__ suh, int in,
-                                                       int rows, uint16_t* __restrict__ xhat) {
-  const int nb = in >> 7, runs = (nb + 7) >> 3;
+// xhat[i] = prologue(x, suh[i]) for all rows of each member i (grid.y): one
+// wave per (row, run of eight 128-input blocks), pair layout with the run's
+// loads in flight together.  grid (ceil(rows * runs / 4), members), 256 threads.
+__global__ __launch_bounds__(256) void prologue_kernel(PrologueParams p) {
+  const int nb = p.in >> 7, runs = (nb + 7) >> 3;
   const int job = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int row = job / runs, run = job - row * runs;
-  if (row >= rows) return;  // uniform per wave
-  pair_prologue_row(x, x_dtype, (size_t)row * in, suh, 8 * run, min(8 * run + 8, nb),
-                    threadIdx.x & 63, xhat + (size_t)row * in);
+  if (row >= p.rows) return;  // uniform per wave
+  const uint16_t* suh = p.suh[0];
+  uint16_t* xhat = p.xhat[0];
+#pragma unroll
+  for (int i = 1; i < kMaxMembers; ++i)
+    if ((int)blockIdx.y == i) {
+      suh = p.suh[i];
+      xhat = p.xhat[i];
+    }
+  pair_prologue_row(p.x, p.x_dtype, (size_t)row * p.in, suh, 8 * run, min(8 * run + 8, nb),
+                    threadIdx.x & 63, xhat + (size_t)row * p.in);
 }
 
 template <int STRIDE>
@@ -92,7 +98,8 @@ __device__ __forceinline__ uint32_t out16(float v16, float b, bool has_bias, int
 // one 16-byte store (two for f32).  sv/bv: svh and bias of the lane's columns.
 __device__ __forceinline__ void qmm_finish_chunk(const u32x4 raw, const float (&sv)[8],
                                                  const float (&bv)[8], int lane, bool live,
-                                                 const QmmParams& p, size_t yoff) {
+                                                 const Member& mm, int y_dtype, bool coherent,
+                                                 size_t yoff) {
   float v[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -120,15 +127,15 @@ __device__ __forceinline__ void qmm_finish_chunk(const u32x4 raw, const float (&
 #pragma unroll
   for (int j = 0; j < 8; ++j) v[j] = round_f16(round_f16(v[j] * kHadScale) * sv[j]);
   if (!live) return;
-  const bool has_bias = p.bias != nullptr;
-  if (p.y_dtype == DT_F32) {
+  const bool has_bias = mm.bias != nullptr;
+  if (y_dtype == DT_F32) {
     float4v o0, o1;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       o0[j] = has_bias ? v[j] + bv[j] : v[j];
       o1[j] = has_bias ? v[j + 4] + bv[j + 4] : v[j + 4];
     }
-    float4v* yp = (float4v*)((float*)p.y + yoff);
+    float4v* yp = (float4v*)((float*)mm.y + yoff);
     yp[0] = o0;
     yp[1] = o1;
     return;
@@ -136,9 +143,16 @@ __device__ __forceinline__ void qmm_finish_chunk(const u32x4 raw, const float (&
   u32x4 o;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    o[i] = out16(v[2 * i], bv[2 * i], has_bias, p.y_dtype) |
-           (out16(v[2 * i + 1], bv[2 * i + 1], has_bias, p.y_dtype) << 16);
-  *(u32x4*)((uint16_t*)p.y + yoff) = o;
+    o[i] = out16(v[2 * i], bv[2 * i], has_bias, y_dtype) |
+           (out16(v[2 * i + 1], bv[2 * i + 1], has_bias, y_dtype) << 16);
+  if (coherent) {  // read by another workgroup of the same launch
+    uint32_t* yw = (uint32_t*)((uint16_t*)mm.y + yoff);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __hip_atomic_store(yw + i, o[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  *(u32x4*)((uint16_t*)mm.y + yoff) = o;
 }
 
 // Decode one step's 8 tiles of a producer (B[0] = previous lane's last word,
@@ -151,6 +165,38 @@ __device__ __forceinline__ void qmm_produce(const uint32_t (&B)[K + 1], u32x4* d
   dst[1 * 64 + lane] = __builtin_bit_cast(u32x4, decode_fragment<CB, K, 0, 1>(src));
   dst[2 * 64 + lane] = __builtin_bit_cast(u32x4, decode_fragment<CB, K, 1, 0>(src));
   dst[3 * 64 + lane] = __builtin_bit_cast(u32x4, decode_fragment<CB, K, 1, 1>(src));
+}
+
+// SwiGLU edge of a finished (gate, up) tile pair: rows [row0, row0 + 64*MB)
+// of columns [colb, colb + 128), one row per wave at a time in the pair
+// layout (lane holds columns colb + 2*lane, +1).  Kept out of line so that its
+// registers do not add to the main loop's.
+template <int MB>
+__device__ __attribute__((noinline)) void qmm_glu_rows(const uint16_t* gate_y,
+                                                       const uint16_t* up_y,
+                                                       const uint16_t* down_suh, uint16_t* out,
+                                                       int H, int M, int row0, int colb, int wave,
+                                                       int lane) {
+  const uint32_t* gy = (const uint32_t*)(gate_y + colb);
+  const uint32_t* uy = (const uint32_t*)(up_y + colb);
+  for (int rl = wave; rl < 64 * MB; rl += 8) {
+    const int row = row0 + rl;
+    if (row >= M) break;  // uniform per wave
+    const size_t w = (size_t)row * (H >> 1) + lane;
+    const uint32_t gp = __hip_atomic_load(gy + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t up = __hip_atomic_load(uy + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float a0 = swiglu_f16(h2f((uint16_t)gp), h2f((uint16_t)up));
+    const float a1 = swiglu_f16(h2f((uint16_t)(gp >> 16)), h2f((uint16_t)(up >> 16)));
+    uint32_t bits;
+    if (down_suh) {  // the down projection's prologue on this 128-block
+      const uint32_t s = ((const uint32_t*)(down_suh + colb))[lane];
+      bits = pair_h128_bits(round_f16(a0 * h2f((uint16_t)s)),
+                            round_f16(a1 * h2f((uint16_t)(s >> 16))), lane);
+    } else {
+      bits = (uint32_t)f2h(a0) | ((uint32_t)f2h(a1) << 16);
+    }
+    ((uint32_t*)(out + colb))[(size_t)row * (H >> 1) + lane] = bits;
+  }
 }
 
 template <int K, int CB, int MB>
@@ -169,7 +215,6 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int role = wave & 3;
-  const int TN = p.out >> 4;
 
   // Workgroup -> (row tile, column block, split).  Workgroups are dispatched
   // round-robin over the 8 XCDs; renumbering them so that each XCD takes a
@@ -182,7 +227,11 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
   const int per_tile = p.col_blocks * p.splits;
   const int mtile = lin / per_tile;
   const int rest = lin - mtile * per_tile;
-  const int cblk = rest % p.col_blocks, split = rest / p.col_blocks;
+  const int cblk = rest % p.col_blocks, split = rest / p.col_blocks;  // global column block
+  const Member mm = select_member(p, cblk);
+  const int cblk_l = cblk - mm.cblk0;  // column block inside the member
+  const int TN = mm.out >> 4;
+  const int TO = p.total_out;
   const int nq_all = p.in >> 6;
   const int qa = split * nq_all / p.splits, nq = (split + 1) * nq_all / p.splits - qa;
   const int qlast = nq - 1;
@@ -202,14 +251,14 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
     // ---- producer `role`: B tiles of output tiles 2*role, 2*role+1 and the
     // A rows of consumer `role` ----
     if (threadIdx.x < 128) {
-      s_svh[threadIdx.x] = h2f(p.svh[cblk * 128 + threadIdx.x]);
-      s_bias[threadIdx.x] = p.bias ? h2f(p.bias[cblk * 128 + threadIdx.x]) : 0.f;
+      s_svh[threadIdx.x] = h2f(mm.svh[cblk_l * 128 + threadIdx.x]);
+      s_bias[threadIdx.x] = mm.bias ? h2f(mm.bias[cblk_l * 128 + threadIdx.x]) : 0.f;
     }
     constexpr int PD = 4;  // trellis slices in flight
     const int hsel = (lane >> 3) & 1, j = lane & 7;
     const size_t qstride = (size_t)4 * TN * 8 * K;
-    const uint32_t* tp = p.trellis +
-                         ((size_t)(4 * qa + g) * TN + cblk * 8 + role * 2 + hsel) * (8 * K) +
+    const uint32_t* tp = mm.trellis +
+                         ((size_t)(4 * qa + g) * TN + cblk_l * 8 + role * 2 + hsel) * (8 * K) +
                          (size_t)j * K;
     const int prev_off = j == 0 ? 8 * K - 1 : -1;
     uint32_t sl[PD][K + 1];
@@ -222,7 +271,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
 #pragma unroll
     for (int i = 0; i < 2 * MB; ++i) {
       const int row = row_base + 8 * i + ar;
-      ap[i] = p.xhat + (size_t)(row < p.M ? row : 0) * p.in + (size_t)qa * 64 + ac * 8;
+      ap[i] = mm.xhat + (size_t)(row < p.M ? row : 0) * p.in + (size_t)qa * 64 + ac * 8;
     }
     // A rows of steps q+2 and q+3 in flight (register sets alternate by step)
     u32x4 areg[2][2 * MB];
@@ -355,7 +404,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
       });
     } else {
       // split-K: f32 partials out, through agent-scope relaxed atomics
-      float* part = p.partials + (size_t)split * p.M * p.out;
+      float* part = p.partials + (size_t)split * p.M * TO;
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -365,7 +414,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
 #pragma unroll
             for (int f = 0; f < 8; ++f) {
               const int c = colb + 32 * (f >> 1) + 16 * (n >> 3) + 8 * (f & 1) + (n & 7);
-              store_coherent(part + (size_t)row * p.out + c, acc[mb][f][r]);
+              store_coherent(part + (size_t)row * TO + c, acc[mb][f][r]);
             }
           }
         }
@@ -399,7 +448,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
       for (int j = 0; j < 16; j += 2) {
         float s0 = 0.f, s1 = 0.f;
         for (int s = 0; s < p.splits; ++s) {
-          const float* ps = p.partials + ((size_t)s * p.M + lrow) * p.out + colb + c0 + j;
+          const float* ps = p.partials + ((size_t)s * p.M + lrow) * TO + colb + c0 + j;
           s0 += load_coherent(ps);
           s1 += load_coherent(ps + 1);
         }
@@ -411,7 +460,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
 
   // ---- epilogue: all 8 waves finish 8*MB rows each, 4 rows per pass ----
   {
-    const int colb = cblk * 128;
+    const int colb = cblk_l * 128;
     const int chunk = lane & 15;
     float sv[8], bv[8];
 #pragma unroll
@@ -424,9 +473,27 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
       const int rl = wave * 8 * MB + 4 * i + (lane >> 4);
       const int row = mtile * 64 * MB + rl;
       const u32x4 raw = *(const u32x4*)(ys + rl * kYStride + 8 * chunk);
-      qmm_finish_chunk(raw, sv, bv, lane, row < p.M, p, (size_t)row * p.out + colb + 8 * chunk);
+      qmm_finish_chunk(raw, sv, bv, lane, row < p.M, mm, p.y_dtype, p.glu.on,
+                       (size_t)row * mm.out + colb + 8 * chunk);
     }
   }
+  if (!p.glu.on) return;
+
+  // ---- SwiGLU edge: the second of the (gate, up) tiles to finish computes
+  // act = swiglu(g, u) for the tile (and the down projection's prologue) ----
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  const int H = p.mem[0].out;
+  uint32_t* pc = p.glu.pair_counters + (size_t)mtile * (H >> 7) + cblk_l;
+  if (threadIdx.x == 0) {
+    uint32_t old = __hip_atomic_fetch_add(pc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (old == 1u);
+  }
+  __syncthreads();
+  if (!s_last) return;  // uniform across the workgroup
+  if (threadIdx.x == 0) __hip_atomic_store(pc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  qmm_glu_rows<MB>((const uint16_t*)p.mem[0].y, (const uint16_t*)p.mem[1].y, p.glu.down_suh,
+                   p.glu.out, H, p.M, mtile * 64 * MB, cblk_l * 128, wave, lane);
 }
 
 }  // namespace exl3

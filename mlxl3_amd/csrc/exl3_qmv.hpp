@@ -116,21 +116,43 @@ __device__ __forceinline__ void qmv_step(const uint32_t (&w)[K], int lane, half8
 
 // Epilogue for one row of a 128-column block held as (v0, v1) = columns
 // (lane, lane+64): f16(sum) -> staged H128 -> f16(*1/sqrt128) -> f16(*svh)
-// -> cast (+bias).
-__device__ __forceinline__ void finish_row128(float v0, float v1, int lane, int col0,
-                                              const uint16_t* __restrict__ svh,
-                                              const uint16_t* __restrict__ bias, void* y,
-                                              int y_dtype, size_t row_off) {
+// (finish_vals128), then cast (+bias) and store (finish_row128).
+__device__ __forceinline__ void finish_vals128(float& v0, float& v1, int lane, int col0,
+                                               const uint16_t* __restrict__ svh) {
   v0 = round_f16(v0);
   v1 = round_f16(v1);
   h128_wave<true>(v0, v1, lane);
   v0 = round_f16(v0 * kHadScale);
   v1 = round_f16(v1 * kHadScale);
+  v0 = round_f16(v0 * h2f(svh[col0 + lane]));
+  v1 = round_f16(v1 * h2f(svh[col0 + lane + 64]));
+}
+__device__ __forceinline__ void finish_row128(float v0, float v1, int lane, int col0,
+                                              const uint16_t* __restrict__ svh,
+                                              const uint16_t* __restrict__ bias, void* y,
+                                              int y_dtype, size_t row_off) {
+  finish_vals128(v0, v1, lane, col0, svh);
   int c0 = col0 + lane, c1 = col0 + lane + 64;
-  v0 = round_f16(v0 * h2f(svh[c0]));
-  v1 = round_f16(v1 * h2f(svh[c1]));
   store_out(y, y_dtype, row_off + c0, v0, bias, c0);
   store_out(y, y_dtype, row_off + c1, v1, bias, c1);
+}
+// f16 output value with the optional bias added in f16 (y + bias).
+__device__ __forceinline__ float with_bias_f16(float v16, const uint16_t* __restrict__ bias,
+                                               int col) {
+  return bias ? round_f16(v16 + h2f(bias[col])) : v16;
+}
+
+// SwiGLU of f16 operands in f16 arithmetic, the compiled MLX expression
+// (g * sigmoid(g)) * u of Array::swiglu (native/ffi/mlx_bridge.cpp:745-749),
+// with MLX's sigmoid y = 1 / (1 + exp(-|g|)), g < 0 ? 1 - y : y; every
+// operation rounds to f16 (exp is evaluated in f32 and rounded).
+__device__ __forceinline__ float sigmoid_f16(float g) {
+  const float e = round_f16(expf(-fabsf(g)));
+  const float y = round_f16(1.0f / round_f16(1.0f + e));
+  return g < 0.f ? round_f16(1.0f - y) : y;
+}
+__device__ __forceinline__ float swiglu_f16(float g, float u) {
+  return round_f16(round_f16(g * sigmoid_f16(g)) * u);
 }
 
 // Prologue for one row of one 128-input block, split into its loads and its
@@ -202,18 +224,10 @@ __device__ __forceinline__ PairIn pair_load(const void* x, int x_dtype, size_t o
   in.s = ((const uint32_t*)(suh + e0))[lane];
   return in;
 }
-// xhat bits of the lane's two elements, packed (element 2*lane low).
-__device__ __forceinline__ uint32_t pair_finish(const PairIn& in, int x_dtype, int lane) {
-  float a, b;
-  if (x_dtype == DT_F32) {
-    a = __builtin_bit_cast(float, in.x0);
-    b = __builtin_bit_cast(float, in.x1);
-  } else {
-    a = raw_act(in.x0 & 0xffffu, x_dtype);
-    b = raw_act(in.x0 >> 16, x_dtype);
-  }
-  float v0 = round_f16(round_f16(a) * h2f((uint16_t)in.s));
-  float v1 = round_f16(round_f16(b) * h2f((uint16_t)(in.s >> 16)));
+// Staged H128 of a 128-block in the pair layout (lane holds elements 2*lane,
+// 2*lane+1 as v0, v1), then f16(* 1/sqrt 128): the packed f16 bits (element
+// 2*lane low).
+__device__ __forceinline__ uint32_t pair_h128_bits(float v0, float v1, int lane) {
   {  // stride 1
     const float t = v0;
     v0 = t + v1;
@@ -235,6 +249,20 @@ __device__ __forceinline__ uint32_t pair_finish(const PairIn& in, int x_dtype, i
     }
   });
   return (uint32_t)f2h(v0 * kHadScale) | ((uint32_t)f2h(v1 * kHadScale) << 16);
+}
+// xhat bits of the lane's two elements, packed (element 2*lane low).
+__device__ __forceinline__ uint32_t pair_finish(const PairIn& in, int x_dtype, int lane) {
+  float a, b;
+  if (x_dtype == DT_F32) {
+    a = __builtin_bit_cast(float, in.x0);
+    b = __builtin_bit_cast(float, in.x1);
+  } else {
+    a = raw_act(in.x0 & 0xffffu, x_dtype);
+    b = raw_act(in.x0 >> 16, x_dtype);
+  }
+  const float v0 = round_f16(round_f16(a) * h2f((uint16_t)in.s));
+  const float v1 = round_f16(round_f16(b) * h2f((uint16_t)(in.s >> 16)));
+  return pair_h128_bits(v0, v1, lane);
 }
 
 // Prologue of 128-input blocks [b_begin, b_end) of a row by one wave in the
@@ -269,8 +297,10 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int pair = wave & 3, kpart = wave >> 2;
-  const int TN = p.out >> 4, NB = p.in >> 7;
-  const int cblk = blockIdx.x, split = blockIdx.y;
+  const int cblk = blockIdx.x, split = blockIdx.y;  // global column block
+  const Member mm = select_member(p, cblk);
+  const int cblk_l = cblk - mm.cblk0;  // column block inside the member
+  const int TN = mm.out >> 4, NB = p.in >> 7;
   const int b0 = split * NB / p.splits, b1 = (split + 1) * NB / p.splits;
   const int row0 = b0 * 128, nrows = (b1 - b0) * 128, nq_wg = nrows >> 6;
   const int q_lo = kpart * nq_wg / KW, q_hi = (kpart + 1) * nq_wg / KW;
@@ -292,15 +322,15 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   for (int t = 0; t < kPrologueEarly; ++t) {
     const int job = min(wave + t * 4 * KW, njobs - 1);  // clamped: always a valid job
     const int m = job / nb, b = job - m * nb;
-    first[t] = prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128, p.suh,
+    first[t] = prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128, mm.suh,
                              row0 + b * 128, lane);
   }
   __builtin_amdgcn_sched_barrier(0);
 
   const int g = lane >> 4, hsel = (lane >> 3) & 1, j = lane & 7;
-  const int tn0 = cblk * 8 + pair * 2;
+  const int tn0 = cblk_l * 8 + pair * 2;
   const size_t qstride = (size_t)4 * TN * 8 * K;
-  const uint32_t* tp = p.trellis +
+  const uint32_t* tp = mm.trellis +
                        ((size_t)((row0 >> 4) + 4 * q_lo + g) * TN + tn0 + hsel) * (8 * K) +
                        (size_t)j * K;
   constexpr int D = kQmvDepth<K>;
@@ -327,7 +357,7 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   for (int job = wave + kPrologueEarly * 4 * KW; job < njobs; job += 4 * KW) {
     const int m = job / nb, b = job - m * nb;
     const PrologueIn in = prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128,
-                                        p.suh, row0 + b * 128, lane);
+                                        mm.suh, row0 + b * 128, lane);
     float v0, v1;
     prologue_finish(in, p.x_dtype, lane, v0, v1);
     xs[m * nrows + b * 128 + lane] = (_Float16)v0;
@@ -392,15 +422,17 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   const bool writer = kpart == 0;
 
   // accumulator lane l: rows 4*(l/16)+r, column 16*(tn0 + n/8) + n%8 + 8*cg
+  // of the member; partials are laid out by global column
   const int n = lane & 15;
-  const int col = 16 * (tn0 + (n >> 3)) + (n & 7);
-  float* part = p.partials + (size_t)split * M * p.out;
+  const int col = 128 * cblk + 16 * (pair * 2 + (n >> 3)) + (n & 7);
+  const int TO = p.total_out;
+  float* part = p.partials + (size_t)split * M * TO;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     int m = 4 * g + r;
     if (writer && m < M) {
-      store_coherent(part + (size_t)m * p.out + col, acc0[r]);
-      store_coherent(part + (size_t)m * p.out + col + 8, acc1[r]);
+      store_coherent(part + (size_t)m * TO + col, acc0[r]);
+      store_coherent(part + (size_t)m * TO + col + 8, acc1[r]);
     }
   }
 
@@ -408,31 +440,67 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   // are exchanged only through agent-scope relaxed atomics (served at the
   // device coherence point, no L2 writeback); s_waitcnt + barrier order every
   // partial store of the workgroup before its counter increment.
-  if (p.splits > 1) {
+  // A SwiGLU group finishes a column block once both members' splits are in
+  // (one counter per block pair).
+  const int arrivals = p.glu.on ? 2 * p.splits : p.splits;
+  const int cidx = p.glu.on ? cblk_l : cblk;
+  if (arrivals > 1) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
-      uint32_t old = __hip_atomic_fetch_add(&p.counters[cblk], 1u, __ATOMIC_RELAXED,
+      uint32_t old = __hip_atomic_fetch_add(&p.counters[cidx], 1u, __ATOMIC_RELAXED,
                                             __HIP_MEMORY_SCOPE_AGENT);
-      s_last = (old == (uint32_t)(p.splits - 1));
+      s_last = (old == (uint32_t)(arrivals - 1));
     }
     __syncthreads();
     if (!s_last) return;  // uniform across the workgroup
     if (threadIdx.x == 0)
-      __hip_atomic_store(&p.counters[cblk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&p.counters[cidx], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
-  const int colb = cblk * 128;
-  for (int m = wave; m < M; m += 4 * KW) {
-    float v0 = 0.f, v1 = 0.f;
+  const int colb_l = cblk_l * 128;
+  auto sum_row = [&](int m, int colg, float& v0, float& v1) {
+    v0 = 0.f;
+    v1 = 0.f;
     for (int s = 0; s < p.splits; ++s) {
-      const float* ps = p.partials + ((size_t)s * M + m) * p.out + colb;
+      const float* ps = p.partials + ((size_t)s * M + m) * TO + colg;
       v0 += load_coherent(ps + lane);
       v1 += load_coherent(ps + lane + 64);
     }
-    finish_row128(v0, v1, lane, colb, p.svh, p.bias, p.y, p.y_dtype, (size_t)m * p.out);
+  };
+  if (!p.glu.on) {
+    for (int m = wave; m < M; m += 4 * KW) {
+      float v0, v1;
+      sum_row(m, cblk * 128, v0, v1);
+      finish_row128(v0, v1, lane, colb_l, mm.svh, mm.bias, mm.y, p.y_dtype, (size_t)m * mm.out);
+    }
+    return;
+  }
+  const Member& gm = p.mem[0];
+  const Member& um = p.mem[1];
+  const int H = gm.out;
+  for (int m = wave; m < M; m += 4 * KW) {
+    float g0, g1, u0, u1;
+    sum_row(m, (gm.cblk0 + cblk_l) * 128, g0, g1);
+    sum_row(m, (um.cblk0 + cblk_l) * 128, u0, u1);
+    finish_vals128(g0, g1, lane, colb_l, gm.svh);
+    finish_vals128(u0, u1, lane, colb_l, um.svh);
+    g0 = with_bias_f16(g0, gm.bias, colb_l + lane);
+    g1 = with_bias_f16(g1, gm.bias, colb_l + lane + 64);
+    u0 = with_bias_f16(u0, um.bias, colb_l + lane);
+    u1 = with_bias_f16(u1, um.bias, colb_l + lane + 64);
+    float a0 = swiglu_f16(g0, u0), a1 = swiglu_f16(g1, u1);
+    if (p.glu.down_suh) {  // the down projection's prologue on this 128-block
+      a0 = round_f16(a0 * h2f(p.glu.down_suh[colb_l + lane]));
+      a1 = round_f16(a1 * h2f(p.glu.down_suh[colb_l + lane + 64]));
+      h128_wave<true>(a0, a1, lane);
+      a0 = round_f16(a0 * kHadScale);
+      a1 = round_f16(a1 * kHadScale);
+    }
+    p.glu.out[(size_t)m * H + colb_l + lane] = f2h(a0);
+    p.glu.out[(size_t)m * H + colb_l + lane + 64] = f2h(a1);
   }
 }
 

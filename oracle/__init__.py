@@ -49,6 +49,8 @@ def lib():
         L.exl3o_bf16_to_f32.argtypes = [ctypes.c_uint16]
         L.exl3o_f32_to_bf16.restype = ctypes.c_uint16
         L.exl3o_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.exl3o_swiglu.restype = None
+        L.exl3o_swiglu.argtypes = [_u16p, _u16p, _u16p, ctypes.c_int64]
         L.exl3o_codeword.restype = ctypes.c_uint16
         L.exl3o_codeword.argtypes = [ctypes.c_uint16, ctypes.c_int]
         L.exl3o_codebook.restype = None
@@ -203,3 +205,23 @@ def moe_forward(x, selected, scores, gu_trellis, gu_suh, gu_svh, down_trellis, d
     if rc:
         raise ValueError(f"oracle MoE forward failed ({rc})")
     return y.view(np.float16)
+
+
+def swiglu(gate, up) -> np.ndarray:
+    """Array::swiglu (mlx_bridge.cpp:745-749) on f16 arrays of one shape."""
+    g = np.ascontiguousarray(np.asarray(gate, dtype=np.float16)).view(np.uint16)
+    u = np.ascontiguousarray(np.asarray(up, dtype=np.float16)).view(np.uint16)
+    assert g.shape == u.shape
+    out = np.empty_like(g)
+    lib().exl3o_swiglu(g.reshape(-1), u.reshape(-1), out.reshape(-1), g.size)
+    return out.view(np.float16)
+
+
+def mlp_forward(x, gate, up, down, mode: int = 1) -> np.ndarray:
+    """Dense SwiGLU MLP of a decoder layer (qwen35.rs:303-307): gate and up
+    projections of x (f16 outputs), swiglu, down projection.  gate/up/down:
+    (trellis, suh, svh, bias, k, cb) tuples."""
+    g = forward(x, *gate[:3], gate[4], gate[5], bias=gate[3], mode=mode)
+    u = forward(x, *up[:3], up[4], up[5], bias=up[3], mode=mode)
+    act = swiglu(g, u)
+    return forward(act, *down[:3], down[4], down[5], bias=down[3], mode=mode)

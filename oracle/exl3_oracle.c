@@ -535,3 +535,14 @@ int exl3o_moe_forward(const uint16_t* x, int64_t rows, int in, int hidden, int e
     }
     return err;
 }
+
+/* ---- dense SwiGLU: mlx_bridge.cpp:745-749 (MLX Sigmoid on float16) ---- */
+void exl3o_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float g = h2f(gate[i]), u = h2f(up[i]);
+        const float e = rh(expf(-fabsf(g)));
+        const float y = rh(1.0f / rh(1.0f + e));
+        const float s = g < 0.0f ? rh(1.0f - y) : y;
+        out[i] = f2h(rh(g * s) * u);
+    }
+}

@@ -85,6 +85,14 @@ int exl3o_moe_forward(const uint16_t* x, int64_t rows, int in, int hidden, int e
                       const uint16_t* down_svh, const uint32_t* selected,
                       const uint16_t* scores, uint16_t* y, int threads);
 
+/* ---- dense SwiGLU (Array::swiglu, native/ffi/mlx_bridge.cpp:745-749) ----
+ * out[i] = (g * sigmoid(g)) * u for f16 g, u in f16 arithmetic: the compiled
+ * MLX expression evaluated on float16 arrays (MLX 0.32.2, the version the
+ * engine pins), whose Sigmoid functor is y = 1 / (1 + exp(-|x|)),
+ * x < 0 ? 1 - y : y.  Every operation rounds to f16; exp is evaluated in f32
+ * (expf) and rounded. */
+void exl3o_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n);
+
 #ifdef __cplusplus
 }
 #endif

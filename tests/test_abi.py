@@ -166,3 +166,39 @@ def test_moe_create_workspace_and_forward_rejects():
         assert "workspace too small" in lib.exl3_last_error().decode()
     finally:
         lib.exl3_moe_destroy(h)
+
+
+def test_group_and_mlp_reject_before_launch():
+    lib = mlxl3_amd.load_library()
+    hs = [create(n_in=256, n_out=256)[1] for _ in range(9)]
+    d_bad = create(n_in=512, n_out=256)[1]
+    g_k = create(k=3, n_in=256, n_out=256)[1]
+    try:
+        parts = (ctypes.c_void_p * 9)(*[h.value for h in hs])
+        ys = (ctypes.c_void_p * 9)(*([FAKE] * 9))
+        assert lib.exl3_group_forward(parts, 9, FAKE, 9, 1, ys, FAKE, 1 << 20, None) == -4
+        assert "more than 8" in lib.exl3_last_error().decode()
+        assert lib.exl3_group_workspace_bytes(parts, 9, 1) == 0
+        assert lib.exl3_group_workspace_bytes(parts, 8, 1) > lib.exl3_group_workspace_bytes(parts, 1, 1)
+        assert lib.exl3_group_forward(parts, 0, FAKE, 9, 1, ys, FAKE, 1 << 20, None) == -1
+        # workspace sized for one member is too small for eight
+        small = lib.exl3_group_workspace_bytes(parts, 1, 4)
+        assert lib.exl3_group_forward(parts, 8, FAKE, 9, 4, ys, FAKE, small, None) == -1
+        assert "workspace too small" in lib.exl3_last_error().decode()
+        # MLP: gate/up must match, down.in == gate.out, f16 only
+        a, b = hs[0], hs[1]
+        assert lib.exl3_mlp_forward(a, g_k, b, FAKE, 1, FAKE, FAKE, 1 << 24, None) == -1
+        assert "incompatible grouped projections" in lib.exl3_last_error().decode()
+        assert lib.exl3_mlp_forward(a, b, d_bad, FAKE, 1, FAKE, FAKE, 1 << 24, None) == -1
+        assert "down projection expects 512 inputs" in lib.exl3_last_error().decode()
+        assert lib.exl3_mlp_workspace_bytes(a, b, d_bad, 1) == 0
+        need = lib.exl3_mlp_workspace_bytes(a, b, hs[2], 40)
+        assert need > 65536
+        assert lib.exl3_mlp_forward(a, b, hs[2], FAKE, 40, FAKE, FAKE, need - 1, None) == -1
+        assert "workspace too small" in lib.exl3_last_error().decode()
+        assert lib.exl3_mlp_forward(a, b, hs[2], FAKE, 0, FAKE, FAKE, need, None) == -1
+        assert lib.exl3_swiglu(FAKE, FAKE, FAKE, -1, None) == -1
+        assert lib.exl3_swiglu(None, None, None, 0, None) == 0
+    finally:
+        for h in hs + [d_bad, g_k]:
+            lib.exl3_linear_destroy(h)

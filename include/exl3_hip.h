@@ -149,6 +149,22 @@ int exl3_moe_forward(const exl3_moe* handle, const uint16_t* x, int64_t rows,
 int exl3_decode_tiles(const uint16_t* packed, int64_t tiles, int32_t k, int32_t cb,
                       uint16_t* states, uint16_t* values, void* stream);
 
+/* Codewords of arbitrary states, the `codebook` codec op (main.rs:301-307,
+ * decode_codeword codec.rs:52-71): values[i] = f16 bits of codeword(states[i]). */
+int exl3_codewords(const uint16_t* states, int64_t count, int32_t cb, uint16_t* values,
+                   void* stream);
+
+/* The reference's serial inner QMV without glue, the `metal-qmv` codec op
+ * (gpu.rs:1561-1593 with exl3_qmv, exl3.metal:118-142): y[n] =
+ * f16(sum_r x[r] * W[r][n]) for a packed trellis of rows x cols (both
+ * multiples of 16) in [rows/16][cols/16][16k] order, x f16[rows], y f16[cols];
+ * f32 accumulation.  Workspace: exl3_qmv_inner_workspace_bytes (the decoded
+ * tiles). */
+size_t exl3_qmv_inner_workspace_bytes(int32_t rows, int32_t cols);
+int exl3_qmv_inner(const uint16_t* packed, int32_t rows, int32_t cols, int32_t k, int32_t cb,
+                   const uint16_t* x, uint16_t* y, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
 /* ------------------------------------------------------------------------
  * Checkpoints (safetensors EXL3 model directories).
  *

@@ -19,6 +19,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libexl3_hip.so"
+CODEC = HERE / "exl3_codec"  # the codec JSON-lines driver (links LIB)
 SOURCES = ["exl3_api.hip", "exl3_qmv.hip", "exl3_qmm.hip", "exl3_moe.hip", "exl3_checkpoint.cpp"]
 ARCH = "gfx950"
 
@@ -79,8 +80,16 @@ def build(verbose: bool = True) -> Path:
         if res.returncode != 0:
             raise RuntimeError(f"link failed:\n{res.stderr}")
         shutil.copy2(tmp_lib, LIB)
+        # the codec driver: host code against the library just built
+        tmp_codec = Path(tmp) / CODEC.name
+        cmd = [hipcc(), "-O2", "-std=c++17", "-Wall", str(CSRC / "exl3_codec.cpp"), "-o",
+               str(tmp_codec), f"-L{HERE}", "-lexl3_hip", "-Wl,-rpath,$ORIGIN"]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"codec driver build failed:\n{res.stderr}")
+        shutil.copy2(tmp_codec, CODEC)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {CODEC}")
     return LIB
 
 

@@ -537,5 +537,40 @@ int exl3_decode_tiles(const uint16_t* packed, int64_t tiles, int32_t k, int32_t 
   return check_launch("EXL3 decode launch");
 }
 
+int exl3_codewords(const uint16_t* states, int64_t count, int32_t cb, uint16_t* values,
+                   void* stream) {
+  if (cb < 0 || cb > 2) return fail(EXL3_EINVAL, "invalid EXL3 codebook %d", cb);
+  if (count < 0) return fail(EXL3_EINVAL, "negative element count");
+  if (count == 0) return EXL3_OK;
+  if (!states || !values) return fail(EXL3_EINVAL, "null codeword buffer");
+  if ((count + 255) / 256 > INT32_MAX) return fail(EXL3_EINVAL, "too many states");
+  launch_codewords(states, count, cb, values, (hipStream_t)stream);
+  return check_launch("EXL3 codeword launch");
+}
+
+size_t exl3_qmv_inner_workspace_bytes(int32_t rows, int32_t cols) {
+  if (rows <= 0 || cols <= 0 || rows % 16 || cols % 16) return 0;
+  return align_up(sizeof(uint16_t) * (size_t)rows * cols);
+}
+
+int exl3_qmv_inner(const uint16_t* packed, int32_t rows, int32_t cols, int32_t k, int32_t cb,
+                   const uint16_t* x, uint16_t* y, void* workspace, size_t workspace_bytes,
+                   void* stream) {
+  if (k < 1 || k > 8) return fail(EXL3_EINVAL, "K must be in 1..=8, got %d", k);
+  if (cb < 0 || cb > 2) return fail(EXL3_EINVAL, "invalid EXL3 codebook %d", cb);
+  if (rows <= 0 || cols <= 0 || rows % 16 || cols % 16)
+    return fail(EXL3_EINVAL, "expected positive 16-aligned dimensions");
+  if (!packed || !x || !y) return fail(EXL3_EINVAL, "null QMV buffer");
+  const size_t need = exl3_qmv_inner_workspace_bytes(rows, cols);
+  if (!workspace || workspace_bytes < need)
+    return fail(EXL3_EINVAL, "workspace too small: %zu bytes given, %zu needed", workspace_bytes,
+                need);
+  const int64_t tiles = (int64_t)(rows / 16) * (cols / 16);
+  int rc = exl3_decode_tiles(packed, tiles, k, cb, nullptr, (uint16_t*)workspace, stream);
+  if (rc) return rc;
+  launch_qmv_inner((const uint16_t*)workspace, x, rows, cols, y, (hipStream_t)stream);
+  return check_launch("EXL3 inner QMV launch");
+}
+
 }  // extern "C"
 

@@ -1,0 +1,378 @@
+// exl3_codec: the reference engine's `codec` JSON-lines protocol
+// (codec_loop, native/src/main.rs:286-1360; request fields CodecRequest
+// main.rs:78-270) served by this library, so the reference's harnesses that
+// drive `mlxl3-rs codec` (e.g. docs/native-coverage/baselines/exl3/
+// check-metal-tiles.py.txt) can drive the HIP build instead.
+//
+// One request per input line, one response per output line:
+// {"data": ...} or {"error": "..."}.  Operations:
+//   pack, permutation                 host (codec.rs:73-100, :126-138)
+//   unpack, metal-decode              GPU tile decode (exl3_decode_tiles)
+//   codebook                          GPU codewords (exl3_codewords)
+//   metal-qmv                         GPU inner QMV (exl3_qmv_inner)
+//   metal-swiglu                      GPU SwiGLU (exl3_swiglu)
+//   mlx-linear, mlx-group             GPU Exl3Linear / Exl3Group forward
+// Any other op answers "unknown or unavailable codec operation <op>", as a
+// reference build without the feature does.  The GPU is initialised on the
+// first request that needs it.
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <iostream>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "../../include/exl3_hip.h"
+#include "exl3_json.hpp"
+
+namespace {
+
+using exl3::json::Value;
+
+struct Failure {
+  std::string msg;
+};
+[[noreturn]] void bail(const std::string& msg) { throw Failure{msg}; }
+
+// ---- request (CodecRequest: serde defaults, unknown fields ignored) ---------
+struct Request {
+  std::string op;
+  uint64_t k = 4;  // default_k, main.rs:273-275
+  uint64_t mode = 0;
+  uint64_t cols = 0;
+  std::vector<uint16_t> data, x, suh, svh;
+  std::vector<uint64_t> widths;
+};
+
+std::vector<uint16_t> u16_array(const Value* v, const char* field) {
+  std::vector<uint16_t> out;
+  if (!v) return out;
+  if (!v->is_array()) bail(std::string("invalid codec request: ") + field + " must be an array");
+  out.reserve(v->arr.size());
+  for (const Value& e : v->arr) {
+    if (!e.is_number() || !e.is_uint || e.u > 0xFFFF)
+      bail(std::string("invalid codec request: ") + field + " must hold u16 values");
+    out.push_back((uint16_t)e.u);
+  }
+  return out;
+}
+
+uint64_t uint_field(const Value* v, const char* field, uint64_t dflt, uint64_t max) {
+  if (!v) return dflt;
+  if (!v->is_number() || !v->is_uint || v->u > max)
+    bail(std::string("invalid codec request: ") + field + " must be an unsigned integer");
+  return v->u;
+}
+
+Request parse_request(const std::string& line) {
+  Value v;
+  std::string why;
+  if (!exl3::json::parse(line.data(), line.size(), v, why)) bail("invalid codec request: " + why);
+  if (!v.is_object()) bail("invalid codec request: expected an object");
+  Request r;
+  const Value* op = v.find("op");
+  if (!op || !op->is_string()) bail("invalid codec request: missing field `op`");
+  r.op = op->str;
+  r.k = uint_field(v.find("k"), "k", 4, UINT64_MAX);
+  r.mode = uint_field(v.find("mode"), "mode", 0, UINT32_MAX);
+  r.cols = uint_field(v.find("cols"), "cols", 0, UINT64_MAX);
+  r.data = u16_array(v.find("data"), "data");
+  r.x = u16_array(v.find("x"), "x");
+  r.suh = u16_array(v.find("suh"), "suh");
+  r.svh = u16_array(v.find("svh"), "svh");
+  if (const Value* w = v.find("widths")) {
+    if (!w->is_array()) bail("invalid codec request: widths must be an array");
+    for (const Value& e : w->arr) r.widths.push_back(uint_field(&e, "widths", 0, UINT64_MAX));
+  }
+  return r;
+}
+
+// ---- JSON output ------------------------------------------------------------
+std::string json_string(const std::string& s) {
+  std::string o = "\"";
+  for (unsigned char c : s) {
+    if (c == '"' || c == '\\') {
+      o += '\\';
+      o += (char)c;
+    } else if (c < 0x20) {
+      char buf[8];
+      snprintf(buf, sizeof buf, "\\u%04x", c);
+      o += buf;
+    } else {
+      o += (char)c;
+    }
+  }
+  return o + "\"";
+}
+template <typename T>
+std::string json_list(const std::vector<T>& v) {
+  std::string o = "[";
+  for (size_t i = 0; i < v.size(); ++i) {
+    if (i) o += ',';
+    o += std::to_string(v[i]);
+  }
+  return o + "]";
+}
+
+// ---- host codec (the on-disk format) -----------------------------------------
+void check_k(uint64_t k) {
+  if (k < 1 || k > 8) bail("K must be in 1..=8, got " + std::to_string(k));
+}
+
+// pack, codec.rs:73-100: output word `logical` of a tile (stored at
+// logical ^ 1) gathers 16 stream bits, most significant first; stream bit sb
+// of span logical/k is bit k-1-sb%k of state span*16 + sb/k.
+std::vector<uint16_t> pack(const std::vector<uint16_t>& states, int k) {
+  std::vector<uint16_t> out(states.size() / 256 * 16 * k);
+  for (size_t t = 0; t < states.size() / 256; ++t) {
+    const uint16_t* in = &states[t * 256];
+    uint16_t* o = &out[t * 16 * k];
+    for (int logical = 0; logical < 16 * k; ++logical) {
+      uint32_t word = 0;
+      const int span = logical / k;
+      for (int bit = 0; bit < 16; ++bit) {
+        const int sb = (logical % k) * 16 + bit;
+        word = (word << 1) | ((in[span * 16 + sb / k] >> (k - 1 - sb % k)) & 1u);
+      }
+      o[logical ^ 1] = (uint16_t)word;
+    }
+  }
+  return out;
+}
+
+// permutation, codec.rs:126-138: stored index 8*lane + 4*cg + ri holds tile
+// element (row {r0, r0+1, r0+8, r0+9}[ri], column lane/4 + 8*cg), r0 = 2*(lane%4).
+std::vector<uint64_t> permutation() {
+  std::vector<uint64_t> p(256);
+  for (int lane = 0; lane < 32; ++lane) {
+    const int r0 = 2 * (lane % 4), c = lane / 4;
+    const int rows[4] = {r0, r0 + 1, r0 + 8, r0 + 9};
+    for (int cg = 0; cg < 2; ++cg)
+      for (int ri = 0; ri < 4; ++ri) p[lane * 8 + cg * 4 + ri] = rows[ri] * 16 + c + 8 * cg;
+  }
+  return p;
+}
+
+// ---- device plumbing -----------------------------------------------------------
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) bail(std::string(what) + ": " + hipGetErrorString(e));
+}
+void lib_check(int rc) {
+  if (rc != EXL3_OK) bail(exl3_last_error());
+}
+
+struct DeviceBuffer {
+  void* p = nullptr;
+  size_t bytes = 0;
+  explicit DeviceBuffer(size_t n) : bytes(n) {
+    hip_check(hipMalloc(&p, n ? n : 16), "hipMalloc");
+  }
+  template <typename T>
+  DeviceBuffer(const std::vector<T>& v) : DeviceBuffer(v.size() * sizeof(T)) {
+    if (!v.empty()) hip_check(hipMemcpy(p, v.data(), bytes, hipMemcpyHostToDevice), "hipMemcpy");
+  }
+  ~DeviceBuffer() { (void)hipFree(p); }
+  DeviceBuffer(const DeviceBuffer&) = delete;
+  DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+  template <typename T>
+  std::vector<T> read(size_t n) const {
+    std::vector<T> v(n);
+    hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    if (n) hip_check(hipMemcpy(v.data(), p, n * sizeof(T), hipMemcpyDeviceToHost), "hipMemcpy");
+    return v;
+  }
+  template <typename T>
+  T* as() const {
+    return (T*)p;
+  }
+};
+
+// workspaces come from *_workspace_bytes (multiples of 256 bytes)
+void zero_workspace(DeviceBuffer& ws) {
+  lib_check(exl3_workspace_init(ws.p, ws.bytes / 4 * 4, nullptr));
+}
+
+// states and values of whole tiles (gpu.rs:1498-1521 / metal-decode)
+void decode(const std::vector<uint16_t>& packed, int k, int cb, std::vector<uint16_t>* states,
+            std::vector<uint16_t>* values) {
+  const int64_t tiles = (int64_t)(packed.size() / (16 * k));
+  DeviceBuffer in(packed), st(tiles * 256 * 2), val(tiles * 256 * 2);
+  lib_check(exl3_decode_tiles(in.as<uint16_t>(), tiles, k, cb, states ? st.as<uint16_t>() : nullptr,
+                              val.as<uint16_t>(), nullptr));
+  if (states) *states = st.read<uint16_t>(tiles * 256);
+  if (values) *values = val.read<uint16_t>(tiles * 256);
+}
+
+// ---- operations ------------------------------------------------------------
+std::string run(const Request& r) {
+  if (r.mode > 2) bail("invalid EXL3 codebook " + std::to_string(r.mode));
+  const int cb = (int)r.mode;
+  if (r.op == "pack") {
+    check_k(r.k);
+    if (r.data.size() % 256) bail("encoded length must be a multiple of 256");
+    return json_list(pack(r.data, (int)r.k));
+  }
+  if (r.op == "unpack") {
+    check_k(r.k);
+    if (r.data.size() % (16 * r.k)) bail("packed length is not a whole tile");
+    std::vector<uint16_t> states;
+    if (!r.data.empty()) decode(r.data, (int)r.k, cb, &states, nullptr);
+    return json_list(states);
+  }
+  if (r.op == "codebook") {
+    std::vector<uint16_t> values;
+    if (!r.data.empty()) {
+      DeviceBuffer in(r.data), out(r.data.size() * 2);
+      lib_check(exl3_codewords(in.as<uint16_t>(), (int64_t)r.data.size(), cb, out.as<uint16_t>(),
+                               nullptr));
+      values = out.read<uint16_t>(r.data.size());
+    }
+    return json_list(values);
+  }
+  if (r.op == "permutation") return json_list(permutation());
+  if (r.op == "metal-decode") {
+    check_k(r.k);
+    if (r.data.size() % (16 * r.k)) bail("expected whole packed tiles");
+    std::vector<uint16_t> states, values;
+    if (!r.data.empty()) decode(r.data, (int)r.k, cb, &states, &values);
+    return "{\"states\":" + json_list(states) + ",\"values\":" + json_list(values) + "}";
+  }
+  if (r.op == "metal-qmv") {
+    check_k(r.k);
+    const uint64_t rows = r.x.size(), cols = r.cols;
+    if (!(rows > 0 && cols > 0 && rows % 16 == 0 && cols % 16 == 0))
+      bail("expected positive 16-aligned dimensions");
+    if (rows > INT32_MAX || cols > INT32_MAX || r.data.size() != rows / 16 * (cols / 16) * 16 * r.k)
+      bail("invalid trellis size or Metal index overflow");
+    DeviceBuffer packed(r.data), x(r.x), y(cols * 2);
+    const size_t wb = exl3_qmv_inner_workspace_bytes((int)rows, (int)cols);
+    DeviceBuffer ws(wb);
+    lib_check(exl3_qmv_inner(packed.as<uint16_t>(), (int)rows, (int)cols, (int)r.k, cb,
+                             x.as<uint16_t>(), y.as<uint16_t>(), ws.p, wb, nullptr));
+    return json_list(y.read<uint16_t>(cols));
+  }
+  if (r.op == "metal-swiglu") {
+    if (r.x.empty() || r.x.size() != r.data.size()) bail("invalid SwiGLU input extents");
+    DeviceBuffer g(r.x), u(r.data), o(r.x.size() * 2);
+    lib_check(exl3_swiglu(g.as<uint16_t>(), u.as<uint16_t>(), o.as<uint16_t>(),
+                          (int64_t)r.x.size(), nullptr));
+    return json_list(o.read<uint16_t>(r.x.size()));
+  }
+  if (r.op == "mlx-linear") {  // main.rs:310-334
+    check_k(r.k);
+    const uint64_t rows = r.suh.size();
+    if (!(rows > 0 && r.x.size() % rows == 0)) bail("invalid linear input rows");
+    const uint64_t m = r.x.size() / rows, cols = r.cols;
+    if (rows > INT32_MAX || cols > INT32_MAX || m > INT32_MAX) bail("out of range integral type conversion attempted");
+    if (r.data.size() != rows / 16 * (cols / 16) * 16 * r.k || rows % 16 || cols % 16)
+      bail("invalid trellis shape");
+    if (r.svh.size() != cols) bail("EXL3 scales have wrong dimensions");
+    DeviceBuffer tr(r.data), su(r.suh), sv(r.svh), x(r.x), y(m * cols * 2);
+    exl3_linear* h = nullptr;
+    lib_check(exl3_linear_create(tr.as<uint16_t>(), (int)rows, (int)cols, (int)r.k, cb,
+                                 su.as<uint16_t>(), sv.as<uint16_t>(), nullptr, &h));
+    struct Guard {
+      exl3_linear* h;
+      ~Guard() { exl3_linear_destroy(h); }
+    } guard{h};
+    if (m == 0) bail("EXL3 linear input cannot be empty");
+    const size_t wb = exl3_linear_workspace_bytes(h, (int64_t)m);
+    DeviceBuffer ws(wb);
+    zero_workspace(ws);
+    lib_check(exl3_linear_forward(h, x.p, EXL3_F16, (int64_t)m, y.p, EXL3_F16, ws.p, wb, nullptr));
+    return json_list(y.read<uint16_t>(m * cols));
+  }
+  if (r.op == "mlx-group") {  // main.rs:336-426
+    check_k(r.k);
+    if (r.widths.empty()) bail("missing group widths");
+    if (r.suh.size() % r.widths.size()) bail("invalid grouped input scales");
+    const uint64_t rows = r.suh.size() / r.widths.size();
+    if (!(rows > 0 && rows % 128 == 0 && r.x.size() % rows == 0)) bail("invalid grouped input size");
+    const uint64_t m = r.x.size() / rows;
+    if (!(r.widths.size() >= 2 && r.k != 7)) bail("unsupported group");
+    if (r.widths.size() > 8) bail("EXL3 groups of more than 8 projections are not supported");
+    if (rows > INT32_MAX || m > INT32_MAX) bail("out of range integral type conversion attempted");
+    uint64_t data_off = 0, scale_off = 0;
+    std::vector<exl3_linear*> parts;
+    std::vector<DeviceBuffer*> bufs;
+    struct Cleanup {
+      std::vector<exl3_linear*>& parts;
+      std::vector<DeviceBuffer*>& bufs;
+      ~Cleanup() {
+        for (auto* h : parts) exl3_linear_destroy(h);
+        for (auto* b : bufs) delete b;
+      }
+    } cleanup{parts, bufs};
+    for (size_t i = 0; i < r.widths.size(); ++i) {
+      const uint64_t width = r.widths[i];
+      if (!(width > 0 && width % 128 == 0)) bail("invalid group width");
+      const uint64_t words = rows / 16 * (width / 16) * 16 * r.k;
+      if (data_off + words > r.data.size()) bail("truncated grouped trellis");
+      if (scale_off + width > r.svh.size()) bail("truncated grouped scales");
+      auto* tr = new DeviceBuffer(std::vector<uint16_t>(r.data.begin() + data_off,
+                                                        r.data.begin() + data_off + words));
+      bufs.push_back(tr);
+      auto* su = new DeviceBuffer(std::vector<uint16_t>(r.suh.begin() + i * rows,
+                                                        r.suh.begin() + (i + 1) * rows));
+      bufs.push_back(su);
+      auto* sv = new DeviceBuffer(std::vector<uint16_t>(r.svh.begin() + scale_off,
+                                                        r.svh.begin() + scale_off + width));
+      bufs.push_back(sv);
+      exl3_linear* h = nullptr;
+      lib_check(exl3_linear_create(tr->as<uint16_t>(), (int)rows, (int)width, (int)r.k, cb,
+                                   su->as<uint16_t>(), sv->as<uint16_t>(), nullptr, &h));
+      parts.push_back(h);
+      data_off += words;
+      scale_off += width;
+    }
+    if (data_off != r.data.size() || scale_off != r.svh.size()) bail("extra grouped data");
+    DeviceBuffer x(r.x);
+    std::vector<DeviceBuffer*> ys;
+    std::vector<void*> yp;
+    for (uint64_t w : r.widths) {
+      ys.push_back(new DeviceBuffer(m * w * 2));
+      bufs.push_back(ys.back());
+      yp.push_back(ys.back()->p);
+    }
+    if (m == 0) bail("grouped EXL3 input cannot be empty");
+    const size_t wb = exl3_group_workspace_bytes(parts.data(), (int)parts.size(), (int64_t)m);
+    DeviceBuffer ws(wb);
+    zero_workspace(ws);
+    lib_check(exl3_group_forward(parts.data(), (int)parts.size(), x.p, EXL3_F16, (int64_t)m,
+                                 yp.data(), ws.p, wb, nullptr));
+    std::string out = "[";
+    for (size_t i = 0; i < ys.size(); ++i) {
+      if (i) out += ',';
+      out += json_list(ys[i]->read<uint16_t>(m * r.widths[i]));
+    }
+    return out + "]";
+  }
+  bail("unknown or unavailable codec operation " + r.op);
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  // `exl3_codec` or `exl3_codec codec` (the reference's subcommand form)
+  if (argc > 2 || (argc == 2 && std::strcmp(argv[1], "codec") != 0)) {
+    std::fprintf(stderr, "usage: %s [codec] < requests.jsonl\n", argv[0]);
+    return 2;
+  }
+  std::ios::sync_with_stdio(false);
+  std::string line;
+  while (std::getline(std::cin, line)) {
+    std::string out;
+    try {
+      out = "{\"data\":" + run(parse_request(line)) + "}";
+    } catch (const Failure& f) {
+      out = "{\"error\":" + json_string(f.msg) + "}";
+    } catch (const std::bad_alloc&) {
+      out = "{\"error\":\"out of host memory\"}";
+    }
+    std::cout << out << '\n' << std::flush;
+  }
+  return 0;
+}

@@ -28,6 +28,11 @@ extern const QmmFn kQmm[3][8][3];  // [log2 MB]: 64, 128 or 256 rows per workgro
 
 // xhat of `members` (suh, xhat) pairs of p in one launch.
 void launch_prologue(const PrologueParams& p, int members, hipStream_t s);
+// values[i] = codeword(states[i], cb).
+void launch_codewords(const uint16_t* states, int64_t n, int cb, uint16_t* values, hipStream_t s);
+// y = f16(x . W) over decoded tiles (no glue).
+void launch_qmv_inner(const uint16_t* values, const uint16_t* x, int rows, int cols, uint16_t* y,
+                      hipStream_t s);
 // out[i] = swiglu(gate[i], up[i]) in f16 (Array::swiglu).
 void launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,
                    hipStream_t s);

@@ -13,6 +13,42 @@ namespace exl3 {
                                                       uint16_t*);
 EXL3_INSTANTIATE(EXL3_QMV_INST)
 EXL3_INSTANTIATE(EXL3_DEC_INST)
+template __global__ void codewords_kernel<0>(const uint16_t*, int64_t, uint16_t*);
+template __global__ void codewords_kernel<1>(const uint16_t*, int64_t, uint16_t*);
+template __global__ void codewords_kernel<2>(const uint16_t*, int64_t, uint16_t*);
+
+// Inner product of a decoded trellis without glue (the reference's serial
+// exl3_qmv, exl3.metal:118-142): y[n] = f16(sum_r x[r] * W[r][n]), W read from
+// the decoded tiles `values` ([tile][256] in stored order) through the tile
+// permutation (codec.rs:126-138: stored index 8*lane + 4*cg + ri holds row
+// {r0, r0+1, r0+8, r0+9}[ri], column lane/4 + 8*cg, r0 = 2*(lane%4)).  One
+// wave per column: lanes take rows lane, lane+64, ... in f32 and meet in a
+// fixed butterfly order.
+__global__ __launch_bounds__(256) void qmv_inner_kernel(const uint16_t* __restrict__ values,
+                                                        const uint16_t* __restrict__ x, int rows,
+                                                        int cols, uint16_t* __restrict__ y) {
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (n >= cols) return;  // uniform per wave
+  const int tn = n >> 4, c = n & 15;
+  const int cg = c >> 3, c0 = c & 7;
+  float acc = 0.f;
+  for (int r = lane; r < rows; r += 64) {
+    const int rr = r & 15;
+    const int ri = (rr & 1) | ((rr >> 3) << 1), r0 = rr & 6;
+    const int t = 8 * (4 * c0 + (r0 >> 1)) + 4 * cg + ri;
+    const int64_t tile = (int64_t)(r >> 4) * (cols >> 4) + tn;
+    acc = fmaf(h2f(x[r]), h2f(values[tile * 256 + t]), acc);
+  }
+  acc += xor_lanes<1>(acc);
+  acc += xor_lanes<2>(acc);
+  acc += xor_lanes<4>(acc);
+  acc += xor_lanes<8>(acc);
+  acc += xor_lanes<16>(acc);
+  acc += xor_lanes<32>(acc);
+  if (lane == 0) y[n] = f2h(acc);
+}
+
 
 // Host-side launchers (not part of the device compilation pass).
 #ifndef __HIP_DEVICE_COMPILE__
@@ -32,6 +68,20 @@ template <int K, int CB>
 static void run_decode(const uint32_t* packed, int64_t tiles, uint16_t* st, uint16_t* val,
                        dim3 grid, hipStream_t s) {
   hipLaunchKernelGGL((decode_tiles_kernel<K, CB>), grid, dim3(256), 0, s, packed, tiles, st, val);
+}
+
+void launch_codewords(const uint16_t* states, int64_t n, int cb, uint16_t* values,
+                      hipStream_t s) {
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (cb == 0) hipLaunchKernelGGL((codewords_kernel<0>), grid, dim3(256), 0, s, states, n, values);
+  else if (cb == 1) hipLaunchKernelGGL((codewords_kernel<1>), grid, dim3(256), 0, s, states, n, values);
+  else hipLaunchKernelGGL((codewords_kernel<2>), grid, dim3(256), 0, s, states, n, values);
+}
+
+void launch_qmv_inner(const uint16_t* values, const uint16_t* x, int rows, int cols, uint16_t* y,
+                      hipStream_t s) {
+  hipLaunchKernelGGL(qmv_inner_kernel, dim3((unsigned)((cols + 3) / 4)), dim3(256), 0, s, values,
+                     x, rows, cols, y);
 }
 
 const QmvFn kQmv[3][8][3] = {EXL3_TABLE(run_qmv1), EXL3_TABLE(run_qmv2), EXL3_TABLE(run_qmv4)};

@@ -540,4 +540,17 @@ __global__ __launch_bounds__(256) void decode_tiles_kernel(const uint32_t* __res
   });
 }
 
+// Codewords of arbitrary 16-bit states (the reference's `codebook` codec op,
+// codec.rs:52-71), with the decode code the kernels use (state in the low
+// half of a window).
+template <int CB>
+__global__ __launch_bounds__(256) void codewords_kernel(const uint16_t* __restrict__ states,
+                                                        int64_t n, uint16_t* __restrict__ values) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  uint32_t src[32];
+  src[0] = states[i];
+  values[i] = (uint16_t)decode_one<CB, 3, 0>(src);  // K = 3: state 0 sits in the low half
+}
+
 }  // namespace exl3

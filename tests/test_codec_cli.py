@@ -1,0 +1,86 @@
+"""The codec JSON-lines driver's host operations and error protocol (no GPU):
+codec_loop, native/src/main.rs:286-1360.  pack and permutation run on the host
+and are checked against the oracle and the reference's golden packed vectors;
+every malformed request gets one {"error": ...} line and the stream goes on."""
+
+import json
+
+import numpy as np
+import pytest
+
+import oracle
+from codec_client import CODEC, run
+
+pytestmark = pytest.mark.skipif(not CODEC.exists(), reason="codec driver not built")
+
+
+def test_permutation_matches_oracle():
+    (row,) = run([{"op": "permutation"}])
+    assert row == {"data": oracle.permutation().tolist()}
+
+
+def test_pack_golden_and_oracle(golden):
+    sums = json.loads((golden / "quantizer" / "checksums.json").read_text())
+    reqs, want = [], []
+    for name in sorted(sums):
+        if not name.endswith("-states.u16"):
+            continue
+        _, k, cb, _ = name.split("-")
+        states = np.fromfile(golden / "quantizer" / name, dtype="<u2")
+        packed = np.fromfile(golden / "quantizer" / name.replace("states", "packed"), dtype="<u2")
+        reqs.append({"op": "pack", "k": int(k), "mode": int(cb), "data": states.tolist()})
+        want.append(packed.tolist())
+    rng = np.random.default_rng(3)
+    for k in range(1, 9):
+        states = rng.integers(0, 1 << 16, size=512, dtype=np.uint16)
+        reqs.append({"op": "pack", "k": k, "data": states.tolist()})
+        want.append(oracle.pack(states, k).ravel().tolist())
+    rows = run(reqs)
+    assert len(want) >= 8 + 8
+    for row, w in zip(rows, want):
+        assert row == {"data": w}
+
+
+@pytest.mark.parametrize(
+    "req, message",
+    [
+        ({"op": "pack", "k": 0}, "K must be in 1..=8, got 0"),
+        ({"op": "pack", "k": 9, "data": []}, "K must be in 1..=8, got 9"),
+        ({"op": "pack", "k": 3, "data": [1] * 255}, "encoded length must be a multiple of 256"),
+        ({"op": "unpack", "k": 2, "data": [1] * 31}, "packed length is not a whole tile"),
+        ({"op": "metal-decode", "k": 0, "data": []}, "K must be in 1..=8, got 0"),
+        ({"op": "metal-decode", "k": 2, "data": [0] * 33}, "expected whole packed tiles"),
+        ({"op": "metal-qmv", "k": 2, "x": [0] * 15, "cols": 16, "data": []},
+         "expected positive 16-aligned dimensions"),
+        ({"op": "metal-qmv", "k": 2, "x": [0] * 16, "cols": 16, "data": [0] * 31},
+         "invalid trellis size or Metal index overflow"),
+        ({"op": "metal-swiglu", "x": [1, 2], "data": [1]}, "invalid SwiGLU input extents"),
+        ({"op": "mlx-linear", "k": 2, "suh": [], "x": [1]}, "invalid linear input rows"),
+        ({"op": "mlx-group", "k": 2, "widths": []}, "missing group widths"),
+        ({"op": "mlx-group", "k": 7, "widths": [128, 128], "suh": [0] * 256, "x": [0] * 128},
+         "unsupported group"),
+        ({"op": "codebook", "mode": 3, "data": [1]}, "invalid EXL3 codebook 3"),
+        ({"op": "unpack", "mode": 7, "k": 0}, "invalid EXL3 codebook 7"),
+        ({"op": "mlx-gdn"}, "unknown or unavailable codec operation mlx-gdn"),
+        ({"op": "pack", "k": 2, "data": [70000] * 256}, "invalid codec request"),
+        ({"op": "pack", "k": -1}, "invalid codec request"),
+        ({"k": 2}, "invalid codec request"),
+    ],
+)
+def test_errors_are_lines(req, message):
+    rows = run([req, {"op": "permutation"}])
+    assert list(rows[0]) == ["error"] and message in rows[0]["error"], rows[0]
+    assert "data" in rows[1]  # the stream continues
+
+
+def test_malformed_lines_and_defaults():
+    import subprocess
+
+    res = subprocess.run([str(CODEC)], input='not json\n[1]\n{"op": "pack", "data": []}\n',
+                         text=True, capture_output=True, check=True, timeout=60)
+    rows = [json.loads(line) for line in res.stdout.splitlines()]
+    assert "invalid codec request" in rows[0]["error"]
+    assert "invalid codec request" in rows[1]["error"]
+    assert rows[2] == {"data": []}  # default k = 4 is valid, nothing to pack
+    bad = subprocess.run([str(CODEC), "serve"], capture_output=True, text=True, timeout=60)
+    assert bad.returncode == 2

@@ -230,6 +230,110 @@ def moe_leg(steps, warmup):
     }
 
 
+def mlp_leg(steps, warmup, rows=1):
+    """Dense SwiGLU MLP of a decoder layer at the north-star shape (gate/up
+    4096 -> 14336, down 14336 -> 4096, K=4 3INST): exl3_mlp_forward (the SwiGLU
+    in the gate/up epilogue) against the unfused composition of the reference
+    (Exl3Group of gate/up, Array::swiglu, down Exl3Linear), graph replays
+    rotating over weight copies so every step streams from HBM."""
+    import ctypes
+
+    import torch
+
+    import mlxl3_amd
+
+    in_f, hidden, k = 4096, 14336, 4
+    gen = torch.Generator(device="cuda").manual_seed(7)
+
+    def trellis(n_in, n_out):
+        return torch.randint(-32768, 32768, (n_in // 16, n_out // 16, 16 * k), dtype=torch.int16,
+                             device="cuda", generator=gen)
+
+    def scales(n, fan):
+        return ((torch.rand(n, device="cuda", generator=gen) + 0.5) / math.sqrt(fan)).half()
+
+    per_copy = 3 * in_f * hidden * k // 8
+    copies = max(2, math.ceil(ROTATE_BYTES / per_copy))
+    su_g, su_u, su_d = scales(in_f, 1), scales(in_f, 1), scales(hidden, 1)
+    sv_g, sv_u, sv_d = scales(hidden, in_f), scales(hidden, in_f), scales(in_f, hidden)
+    layers = []
+    for _ in range(copies):
+        gate = mlxl3_amd.Exl3Linear(trellis(in_f, hidden), su_g, sv_g, None, k, 0)
+        up = mlxl3_amd.Exl3Linear(trellis(in_f, hidden), su_u, sv_u, None, k, 0)
+        down = mlxl3_amd.Exl3Linear(trellis(hidden, in_f), su_d, sv_d, None, k, 0)
+        layers.append((gate, up, down))
+    lib = mlxl3_amd.load_library()
+    x = torch.randn(rows, in_f, device="cuda", generator=gen).half()
+    y = torch.empty(rows, in_f, dtype=torch.float16, device="cuda")
+    g_out = torch.empty(rows, hidden, dtype=torch.float16, device="cuda")
+    u_out = torch.empty_like(g_out)
+    act = torch.empty_like(g_out)
+    gate, up, down = layers[0]
+    parts2 = (ctypes.c_void_p * 2)(gate.handle.value, up.handle.value)
+    need = max(int(lib.exl3_mlp_workspace_bytes(gate.handle, up.handle, down.handle, rows)),
+               int(lib.exl3_group_workspace_bytes(parts2, 2, rows)),
+               int(down.workspace_bytes(rows)))
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+
+    def check(rc):
+        if rc:
+            raise RuntimeError(lib.exl3_last_error().decode())
+
+    def fused(layer):
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        g, u, d = layer
+        check(lib.exl3_mlp_forward(g.handle, u.handle, d.handle, x.data_ptr(), rows, y.data_ptr(),
+                                   ws.data_ptr(), need, s))
+
+    def unfused(layer):
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        g, u, d = layer
+        parts = (ctypes.c_void_p * 2)(g.handle.value, u.handle.value)
+        outs = (ctypes.c_void_p * 2)(g_out.data_ptr(), u_out.data_ptr())
+        check(lib.exl3_group_forward(parts, 2, x.data_ptr(), 9, rows, outs, ws.data_ptr(), need, s))
+        check(lib.exl3_swiglu(g_out.data_ptr(), u_out.data_ptr(), act.data_ptr(), rows * hidden, s))
+        check(lib.exl3_linear_forward(d.handle, act.data_ptr(), 9, rows, y.data_ptr(), 9,
+                                      ws.data_ptr(), need, s))
+
+    def timed(fn):
+        for layer in layers:
+            fn(layer)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for layer in layers:
+                fn(layer)
+        for _ in range(max(1, warmup // copies)):
+            graph.replay()
+        torch.cuda.synchronize()
+        reps = max(1, math.ceil(steps / copies))
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        stream = torch.cuda.current_stream()
+        start.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / (reps * copies), reps * copies
+
+    ms_fused, n = timed(fused)
+    y_fused = y.clone()
+    ms_unfused, _ = timed(unfused)
+    assert torch.equal(y_fused.view(torch.int16), y.view(torch.int16)), "fused != unfused"
+    nbytes = per_copy + (2 * in_f + 2 * hidden + hidden + in_f) * 2 + rows * in_f * 2 * 2
+    gbs = nbytes / (ms_fused * 1e-3) / 1e9
+    return {
+        "workload": f"mlp_swiglu_{in_f}x{hidden}_k{k}_3inst_m{rows}",
+        "ms_per_step": round(ms_fused, 6),
+        "ms_per_step_unfused": round(ms_unfused, 6),
+        "steps": n,
+        "weight_copies_rotated": copies,
+        "bytes_per_step": nbytes,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -238,6 +342,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-qmm", action="store_true", help="skip the QMM M=512 leg")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE SwitchGLU leg")
+    ap.add_argument("--no-mlp", action="store_true", help="skip the dense SwiGLU MLP leg")
     ap.add_argument("--k", type=int, default=4)
     ap.add_argument("--cb", type=int, default=0)
     ap.add_argument("--in-features", type=int, default=4096)
@@ -333,6 +438,9 @@ def main():
 
     if not args.no_moe:
         result["moe"] = moe_leg(max(8, args.steps // 40), max(2, args.warmup // 40))
+    if not args.no_mlp:
+        result["mlp"] = mlp_leg(max(24, args.steps // 10), max(4, args.warmup // 10), rows=1)
+        result["mlp_m512"] = mlp_leg(max(24, args.steps // 40), max(4, args.warmup // 40), rows=512)
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(n_in, n_out, k, cb, rows)

@@ -127,14 +127,11 @@ static QmmShape choose_qmm_shape(int in, int out, int64_t rows) {
   return best;
 }
 
-// Workspace: the first kWorkspaceCounterBytes hold counters that are zero
-// between calls (every call leaves them zero, so one workspace serves every
-// entry point in any order): split-K counters from word 0, the SwiGLU pair
-// counters of a (gate, up) QMM from word kPairCounterBase.  The rest is
-// per-call scratch: QMV partials, or QMM xhat rows (one set per member) and
-// partials.
+// Workspace: the first kWorkspaceCounterBytes hold split-K counters that are
+// zero between calls (every call leaves them zero, so one workspace serves
+// every entry point in any order).  The rest is per-call scratch: QMV
+// partials, or QMM xhat rows (one set per member) and partials.
 static constexpr int kCounterWords = (int)(kWorkspaceCounterBytes / sizeof(uint32_t));
-static constexpr int kPairCounterBase = kCounterWords / 2;
 
 // A launch over 1..kMaxMembers projections sharing one input.
 struct Group {
@@ -156,7 +153,7 @@ static int make_group(const exl3_linear* const* parts, int count, Group& g) {
     g.parts[i] = parts[i];
     total += parts[i]->out;
   }
-  if (total > INT32_MAX || total / 128 > kPairCounterBase)
+  if (total > INT32_MAX || total / 128 > kCounterWords)
     return fail(EXL3_EUNSUPPORTED, "EXL3 group too wide: %lld columns", (long long)total);
   g.count = count;
   g.in = parts[0]->in;
@@ -243,7 +240,7 @@ static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows
 // xhats: per member, null to run the prologue into the scratch.
 static int run_group_qmm(const Group& g, const void* x, int x_type, int64_t rows,
                          void* const* ys, int y_type, uint32_t* counters, char* scratch,
-                         const uint16_t* given_xhat, const Glu& glu, hipStream_t stream) {
+                         const uint16_t* given_xhat, hipStream_t stream) {
   const size_t xbytes = align_up(sizeof(uint16_t) * (size_t)rows * g.in);
   QmmParams q{};
   if (!given_xhat) {
@@ -276,7 +273,6 @@ static int run_group_qmm(const Group& g, const void* x, int x_type, int64_t rows
   q.col_blocks = g.total_out / 128;
   q.mtiles = sh.mtiles;
   q.splits = sh.splits;
-  q.glu = glu;
   const int mbi = sh.mb == 4 ? 2 : sh.mb == 2 ? 1 : 0;
   const int64_t wgs = (int64_t)sh.mtiles * q.col_blocks * sh.splits;
   if (wgs > INT32_MAX) return fail(EXL3_EINVAL, "EXL3 QMM grid too large");
@@ -301,16 +297,17 @@ static int group_forward(const Group& g, const void* x, int x_type, int64_t rows
   const Glu none{};
   if (rows <= kQmvMaxRows)
     return run_group_qmv(g, x, x_type, rows, ys, y_type, counters, scratch, none, stream);
-  return run_group_qmm(g, x, x_type, rows, ys, y_type, counters, scratch, nullptr, none, stream);
+  return run_group_qmm(g, x, x_type, rows, ys, y_type, counters, scratch, nullptr, stream);
 }
 
 // ---------------------------------------------------------------------------
 // SwiGLU MLP: y = down(swiglu(gate(x), up(x))), f16 activations.
-// rows <= 16: (gate, up) QMV with the SwiGLU edge -> act, then the down QMV
-// (its prologue fused as for any linear).  rows > 16: prologue of gate and up,
-// the (gate, up) QMM whose edge writes the down projection's xhat, then the
-// down QMM.  Rows are processed in chunks whose tile count fits the pair
-// counters.
+// rows <= 16: one (gate, up) QMV launch whose epilogue applies the SwiGLU
+// (the last workgroup of a column block pair holds both partial sums), then
+// the down QMV (its prologue fused as for any linear): 2 launches.
+// rows > 16: the (gate, up) group (prologue + QMM), one kernel applying the
+// SwiGLU and the down projection's prologue, then the down QMM on that xhat:
+// 4 launches instead of 6, and the activation never round-trips HBM.
 // ---------------------------------------------------------------------------
 static int mlp_check(const exl3_linear* gate, const exl3_linear* up, const exl3_linear* down) {
   if (!gate || !up || !down) return fail(EXL3_EINVAL, "null EXL3 MLP projection");
@@ -322,39 +319,22 @@ static int mlp_check(const exl3_linear* gate, const exl3_linear* up, const exl3_
   return EXL3_OK;
 }
 
-// Rows per MLP chunk: the QMM pair counters hold mtiles * H/128 entries.
-static int64_t mlp_chunk_rows(const exl3_linear* gate) {
-  const int64_t tiles_per_mtile = gate->out / 128;
-  const int64_t mtiles = (kCounterWords - kPairCounterBase) / std::max<int64_t>(1, tiles_per_mtile);
-  return std::max<int64_t>(kQmvMaxRows + 1, mtiles * 64);  // 64-row tiles at the smallest
-}
-
-// Workspace of one MLP chunk of `rows` rows.
-static size_t mlp_chunk_ws(const Group& g, const exl3_linear* down, int64_t rows) {
-  const size_t act = align_up(sizeof(uint16_t) * (size_t)rows * g.parts[0]->out);
-  if (rows <= kQmvMaxRows) {
-    const size_t stage2 = align_up(sizeof(float) * (size_t)down->qmv_splits * rows * down->out);
-    return act + std::max(group_scratch_bytes(g, rows), stage2);
-  }
-  const QmmShape sh = choose_qmm_shape(down->in, down->out, rows);
-  const size_t stage2 =
-      sh.splits > 1 ? align_up(sizeof(float) * (size_t)sh.splits * rows * down->out) : 0;
-  // act (the down xhat) + gate and up outputs exchanged between workgroups
-  return 3 * act + std::max(group_scratch_bytes(g, rows), stage2);
-}
-
 static size_t mlp_ws_bytes(const exl3_linear* gate, const exl3_linear* up,
                            const exl3_linear* down, int64_t rows) {
   const exl3_linear* gu[2] = {gate, up};
   Group g;
   if (make_group(gu, 2, g)) return 0;
+  const size_t act = align_up(sizeof(uint16_t) * (size_t)rows * gate->out);
   size_t need;
   if (rows <= kQmvMaxRows) {
-    need = mlp_chunk_ws(g, down, rows);
+    const size_t stage2 = align_up(sizeof(float) * (size_t)down->qmv_splits * rows * down->out);
+    need = act + std::max(group_scratch_bytes(g, rows), stage2);
   } else {
-    // full chunks, and a last chunk that may fall to the QMV path
-    need = std::max(mlp_chunk_ws(g, down, std::min(rows, mlp_chunk_rows(gate))),
-                    mlp_chunk_ws(g, down, kQmvMaxRows));
+    const QmmShape sh = choose_qmm_shape(down->in, down->out, rows);
+    const size_t stage2 =
+        sh.splits > 1 ? align_up(sizeof(float) * (size_t)sh.splits * rows * down->out) : 0;
+    // down xhat + gate and up outputs
+    need = 3 * act + std::max(group_scratch_bytes(g, rows), stage2);
   }
   return kWorkspaceCounterBytes + need;
 }
@@ -377,43 +357,30 @@ static int mlp_forward(const exl3_linear* gate, const exl3_linear* up, const exl
   if (!ws || ws_bytes < need)
     return fail(EXL3_EINVAL, "workspace too small: %zu bytes given, %zu needed", ws_bytes, need);
   uint32_t* counters = (uint32_t*)ws;
-  const int64_t chunk = rows <= kQmvMaxRows ? rows : mlp_chunk_rows(gate);
-  const size_t H = (size_t)gate->out;
-  for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
-    const int64_t n = std::min(chunk, rows - r0);
-    const uint16_t* xr = (const uint16_t*)x + (size_t)r0 * gate->in;
-    uint16_t* yr = (uint16_t*)y + (size_t)r0 * down->out;
-    char* base = (char*)ws + kWorkspaceCounterBytes;
-    uint16_t* act = (uint16_t*)base;
-    const size_t act_bytes = align_up(sizeof(uint16_t) * (size_t)n * H);
+  char* base = (char*)ws + kWorkspaceCounterBytes;
+  uint16_t* act = (uint16_t*)base;  // the activation (QMV) or the down xhat (QMM)
+  const size_t act_bytes = align_up(sizeof(uint16_t) * (size_t)rows * gate->out);
+  void* dy[1] = {y};
+  if (rows <= kQmvMaxRows) {
     Glu glu{};
     glu.on = 1;
     glu.out = act;
-    if (n <= kQmvMaxRows) {
-      // the pair counters of the QMV are its split counters (one per block pair)
-      void* gu_y[2] = {nullptr, nullptr};  // not written: the edge consumes the partials
-      if (int rc = run_group_qmv(g, xr, EXL3_F16, n, gu_y, EXL3_F16, counters,
-                                 base + act_bytes, glu, stream))
-        return rc;
-      void* dy[1] = {yr};
-      if (int rc = run_group_qmv(d, act, EXL3_F16, n, dy, EXL3_F16, counters, base + act_bytes,
-                                 Glu{}, stream))
-        return rc;
-    } else {
-      void* gu_y[2] = {base + act_bytes, base + 2 * act_bytes};
-      char* scratch = base + 3 * act_bytes;
-      glu.down_suh = down->suh;
-      glu.pair_counters = counters + kPairCounterBase;
-      if (int rc = run_group_qmm(g, xr, EXL3_F16, n, gu_y, EXL3_F16, counters, scratch, nullptr,
-                                 glu, stream))
-        return rc;
-      void* dy[1] = {yr};
-      if (int rc = run_group_qmm(d, nullptr, EXL3_F16, n, dy, EXL3_F16, counters, scratch, act,
-                                 Glu{}, stream))
-        return rc;
-    }
+    void* gu_y[2] = {nullptr, nullptr};  // not written: the edge consumes the partials
+    if (int rc = run_group_qmv(g, x, EXL3_F16, rows, gu_y, EXL3_F16, counters, base + act_bytes,
+                               glu, stream))
+      return rc;
+    return run_group_qmv(d, act, EXL3_F16, rows, dy, EXL3_F16, counters, base + act_bytes, Glu{},
+                         stream);
   }
-  return EXL3_OK;
+  void* gu_y[2] = {base + act_bytes, base + 2 * act_bytes};
+  char* scratch = base + 3 * act_bytes;
+  if (int rc = run_group_qmm(g, x, EXL3_F16, rows, gu_y, EXL3_F16, counters, scratch, nullptr,
+                             stream))
+    return rc;
+  launch_swiglu_prepare((const uint16_t*)gu_y[0], (const uint16_t*)gu_y[1], down->suh, gate->out,
+                        (int)rows, act, stream);
+  if (int rc = check_launch("SwiGLU prepare launch")) return rc;
+  return run_group_qmm(d, nullptr, EXL3_F16, rows, dy, EXL3_F16, counters, scratch, act, stream);
 }
 
 // ---------------------------------------------------------------------------

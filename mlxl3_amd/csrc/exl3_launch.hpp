@@ -33,6 +33,9 @@ void launch_codewords(const uint16_t* states, int64_t n, int cb, uint16_t* value
 // y = f16(x . W) over decoded tiles (no glue).
 void launch_qmv_inner(const uint16_t* values, const uint16_t* x, int rows, int cols, uint16_t* y,
                       hipStream_t s);
+// xhat = the down projection's prologue of swiglu(gate, up), [rows][H].
+void launch_swiglu_prepare(const uint16_t* gate, const uint16_t* up, const uint16_t* down_suh,
+                           int H, int rows, uint16_t* xhat, hipStream_t s);
 // out[i] = swiglu(gate[i], up[i]) in f16 (Array::swiglu).
 void launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,
                    hipStream_t s);

@@ -21,16 +21,15 @@ struct Member {
   int cblk0;                // first global column block
 };
 
-// SwiGLU edge of a (gate, up) group: members 0 and 1 have equal widths; the
-// last workgroup to finish a 128-column block of both computes
-// act = f16((g * sigmoid(g)) * u) for it and writes either act [M][out] or,
-// with down_suh set, the down projection's xhat [M][out]
+// SwiGLU edge of a (gate, up) QMV group: members 0 and 1 have equal widths;
+// the last workgroup to finish a 128-column block of both computes
+// act = f16((g * sigmoid(g)) * u) for it and writes act [M][out] or, with
+// down_suh set, the down projection's xhat [M][out]
 // (f16(H128(f16(act * down_suh)) / sqrt(128))).
 struct Glu {
   int on;
   uint16_t* out;             // act or down xhat, [M][out] f16
   const uint16_t* down_suh;  // null: write act
-  uint32_t* pair_counters;   // QMM: [mtiles][out/128]; QMV uses the split counters
 };
 
 struct QmvParams {
@@ -53,7 +52,6 @@ struct QmmParams {
   int col_blocks;      // total_out / 128
   int mtiles;          // ceil(M / rows per workgroup)
   int splits;          // K-ranges per output tile (global split-K)
-  Glu glu;
 };
 
 struct PrologueParams {

@@ -78,6 +78,13 @@ void launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int6
   hipLaunchKernelGGL(swiglu_kernel, dim3(blocks), dim3(256), 0, s, gate, up, out, n, vec);
 }
 
+void launch_swiglu_prepare(const uint16_t* gate, const uint16_t* up, const uint16_t* down_suh,
+                           int H, int rows, uint16_t* xhat, hipStream_t s) {
+  const int64_t waves = (int64_t)rows * ((H / 128 + 7) / 8);
+  hipLaunchKernelGGL(swiglu_prepare_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s,
+                     gate, up, down_suh, H, rows, xhat);
+}
+
 void launch_fill_zero(uint32_t* p, size_t words, hipStream_t s) {
   unsigned blocks = (unsigned)((words + 255) / 256 < 4096 ? (words + 255) / 256 : 4096);
   hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0, s, p, words);

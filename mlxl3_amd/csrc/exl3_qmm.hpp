@@ -52,6 +52,46 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueParams p) {
                     threadIdx.x & 63, xhat + (size_t)row * p.in);
 }
 
+// The SwiGLU edge between a (gate, up) group and its down projection:
+// xhat_down = f16(H128(f16(swiglu(g, u) * down_suh)) / sqrt(128)) (the down
+// projection's prologue applied to the activation, as the reference's
+// flash_up_finish_swiglu_prepare fuses them, exl3.metal:265-291, with
+// Array::swiglu's f16 arithmetic).  One wave per (row, run of eight
+// 128-blocks), pair layout, the run's loads in flight together.
+// grid (ceil(rows * runs / 4)), 256 threads.
+__global__ __launch_bounds__(256) void swiglu_prepare_kernel(const uint16_t* __restrict__ gate,
+                                                             const uint16_t* __restrict__ up,
+                                                             const uint16_t* __restrict__ down_suh,
+                                                             int H, int rows,
+                                                             uint16_t* __restrict__ xhat) {
+  const int nb = H >> 7, runs = (nb + 7) >> 3;
+  const int job = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = job / runs, run = job - row * runs;
+  if (row >= rows) return;  // uniform per wave
+  const int lane = threadIdx.x & 63;
+  const int b_begin = 8 * run, b_end = min(b_begin + 8, nb);
+  const uint32_t* g32 = (const uint32_t*)(gate + (size_t)row * H);
+  const uint32_t* u32 = (const uint32_t*)(up + (size_t)row * H);
+  const uint32_t* s32 = (const uint32_t*)down_suh;
+  uint32_t* x32 = (uint32_t*)(xhat + (size_t)row * H);
+  uint32_t gp[8], up2[8], sp[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int b = min(b_begin + t, b_end - 1);  // clamped: loads stay in bounds
+    gp[t] = g32[b * 64 + lane];
+    up2[t] = u32[b * 64 + lane];
+    sp[t] = s32[b * 64 + lane];
+  }
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const float a0 = swiglu_f16(h2f((uint16_t)gp[t]), h2f((uint16_t)up2[t]));
+    const float a1 = swiglu_f16(h2f((uint16_t)(gp[t] >> 16)), h2f((uint16_t)(up2[t] >> 16)));
+    const uint32_t bits = pair_h128_bits(round_f16(a0 * h2f((uint16_t)sp[t])),
+                                         round_f16(a1 * h2f((uint16_t)(sp[t] >> 16))), lane);
+    if (b_begin + t < b_end) x32[(b_begin + t) * 64 + lane] = bits;
+  }
+}
+
 template <int STRIDE>
 __device__ __forceinline__ float bfly_lane(float v, int lane) {
   float p = xor_lanes<STRIDE>(v);
@@ -98,8 +138,7 @@ __device__ __forceinline__ uint32_t out16(float v16, float b, bool has_bias, int
 // one 16-byte store (two for f32).  sv/bv: svh and bias of the lane's columns.
 __device__ __forceinline__ void qmm_finish_chunk(const u32x4 raw, const float (&sv)[8],
                                                  const float (&bv)[8], int lane, bool live,
-                                                 const Member& mm, int y_dtype, bool coherent,
-                                                 size_t yoff) {
+                                                 const Member& mm, int y_dtype, size_t yoff) {
   float v[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -145,13 +184,6 @@ __device__ __forceinline__ void qmm_finish_chunk(const u32x4 raw, const float (&
   for (int i = 0; i < 4; ++i)
     o[i] = out16(v[2 * i], bv[2 * i], has_bias, y_dtype) |
            (out16(v[2 * i + 1], bv[2 * i + 1], has_bias, y_dtype) << 16);
-  if (coherent) {  // read by another workgroup of the same launch
-    uint32_t* yw = (uint32_t*)((uint16_t*)mm.y + yoff);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __hip_atomic_store(yw + i, o[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
-  }
   *(u32x4*)((uint16_t*)mm.y + yoff) = o;
 }
 
@@ -165,38 +197,6 @@ __device__ __forceinline__ void qmm_produce(const uint32_t (&B)[K + 1], u32x4* d
   dst[1 * 64 + lane] = __builtin_bit_cast(u32x4, decode_fragment<CB, K, 0, 1>(src));
   dst[2 * 64 + lane] = __builtin_bit_cast(u32x4, decode_fragment<CB, K, 1, 0>(src));
   dst[3 * 64 + lane] = __builtin_bit_cast(u32x4, decode_fragment<CB, K, 1, 1>(src));
-}
-
-// SwiGLU edge of a finished (gate, up) tile pair: rows [row0, row0 + 64*MB)
-// of columns [colb, colb + 128), one row per wave at a time in the pair
-// layout (lane holds columns colb + 2*lane, +1).  Kept out of line so that its
-// registers do not add to the main loop's.
-template <int MB>
-__device__ __attribute__((noinline)) void qmm_glu_rows(const uint16_t* gate_y,
-                                                       const uint16_t* up_y,
-                                                       const uint16_t* down_suh, uint16_t* out,
-                                                       int H, int M, int row0, int colb, int wave,
-                                                       int lane) {
-  const uint32_t* gy = (const uint32_t*)(gate_y + colb);
-  const uint32_t* uy = (const uint32_t*)(up_y + colb);
-  for (int rl = wave; rl < 64 * MB; rl += 8) {
-    const int row = row0 + rl;
-    if (row >= M) break;  // uniform per wave
-    const size_t w = (size_t)row * (H >> 1) + lane;
-    const uint32_t gp = __hip_atomic_load(gy + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t up = __hip_atomic_load(uy + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const float a0 = swiglu_f16(h2f((uint16_t)gp), h2f((uint16_t)up));
-    const float a1 = swiglu_f16(h2f((uint16_t)(gp >> 16)), h2f((uint16_t)(up >> 16)));
-    uint32_t bits;
-    if (down_suh) {  // the down projection's prologue on this 128-block
-      const uint32_t s = ((const uint32_t*)(down_suh + colb))[lane];
-      bits = pair_h128_bits(round_f16(a0 * h2f((uint16_t)s)),
-                            round_f16(a1 * h2f((uint16_t)(s >> 16))), lane);
-    } else {
-      bits = (uint32_t)f2h(a0) | ((uint32_t)f2h(a1) << 16);
-    }
-    ((uint32_t*)(out + colb))[(size_t)row * (H >> 1) + lane] = bits;
-  }
 }
 
 template <int K, int CB, int MB>
@@ -473,27 +473,10 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
       const int rl = wave * 8 * MB + 4 * i + (lane >> 4);
       const int row = mtile * 64 * MB + rl;
       const u32x4 raw = *(const u32x4*)(ys + rl * kYStride + 8 * chunk);
-      qmm_finish_chunk(raw, sv, bv, lane, row < p.M, mm, p.y_dtype, p.glu.on,
+      qmm_finish_chunk(raw, sv, bv, lane, row < p.M, mm, p.y_dtype,
                        (size_t)row * mm.out + colb + 8 * chunk);
     }
   }
-  if (!p.glu.on) return;
-
-  // ---- SwiGLU edge: the second of the (gate, up) tiles to finish computes
-  // act = swiglu(g, u) for the tile (and the down projection's prologue) ----
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  const int H = p.mem[0].out;
-  uint32_t* pc = p.glu.pair_counters + (size_t)mtile * (H >> 7) + cblk_l;
-  if (threadIdx.x == 0) {
-    uint32_t old = __hip_atomic_fetch_add(pc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (old == 1u);
-  }
-  __syncthreads();
-  if (!s_last) return;  // uniform across the workgroup
-  if (threadIdx.x == 0) __hip_atomic_store(pc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  qmm_glu_rows<MB>((const uint16_t*)p.mem[0].y, (const uint16_t*)p.mem[1].y, p.glu.down_suh,
-                   p.glu.out, H, p.M, mtile * 64 * MB, cblk_l * 128, wave, lane);
 }
 
 }  // namespace exl3

@@ -60,6 +60,29 @@ __device__ __forceinline__ void load_slice_prev(const uint32_t* __restrict__ p, 
   }
 }
 
+// The same loads from a wave-uniform base plus per-lane byte offsets (the
+// lane's own words at `loff`, the previous lane's last word at `loff_prev`):
+// the address stays a scalar base + 32-bit vector offset, so a slice costs no
+// vector address arithmetic.
+template <int K>
+__device__ __forceinline__ void load_slice_prev_s(const char* sbase, uint32_t loff,
+                                                  uint32_t loff_prev, uint32_t (&w)[K + 1]) {
+  w[0] = __builtin_nontemporal_load((const uint32_t*)(sbase + loff_prev));
+  const uint32_t* p = (const uint32_t*)(sbase + loff);
+  if constexpr (K == 4) {
+    u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    w[1] = v[0], w[2] = v[1], w[3] = v[2], w[4] = v[3];
+  } else if constexpr (K == 8) {
+    u32x4 v0 = __builtin_nontemporal_load((const u32x4*)p);
+    u32x4 v1 = __builtin_nontemporal_load((const u32x4*)p + 1);
+    w[1] = v0[0], w[2] = v0[1], w[3] = v0[2], w[4] = v0[3];
+    w[5] = v1[0], w[6] = v1[1], w[7] = v1[2], w[8] = v1[3];
+  } else {
+#pragma unroll
+    for (int i = 0; i < K; ++i) w[i + 1] = __builtin_nontemporal_load(p + i);
+  }
+}
+
 // Load the K words of this lane's slice of a tile.
 template <int K>
 __device__ __forceinline__ void load_slice(const uint32_t* __restrict__ p, uint32_t (&w)[K]) {
@@ -329,17 +352,19 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
 
   const int g = lane >> 4, hsel = (lane >> 3) & 1, j = lane & 7;
   const int tn0 = cblk_l * 8 + pair * 2;
-  const size_t qstride = (size_t)4 * TN * 8 * K;
-  const uint32_t* tp = mm.trellis +
-                       ((size_t)((row0 >> 4) + 4 * q_lo + g) * TN + tn0 + hsel) * (8 * K) +
-                       (size_t)j * K;
+  const size_t qstride = (size_t)4 * TN * 8 * K;  // words per quad of tile rows
+  // wave-uniform base of the K-part's first quad; per-lane byte offsets
+  const uint32_t* wbase = mm.trellis + ((size_t)((row0 >> 4) + 4 * q_lo) * TN + tn0) * (8 * K);
+  const uint32_t loff = (uint32_t)(((g * TN + hsel) * 8 * K + j * K) * 4);
+  const uint32_t loff_prev = loff + (uint32_t)((j == 0 ? 8 * K - 1 : -1) * 4);
   constexpr int D = kQmvDepth<K>;
-  const int prev_off = j == 0 ? 8 * K - 1 : -1;  // previous lane's last word of the tile
   uint32_t setA[D][K + 1], setB[D][K + 1];
   const int qlast = nquads > 0 ? nquads - 1 : 0;
+  auto slice_base = [&](int q) {
+    return (const char*)(wbase + (size_t)min(q, qlast) * qstride);
+  };
 #pragma unroll
-  for (int d = 0; d < D; ++d)
-    load_slice_prev<K>(tp + (size_t)min(d, qlast) * qstride, prev_off, setA[d]);
+  for (int d = 0; d < D; ++d) load_slice_prev_s<K>(slice_base(d), loff, loff_prev, setA[d]);
   __builtin_amdgcn_sched_barrier(0);
 
   // prologue into LDS
@@ -367,26 +392,26 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
 
   // main loop: two sets of D slices in ping-pong; the D loads of one set are
   // issued together, then the other set (already in flight for D steps) is
-  // decoded, so a wait at any point still has D steps of decode behind it
-  const int am = lane & 15;
-  const bool arow = am < M;
+  // decoded, so a wait at any point still has D steps of decode behind it.
+  // A rows >= M read row M-1: MFMA output rows depend only on their own A
+  // row, and rows >= M are never stored.
+  const int am = min(lane & 15, M - 1);
   const _Float16* xrow = xs + (size_t)am * nrows + 64 * q_lo + g * 16;
   float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  const half8 zero8 = {};
+  // issue priority falls at the quarters of the K-range (steps t1, t2, t3)
+  const int t1 = (nquads + 3) / 4, t2 = (2 * nquads + 3) / 4, t3 = (3 * nquads + 3) / 4;
   auto compute = [&](uint32_t(&set)[D][K + 1], int qbase) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const int q = qbase + d;
       if (q < nquads) {
-        half8 a0 = arow ? *(const half8*)(xrow + q * 64) : zero8;
-        half8 a1 = arow ? *(const half8*)(xrow + q * 64 + 8) : zero8;
+        half8 a0 = *(const half8*)(xrow + q * 64);
+        half8 a1 = *(const half8*)(xrow + q * 64 + 8);
         qmv_step_prev<K, CB>(set[d], a0, a1, acc0, acc1);
-        if (4 * (q + 1) / nquads != 4 * q / nquads) {
-          const int level = 4 * (q + 1) / nquads;  // quarter of the K-range completed
-          if (level == 1) __builtin_amdgcn_s_setprio(2);
-          else if (level == 2) __builtin_amdgcn_s_setprio(1);
-          else __builtin_amdgcn_s_setprio(0);
-        }
+        const int t = q + 1;
+        if (t == t3) __builtin_amdgcn_s_setprio(0);
+        else if (t == t2) __builtin_amdgcn_s_setprio(1);
+        else if (t == t1) __builtin_amdgcn_s_setprio(2);
       }
     }
   };
@@ -394,8 +419,7 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   // load count static, so the waits before each decode can be partial.
   auto fetch = [&](uint32_t(&set)[D][K + 1], int qbase) {
 #pragma unroll
-    for (int d = 0; d < D; ++d)
-      load_slice_prev<K>(tp + (size_t)min(qbase + d, qlast) * qstride, prev_off, set[d]);
+    for (int d = 0; d < D; ++d) load_slice_prev_s<K>(slice_base(qbase + d), loff, loff_prev, set[d]);
   };
   for (int q0 = 0; q0 < nquads; q0 += 2 * D) {
     fetch(setB, q0 + D);

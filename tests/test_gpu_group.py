@@ -7,7 +7,9 @@ the GPU, through the C ABI.
   exl3_linear_forward (same kernels, same split order per column block);
 * exl3_swiglu (Array::swiglu, native/ffi/mlx_bridge.cpp:745-749) against the
   oracle's f16-staged restatement: bit-exact for every finite f16 gate value;
-* exl3_mlp_forward (qwen35.rs:303-307) against the unfused composition
+* exl3_mlp_forward (qwen35.rs:303-307; rows <= 16: SwiGLU in the gate/up QMV
+  epilogue; rows > 16: one SwiGLU + down-prologue kernel between the QMMs)
+  against the unfused composition
   exl3_group_forward -> exl3_swiglu -> exl3_linear_forward: bit-exact; and
   against the oracle composition (oracle.mlp_forward) within the linear's
   stated tolerance chain (rel L2 <= 2e-3, max-abs <= 1e-2 of rms(y): the
@@ -152,11 +154,9 @@ def test_mlp_fused_equals_unfused_and_oracle(k, cb, rows):
         check_tol(y.cpu().numpy(), oracle.mlp_forward(x_np, *host), f"mlp k={k} cb={cb} rows={rows}")
 
 
-@pytest.mark.parametrize("rows", [1029, 1100])
-def test_mlp_row_chunks(rows):
-    """A wide intermediate (512 column blocks) splits the rows into chunks of
-    1024 so the SwiGLU pair counters fit; the tail chunk of 5 rows runs the QMV
-    path, the one of 76 the QMM path."""
+@pytest.mark.parametrize("rows", [5, 1100])
+def test_mlp_wide_intermediate(rows):
+    """A wide intermediate (512 column blocks of 128) through both paths."""
     torch = torch_mod()
     mlp, parts, _ = mlp_case(128, 65536, 2, 0, seed=5)
     x = torch.from_numpy(synth.activations(9, rows, rows, 128)).cuda()

@@ -28,6 +28,8 @@ from typing import Optional, Sequence
 LIB_PATH = Path(__file__).resolve().parent / "libexl3_hip.so"
 
 __all__ = [
+    "codewords",
+    "qmv_inner",
     "Exl3Mlp",
     "swiglu",
     "Checkpoint",
@@ -90,6 +92,9 @@ _SIGNATURES = {
     "exl3_moe_workspace_bytes": (_sz, [_vp, _i64]),
     "exl3_moe_forward": (_i32, [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
     "exl3_decode_tiles": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _vp]),
+    "exl3_codewords": (_i32, [_vp, _i64, _i32, _vp, _vp]),
+    "exl3_qmv_inner_workspace_bytes": (_sz, [_i32, _i32]),
+    "exl3_qmv_inner": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "exl3_checkpoint_open": (_i32, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "exl3_checkpoint_close": (None, [_vp]),
     "exl3_checkpoint_path": (ctypes.c_char_p, [_vp]),
@@ -588,6 +593,32 @@ class Exl3SwitchGlu:
         return y
 
     __call__ = forward
+
+
+def codewords(states, cb: int):
+    """f16 codewords of arbitrary 16-bit states (the `codebook` codec op,
+    codec.rs:52-71) on the GPU: int16/uint16 device tensor -> float16."""
+    torch = _torch()
+    states = _require_device(states, "states")
+    values = torch.empty(states.shape, dtype=torch.float16, device=states.device)
+    _check(load_library().exl3_codewords(_ptr(states), states.numel(), int(cb), _ptr(values),
+                                         _stream_ptr(states.device)))
+    return values
+
+
+def qmv_inner(packed, x, cols: int, k: int, cb: int):
+    """The serial inner QMV without glue (the `metal-qmv` codec op, exl3.metal:118-142):
+    y[n] = f16(sum_r x[r] W[r][n]) for a packed [rows/16][cols/16][16k] trellis."""
+    torch = _torch()
+    packed = _require_device(packed, "packed")
+    x = _require_device(x, "x", (torch.float16,))
+    rows = x.numel()
+    y = torch.empty(cols, dtype=torch.float16, device=x.device)
+    need = int(load_library().exl3_qmv_inner_workspace_bytes(rows, int(cols)))
+    ws = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device)
+    _check(load_library().exl3_qmv_inner(_ptr(packed), rows, int(cols), int(k), int(cb), _ptr(x),
+                                         _ptr(y), _ptr(ws), ws.numel(), _stream_ptr(x.device)))
+    return y
 
 
 def decode_tiles(packed, k: int, cb: int, with_states: bool = True):

@@ -334,6 +334,221 @@ def mlp_leg(steps, warmup, rows=1):
     }
 
 
+def _dev_linear(n_in, n_out, k, cb, gen, out_scale=1.0):
+    """An Exl3Linear over device-generated random trellis words (every bitstream
+    is a valid trellis) and +-U(0.5, 1.5) f16 scales (svh times out_scale),
+    seeded by `gen`."""
+    import torch
+
+    import mlxl3_amd
+
+    tr = torch.randint(-32768, 32768, (n_in // 16, n_out // 16, 16 * k), dtype=torch.int16,
+                       device="cuda", generator=gen)
+
+    def scales(n):
+        sign = torch.randint(0, 2, (n,), device="cuda", generator=gen).half() * 2 - 1
+        return (sign * (torch.rand(n, device="cuda", generator=gen) + 0.5)).half()
+
+    return mlxl3_amd.Exl3Linear(tr, scales(n_in), (scales(n_out) * out_scale).half(), None, k, cb)
+
+
+def _graph_time(fn, steps, warmup):
+    """ms per call of fn() (which launches on the current stream), as graph
+    replays bracketed by HIP events."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        g.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def _rotated_time(n_in, n_out, k, cb, rows, steps, warmup, gen, x=None):
+    """ms per forward of one linear, rotating over weight copies of 2 GiB in
+    total so that every launch streams its trellis from HBM."""
+    import torch
+
+    per = n_in * n_out * k // 8
+    copies = max(2, min(256, math.ceil(ROTATE_BYTES / per)))
+    lins = [_dev_linear(n_in, n_out, k, cb, gen) for _ in range(copies)]
+    if x is None:
+        x = torch.randn(rows, n_in, device="cuda", generator=gen).half()
+    ws = torch.zeros(lins[0].workspace_bytes(rows), dtype=torch.uint8, device="cuda")
+    y = torch.empty(rows, n_out, dtype=torch.float16, device="cuda")
+    import ctypes
+
+    import mlxl3_amd
+
+    lib = mlxl3_amd.load_library()
+
+    def step():
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for lin in lins:
+            rc = lib.exl3_linear_forward(lin.handle, x.data_ptr(), 9, rows, y.data_ptr(), 9,
+                                         ws.data_ptr(), ws.numel(), s)
+            if rc:
+                raise RuntimeError(lib.exl3_last_error().decode())
+
+    reps = max(1, math.ceil(steps / copies))
+    ms = _graph_time(step, reps, max(1, warmup // copies)) / copies
+    del lins
+    torch.cuda.empty_cache()
+    return ms, reps * copies
+
+
+def configs_leg(steps, warmup):
+    """The remaining configurations of the measurement plan at one GPU:
+    C1 (QMV 4096x4096), the C2 QMM sweep ({4096->14336, 14336->4096} x K{3,4,5}
+    x M{16,128,512,2048}, 1 % x20 outlier channels), C3 (32 chained dense
+    decoder layers at batch 1) and C5 (27B-class verify block, MCG)."""
+    import torch
+
+    import mlxl3_amd
+    from mlxl3_amd import synth
+
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    out = {}
+    # C1
+    ms, n = _rotated_time(4096, 4096, 4, 0, 1, steps, warmup, gen)
+    b = alg_bytes(4096, 4096, 4, 1)
+    out["c1"] = {"workload": "qmv_4096x4096_k4_3inst_m1", "ms_per_step": round(ms, 6), "steps": n,
+                 "gbs": round(b / ms / 1e6, 1), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    # C2
+    sweep = []
+    for n_in, n_out in ((4096, 14336), (14336, 4096)):
+        for k in (3, 4, 5):
+            for m in (16, 128, 512, 2048):
+                x = torch.from_numpy(synth.activations(2, m, m, n_in, outlier_frac=0.01)).cuda()
+                st = max(20, steps // (4 if m <= 128 else 40 if m == 512 else 160))
+                ms, n = _rotated_time(n_in, n_out, k, 0, m, st, max(4, warmup // 10), gen, x=x)
+                tf = 2.0 * m * n_in * n_out / ms / 1e9
+                b = alg_bytes(n_in, n_out, k, m)
+                entry = {"in": n_in, "out": n_out, "k": k, "m": m, "ms": round(ms, 6),
+                         "tflops": round(tf, 1), "frac_mfma": round(tf / FP16_MFMA_PEAK_TFLOPS, 4),
+                         "gbs": round(b / ms / 1e6, 1)}
+                if m == 16:
+                    entry["frac_hbm"] = round(b / ms / 1e6 / HBM_PEAK_GBS, 4)
+                sweep.append(entry)
+    out["c2"] = sweep
+    out["c3"] = _c3_chain(gen, max(3, steps // 200), 2)
+    out["c5"] = _c5_layers(gen, max(10, steps // 40), max(2, warmup // 40))
+    return out
+
+
+def _c3_chain(gen, steps, warmup):
+    """C3: 32 dense decoder layers at batch 1, K=4 3INST, chained as
+    a=rms(x); q,k,v=W a; h=x+W_o rms(q); b=rms(h); u=swiglu(W_g b, W_u b);
+    x'=h+W_d rms(u) (residual f32; rms = f16(v / sqrt(mean v^2 + 1e-6))), one
+    graph per 32-layer step; also the same 224 linears without the glue.  The
+    gate/up output scales carry 1/sqrt(4096): with unit-scale outputs of std ~85
+    the product g*u would overflow f16."""
+    import ctypes
+
+    import torch
+
+    import mlxl3_amd
+
+    hid, inter, kv = 4096, 14336, 1024
+    layers = []
+    for _ in range(32):
+        q, kk, v, o = (_dev_linear(hid, n, 4, 0, gen) for n in (hid, kv, kv, hid))
+        g, u = (_dev_linear(hid, inter, 4, 0, gen, out_scale=1 / 64) for _ in range(2))
+        d = _dev_linear(inter, hid, 4, 0, gen)
+        layers.append((mlxl3_amd.Exl3Group([q, kk, v]), o, mlxl3_amd.Exl3Group([g, u]), d))
+    x0 = torch.randn(1, hid, device="cuda", generator=gen)
+
+    def rms(v):
+        v = v.float()
+        return (v * torch.rsqrt(v.pow(2).mean(-1, keepdim=True) + 1e-6)).half()
+
+    state = {}
+
+    def chain():
+        x = x0.clone()
+        for qkv, o, gu, d in layers:
+            qq, _, _ = qkv(rms(x))
+            h = x + o(rms(qq)).float()
+            gg, uu = gu(rms(h))
+            x = h + d(rms(mlxl3_amd.swiglu(gg, uu))).float()
+        state["y"] = x
+
+    xs = torch.randn(1, inter, device="cuda", generator=gen).half()
+    xh = xs[:, :hid].contiguous()
+
+    def linears_only():
+        for qkv, o, gu, d in layers:
+            qkv(xh)
+            o(xh)
+            gu(xh)
+            d(xs)
+
+    ms = _graph_time(chain, steps, warmup)
+    ms_lin = _graph_time(linears_only, steps, warmup)
+    per_layer = (alg_bytes(hid, hid + 2 * kv, 4, 1) + alg_bytes(hid, hid, 4, 1)
+                 + alg_bytes(hid, 2 * inter, 4, 1) + alg_bytes(inter, hid, 4, 1))
+    b = 32 * per_layer
+    y = state["y"]
+    assert torch.isfinite(y).all(), "C3 chain overflowed"
+    return {"workload": "c3_llama_layer_x32_k4_3inst_m1", "ms_per_step": round(ms, 5),
+            "ms_linears_only": round(ms_lin, 5), "bytes_per_step": b,
+            "gbs": round(b / ms / 1e6, 1), "gbs_linears_only": round(b / ms_lin / 1e6, 1),
+            "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4),
+            "out_rms": round(float(y.pow(2).mean().sqrt()), 3)}
+
+
+def _c5_layers(gen, steps, warmup):
+    """C5: one 27B-class layer of 7 linears (q/k/v as one group, o, gate/up as
+    one group, down) at M in {4, 8, 16}, K in {2, 4}, MCG, rotating over layer
+    copies."""
+    import torch
+
+    import mlxl3_amd
+
+    hid, inter, kv = 5120, 27648, 1024
+    res = []
+    for k in (2, 4):
+        per = (hid * (hid + 2 * kv) + hid * hid + 2 * hid * inter + inter * hid) * k // 8
+        copies = max(2, math.ceil(ROTATE_BYTES / per))
+        layers = []
+        for _ in range(copies):
+            q, kk, v, o = (_dev_linear(hid, n, k, 1, gen) for n in (hid, kv, kv, hid))
+            g, u, d = _dev_linear(hid, inter, k, 1, gen), _dev_linear(hid, inter, k, 1, gen), \
+                _dev_linear(inter, hid, k, 1, gen)
+            layers.append((mlxl3_amd.Exl3Group([q, kk, v]), o, mlxl3_amd.Exl3Group([g, u]), d))
+        for m in (4, 8, 16):
+            xh = torch.randn(m, hid, device="cuda", generator=gen).half()
+            xi = torch.randn(m, inter, device="cuda", generator=gen).half()
+
+            def step():
+                for qkv, o, gu, d in layers:
+                    qkv(xh)
+                    o(xh)
+                    gu(xh)
+                    d(xi)
+
+            reps = max(1, math.ceil(steps / copies))
+            ms = _graph_time(step, reps, max(1, warmup)) / copies
+            b = (alg_bytes(hid, hid + 2 * kv, k, m) + alg_bytes(hid, hid, k, m)
+                 + alg_bytes(hid, 2 * inter, k, m) + alg_bytes(inter, hid, k, m))
+            res.append({"k": k, "m": m, "cb": "mcg", "ms_per_layer": round(ms, 6),
+                        "gbs": round(b / ms / 1e6, 1), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)})
+        del layers
+        torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -343,6 +558,8 @@ def main():
     ap.add_argument("--no-qmm", action="store_true", help="skip the QMM M=512 leg")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE SwitchGLU leg")
     ap.add_argument("--no-mlp", action="store_true", help="skip the dense SwiGLU MLP leg")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the C1/C2-sweep/C3/C5 configuration legs")
     ap.add_argument("--k", type=int, default=4)
     ap.add_argument("--cb", type=int, default=0)
     ap.add_argument("--in-features", type=int, default=4096)
@@ -441,6 +658,8 @@ def main():
     if not args.no_mlp:
         result["mlp"] = mlp_leg(max(24, args.steps // 10), max(4, args.warmup // 10), rows=1)
         result["mlp_m512"] = mlp_leg(max(24, args.steps // 40), max(4, args.warmup // 40), rows=512)
+    if not args.no_configs:
+        result["configs"] = configs_leg(args.steps, args.warmup)
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(n_in, n_out, k, cb, rows)

@@ -339,14 +339,19 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   // only for the (shared, cache-resident) activations, not behind the weights.
   constexpr int kPrologueEarly = 2;
   const int nb = b1 - b0;
-  const int njobs = M * nb;
+  // Multi-row calls get xhat from a separate prologue launch (mm.xhat): the
+  // fused prologue would be repeated by every column block, M times over.
+  const bool pre = mm.xhat != nullptr;
+  const int njobs = pre ? 0 : M * nb;
   PrologueIn first[kPrologueEarly];
+  if (!pre) {
 #pragma unroll
-  for (int t = 0; t < kPrologueEarly; ++t) {
-    const int job = min(wave + t * 4 * KW, njobs - 1);  // clamped: always a valid job
-    const int m = job / nb, b = job - m * nb;
-    first[t] = prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128, mm.suh,
-                             row0 + b * 128, lane);
+    for (int t = 0; t < kPrologueEarly; ++t) {
+      const int job = min(wave + t * 4 * KW, njobs - 1);  // clamped: always a valid job
+      const int m = job / nb, b = job - m * nb;
+      first[t] = prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128, mm.suh,
+                               row0 + b * 128, lane);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -368,6 +373,14 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   __builtin_amdgcn_sched_barrier(0);
 
   // prologue into LDS
+  if (pre) {
+    const int chunks = nrows >> 3;  // 16-byte chunks per row
+    for (int i = threadIdx.x; i < M * chunks; i += 256 * KW) {
+      const int m = i / chunks, c = i - m * chunks;
+      *(u32x4*)(xs + m * nrows + c * 8) =
+          *(const u32x4*)(mm.xhat + (size_t)m * p.in + row0 + c * 8);
+    }
+  }
 #pragma unroll
   for (int t = 0; t < kPrologueEarly; ++t) {
     const int job = wave + t * 4 * KW;
@@ -379,14 +392,29 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
       xs[m * nrows + b * 128 + lane + 64] = (_Float16)v1;
     }
   }
-  for (int job = wave + kPrologueEarly * 4 * KW; job < njobs; job += 4 * KW) {
-    const int m = job / nb, b = job - m * nb;
-    const PrologueIn in = prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128,
-                                        mm.suh, row0 + b * 128, lane);
-    float v0, v1;
-    prologue_finish(in, p.x_dtype, lane, v0, v1);
-    xs[m * nrows + b * 128 + lane] = (_Float16)v0;
-    xs[m * nrows + b * 128 + lane + 64] = (_Float16)v1;
+  // the remaining jobs (multi-row calls) in batches whose loads are in flight
+  // together
+  constexpr int kPrologueBatch = 4;
+  for (int j0 = wave + kPrologueEarly * 4 * KW; j0 < njobs; j0 += kPrologueBatch * 4 * KW) {
+    PrologueIn in[kPrologueBatch];
+#pragma unroll
+    for (int t = 0; t < kPrologueBatch; ++t) {
+      const int job = min(j0 + t * 4 * KW, njobs - 1);  // clamped: always a valid job
+      const int m = job / nb, b = job - m * nb;
+      in[t] = prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128, mm.suh,
+                            row0 + b * 128, lane);
+    }
+#pragma unroll
+    for (int t = 0; t < kPrologueBatch; ++t) {
+      const int job = j0 + t * 4 * KW;
+      if (job < njobs) {
+        const int m = job / nb, b = job - m * nb;
+        float v0, v1;
+        prologue_finish(in[t], p.x_dtype, lane, v0, v1);
+        xs[m * nrows + b * 128 + lane] = (_Float16)v0;
+        xs[m * nrows + b * 128 + lane + 64] = (_Float16)v1;
+      }
+    }
   }
   __syncthreads();
 
@@ -495,10 +523,29 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
     }
   };
   if (!p.glu.on) {
-    for (int m = wave; m < M; m += 4 * KW) {
-      float v0, v1;
-      sum_row(m, cblk * 128, v0, v1);
-      finish_row128(v0, v1, lane, colb_l, mm.svh, mm.bias, mm.y, p.y_dtype, (size_t)m * mm.out);
+    // rows in batches of 4 per wave: the split sums of a batch load together
+    // (each row still adds its splits in split order)
+    constexpr int kRows = 4;
+    for (int m0 = wave; m0 < M; m0 += kRows * 4 * KW) {
+      float v0[kRows], v1[kRows];
+#pragma unroll
+      for (int t = 0; t < kRows; ++t) v0[t] = v1[t] = 0.f;
+      for (int sp = 0; sp < p.splits; ++sp) {
+#pragma unroll
+        for (int t = 0; t < kRows; ++t) {
+          const int m = min(m0 + t * 4 * KW, M - 1);  // clamped rows are loaded, not stored
+          const float* ps = p.partials + ((size_t)sp * M + m) * TO + cblk * 128;
+          v0[t] += load_coherent(ps + lane);
+          v1[t] += load_coherent(ps + lane + 64);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < kRows; ++t) {
+        const int m = m0 + t * 4 * KW;
+        if (m < M)
+          finish_row128(v0[t], v1[t], lane, colb_l, mm.svh, mm.bias, mm.y, p.y_dtype,
+                        (size_t)m * mm.out);
+      }
     }
     return;
   }

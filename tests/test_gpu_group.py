@@ -154,6 +154,18 @@ def test_mlp_fused_equals_unfused_and_oracle(k, cb, rows):
         check_tol(y.cpu().numpy(), oracle.mlp_forward(x_np, *host), f"mlp k={k} cb={cb} rows={rows}")
 
 
+def test_mlp_separate_prologue_rows():
+    """4096 -> 8192 -> 4096 at M = 16: the gate/up QMV and the down QMV both
+    take xhat from the separate prologue launch; fused == unfused bit-exact."""
+    torch = torch_mod()
+    mlp, parts, _ = mlp_case(4096, 8192, 4, 0, seed=9)
+    x = torch.from_numpy(synth.activations(3, 16, 16, 4096)).cuda()
+    y = mlp.forward(x)
+    y_ref = unfused(parts, x)
+    torch.cuda.synchronize()
+    assert same_bits(y, y_ref)
+
+
 @pytest.mark.parametrize("rows", [5, 1100])
 def test_mlp_wide_intermediate(rows):
     """A wide intermediate (512 column blocks of 128) through both paths."""

@@ -193,6 +193,23 @@ def test_north_star_shape_qmv():
     check(y, oracle.forward(x, tr, suh, svh, 4, 0, mode=0), TOL_MODE0_REL, TOL_MODE0_ULP, "NS mode0")
 
 
+@pytest.mark.parametrize("rows", [8, 16])
+def test_north_star_shape_multirow_separate_prologue(rows):
+    """4096 x 14336 at M = 8, 16: rows x blocks per K-range >= 64, so xhat comes
+    from the separate prologue launch.  Every row must equal the same row run
+    alone (fused prologue, M = 1) bit for bit, and the batch the oracle."""
+    torch = torch_mod()
+    lin, (tr, suh, svh, _) = make_layer(2, 4096, 14336, 4, 0)
+    x = synth.activations(7, rows, rows, 4096)
+    y = run(lin, x).cpu().numpy()
+    for r in (0, rows // 2, rows - 1):
+        yr = run(lin, x[r:r + 1]).cpu().numpy()
+        assert np.array_equal(y[r:r + 1].view(np.uint16), yr.view(np.uint16)), r
+    check(y, oracle.forward(x, tr, suh, svh, 4, 0, mode=1), TOL_MODE1_REL, TOL_MODE1_ULP,
+          f"NS M={rows} mode1")
+    del torch
+
+
 def test_qmm_rows_independent_of_batch():
     lin, _ = make_layer(5000, 512, 384, 4, 0)
     x = synth.activations(7, 0, 300, 512)

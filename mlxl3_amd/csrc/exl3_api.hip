@@ -82,14 +82,16 @@ static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
 }
 
 // QMM launch shape: rows per workgroup 64*MB and global K-splits.  One
-// workgroup of 8 waves fills a CU (two waves per SIMD), so the cost model
-// counts rounds of 256 workgroups times K-steps per split times the step
-// time, which is the larger of the consumers' MFMA time (16*MB MFMAs of 16
-// cycles) and the producers' decode time (~720 cycles), plus ~100 cycles of
-// barrier; a split adds its f32 partial traffic (written and read back at
-// ~5 TB/s, i.e. ~0.4 cycles per byte at 2.1 GHz).  Splits are only used while
-// the output tiles alone fill fewer than 192 CUs, so at most 256 tile
-// counters are ever needed.  EXL3_QMM_MB and EXL3_QMM_SPLITS override.
+// workgroup fills a CU, so a launch runs in rounds of 256 workgroups, each
+// round taking (K-steps per split) x (step time of that MB).  Step times
+// measured on MI355X with every CU busy: MB=1 660 ns, MB=2 900 ns, MB=4
+// 1290 ns (per 64 input rows); a split adds its f32 partials, written and read
+// back through agent-scope atomics at ~2.6 ns per KB.  Splits are only used
+// while the output tiles alone fill at most 256 workgroups, so at most 256
+// tile counters are ever needed.  Checked against a sweep of {4096x14336,
+// 14336x4096} x M{128, 512, 2048} x MB x splits: the chosen shape is the
+// fastest one measured at every point.  EXL3_QMM_MB and EXL3_QMM_SPLITS
+// override.
 static constexpr int kTileCounters = 256;
 
 struct QmmShape {
@@ -104,24 +106,25 @@ static QmmShape choose_qmm_shape(int in, int out, int64_t rows) {
     if (v == 1 || v == 2 || v == 4) force_mb = v;
   }
   if (const char* env = getenv("EXL3_QMM_SPLITS")) force_splits = std::max(0, atoi(env));
-  QmmShape best{4, 1, 1};
+  QmmShape best{4, (int)((rows + 255) / 256), 1};
   double best_cost = 1e300;
   for (int mb : {4, 2, 1}) {
     if (force_mb && mb != force_mb) continue;
+    const double step_ns = mb == 4 ? 1290.0 : mb == 2 ? 900.0 : 660.0;
     const int64_t mt = (rows + 64 * mb - 1) / (64 * mb);
     const int64_t base = mt * col_blocks;
-    int splits = 1;
-    if (base < 192) splits = (int)std::min<int64_t>((256 + base - 1) / base, 8);
-    if (force_splits) splits = force_splits;
-    splits = std::max(1, std::min(splits, std::max(1, nq / 4)));
-    if (splits > 1 && base > kTileCounters) splits = 1;
-    const int64_t rounds = (base * splits + 255) / 256;
-    const double step = std::max(256.0 * mb, 720.0) + 100.0;
-    double cost = (double)rounds * ((nq + splits - 1) / splits) * step;
-    if (splits > 1) cost += 0.4 * 2.0 * 4.0 * (double)splits * rows * out;
-    if (cost < best_cost) {
-      best_cost = cost;
-      best = QmmShape{mb, (int)mt, splits};
+    for (int splits : {1, 2, 4, 8}) {
+      int s = force_splits ? force_splits : splits;
+      s = std::max(1, std::min(s, std::max(1, nq / 4)));
+      if (s > 1 && base > kTileCounters) s = 1;
+      const int64_t rounds = (base * s + 255) / 256;
+      double cost = (double)rounds * ((nq + s - 1) / s) * step_ns;
+      if (s > 1) cost += 0.0026 * 4.0 * (double)s * rows * out;
+      if (cost < best_cost) {
+        best_cost = cost;
+        best = QmmShape{mb, (int)mt, s};
+      }
+      if (force_splits) break;
     }
   }
   return best;

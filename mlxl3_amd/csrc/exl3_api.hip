@@ -59,8 +59,9 @@ static size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // QMV launch shape.  Workgroups: out/128 column blocks x `splits` K-ranges
 // (global split-K, reduced by the last workgroup of a column block); inside a
 // workgroup KW waves per column pair split the K-range again (LDS reduction).
-// Target: about two workgroups of 4*KW waves per CU, at most 8 Hadamard
-// blocks (1024 rows) per K-range so xhat fits LDS.  EXL3_QMV_SPLITS and
+// Target: about two workgroups of 4*KW waves per CU, at least 4 and at most
+// 8 Hadamard blocks (512-1024 rows) per K-range (the upper bound keeps xhat
+// of 16 rows in 32 KB of LDS).  EXL3_QMV_SPLITS and
 // EXL3_QMV_KW override (tuning).
 static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
   const int nb = in / 128, col_blocks = out / 128;
@@ -72,11 +73,16 @@ static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
   }
   const int target_wgs = 448;
   int s = (target_wgs + col_blocks - 1) / col_blocks;
-  if (const char* env = getenv("EXL3_QMV_SPLITS")) {
+  // K-ranges of at least 4 blocks: shorter ones cost more in the split-K
+  // exchange than they add in parallelism (4096x4096: 8 splits 11.7 us, 14
+  // splits 13.9 us)
+  s = std::min(s, std::max(1, nb / 4));
+  s = std::max(s, min_splits);
+  if (const char* env = getenv("EXL3_QMV_SPLITS")) {  // tuning: any split count
     int v = atoi(env);
     if (v >= 1) s = v;
   }
-  s = std::max(1, std::min(std::max(s, min_splits), nb));
+  s = std::max(1, std::min(s, nb));
   *splits_out = s;
   *kw_out = kw;
 }
@@ -265,7 +271,8 @@ static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows
     max_blocks = std::max(max_blocks, (s + 1) * nb / p.splits - s * nb / p.splits);
   size_t lds = sizeof(uint16_t) * (size_t)rows * max_blocks * 128;
   const int kwi = kw == 4 ? 2 : kw == 2 ? 1 : 0;
-  kQmv[kwi][g.k - 1][g.cb](p, dim3(g.total_out / 128, p.splits), lds, stream);
+  const QmvFn fn = rows == 1 && kw == 1 ? kQmvSingle[g.k - 1][g.cb] : kQmv[kwi][g.k - 1][g.cb];
+  fn(p, dim3(g.total_out / 128, p.splits), lds, stream);
   return check_launch("EXL3 QMV launch");
 }
 

@@ -312,7 +312,9 @@ __device__ __forceinline__ void pair_prologue_row(const void* x, int x_dtype, si
 // KW waves share each column pair and split the workgroup's K-range between
 // them (reduced through LDS in a fixed order), so a workgroup of 4*KW waves
 // amortises one prologue over KW times more weight stream.
-template <int K, int CB, int KW>
+// MULTI = false is the single-row variant (the batch-1 decode): no batched
+// prologue or epilogue code, and never a separate prologue.
+template <int K, int CB, int KW, bool MULTI>
 __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   extern __shared__ __attribute__((aligned(16))) _Float16 xs[];  // [M][rows of split]
   __shared__ int s_last;
@@ -341,7 +343,7 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   const int nb = b1 - b0;
   // Multi-row calls get xhat from a separate prologue launch (mm.xhat): the
   // fused prologue would be repeated by every column block, M times over.
-  const bool pre = mm.xhat != nullptr;
+  const bool pre = MULTI && mm.xhat != nullptr;
   const int njobs = pre ? 0 : M * nb;
   PrologueIn first[kPrologueEarly];
   if (!pre) {
@@ -392,28 +394,40 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
       xs[m * nrows + b * 128 + lane + 64] = (_Float16)v1;
     }
   }
-  // the remaining jobs (multi-row calls) in batches whose loads are in flight
-  // together
-  constexpr int kPrologueBatch = 4;
-  for (int j0 = wave + kPrologueEarly * 4 * KW; j0 < njobs; j0 += kPrologueBatch * 4 * KW) {
-    PrologueIn in[kPrologueBatch];
+  if constexpr (MULTI) {
+    // the remaining jobs (multi-row calls) in batches whose loads are in
+    // flight together
+    constexpr int kPrologueBatch = 4;
+    for (int j0 = wave + kPrologueEarly * 4 * KW; j0 < njobs; j0 += kPrologueBatch * 4 * KW) {
+      PrologueIn in[kPrologueBatch];
 #pragma unroll
-    for (int t = 0; t < kPrologueBatch; ++t) {
-      const int job = min(j0 + t * 4 * KW, njobs - 1);  // clamped: always a valid job
-      const int m = job / nb, b = job - m * nb;
-      in[t] = prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128, mm.suh,
-                            row0 + b * 128, lane);
-    }
-#pragma unroll
-    for (int t = 0; t < kPrologueBatch; ++t) {
-      const int job = j0 + t * 4 * KW;
-      if (job < njobs) {
+      for (int t = 0; t < kPrologueBatch; ++t) {
+        const int job = min(j0 + t * 4 * KW, njobs - 1);  // clamped: always a valid job
         const int m = job / nb, b = job - m * nb;
-        float v0, v1;
-        prologue_finish(in[t], p.x_dtype, lane, v0, v1);
-        xs[m * nrows + b * 128 + lane] = (_Float16)v0;
-        xs[m * nrows + b * 128 + lane + 64] = (_Float16)v1;
+        in[t] = prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128, mm.suh,
+                              row0 + b * 128, lane);
       }
+#pragma unroll
+      for (int t = 0; t < kPrologueBatch; ++t) {
+        const int job = j0 + t * 4 * KW;
+        if (job < njobs) {
+          const int m = job / nb, b = job - m * nb;
+          float v0, v1;
+          prologue_finish(in[t], p.x_dtype, lane, v0, v1);
+          xs[m * nrows + b * 128 + lane] = (_Float16)v0;
+          xs[m * nrows + b * 128 + lane + 64] = (_Float16)v1;
+        }
+      }
+    }
+  } else {
+    for (int job = wave + kPrologueEarly * 4 * KW; job < njobs; job += 4 * KW) {
+      const int m = job / nb, b = job - m * nb;
+      const PrologueIn in = prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128,
+                                          mm.suh, row0 + b * 128, lane);
+      float v0, v1;
+      prologue_finish(in, p.x_dtype, lane, v0, v1);
+      xs[m * nrows + b * 128 + lane] = (_Float16)v0;
+      xs[m * nrows + b * 128 + lane + 64] = (_Float16)v1;
     }
   }
   __syncthreads();
@@ -522,6 +536,14 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
       v1 += load_coherent(ps + lane + 64);
     }
   };
+  if (!MULTI && !p.glu.on) {
+    for (int m = wave; m < M; m += 4 * KW) {
+      float v0, v1;
+      sum_row(m, cblk * 128, v0, v1);
+      finish_row128(v0, v1, lane, colb_l, mm.svh, mm.bias, mm.y, p.y_dtype, (size_t)m * mm.out);
+    }
+    return;
+  }
   if (!p.glu.on) {
     // rows in batches of 4 per wave: the split sums of a batch load together
     // (each row still adds its splits in split order)
@@ -533,10 +555,12 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
       for (int sp = 0; sp < p.splits; ++sp) {
 #pragma unroll
         for (int t = 0; t < kRows; ++t) {
-          const int m = min(m0 + t * 4 * KW, M - 1);  // clamped rows are loaded, not stored
-          const float* ps = p.partials + ((size_t)sp * M + m) * TO + cblk * 128;
-          v0[t] += load_coherent(ps + lane);
-          v1[t] += load_coherent(ps + lane + 64);
+          const int m = m0 + t * 4 * KW;
+          if (m < M) {  // wave-uniform
+            const float* ps = p.partials + ((size_t)sp * M + m) * TO + cblk * 128;
+            v0[t] += load_coherent(ps + lane);
+            v1[t] += load_coherent(ps + lane + 64);
+          }
         }
       }
 #pragma unroll

@@ -271,7 +271,8 @@ static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows
     max_blocks = std::max(max_blocks, (s + 1) * nb / p.splits - s * nb / p.splits);
   size_t lds = sizeof(uint16_t) * (size_t)rows * max_blocks * 128;
   const int kwi = kw == 4 ? 2 : kw == 2 ? 1 : 0;
-  const QmvFn fn = rows == 1 && kw == 1 ? kQmvSingle[g.k - 1][g.cb] : kQmv[kwi][g.k - 1][g.cb];
+  const bool single = rows == 1 && kw == 1 && !glu.on && !p.mem[0].xhat;
+  const QmvFn fn = single ? kQmvSingle[g.k - 1][g.cb] : kQmv[kwi][g.k - 1][g.cb];
   fn(p, dim3(g.total_out / 128, p.splits), lds, stream);
   return check_launch("EXL3 QMV launch");
 }

@@ -312,8 +312,9 @@ __device__ __forceinline__ void pair_prologue_row(const void* x, int x_dtype, si
 // KW waves share each column pair and split the workgroup's K-range between
 // them (reduced through LDS in a fixed order), so a workgroup of 4*KW waves
 // amortises one prologue over KW times more weight stream.
-// MULTI = false is the single-row variant (the batch-1 decode): no batched
-// prologue or epilogue code, and never a separate prologue.
+// MULTI = false is the single-row variant of a plain launch (the batch-1
+// decode): no batched prologue or epilogue code, no separate prologue and no
+// SwiGLU edge.
 template <int K, int CB, int KW, bool MULTI>
 __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   extern __shared__ __attribute__((aligned(16))) _Float16 xs[];  // [M][rows of split]
@@ -508,8 +509,9 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   // partial store of the workgroup before its counter increment.
   // A SwiGLU group finishes a column block once both members' splits are in
   // (one counter per block pair).
-  const int arrivals = p.glu.on ? 2 * p.splits : p.splits;
-  const int cidx = p.glu.on ? cblk_l : cblk;
+  const bool glu = MULTI && p.glu.on;
+  const int arrivals = glu ? 2 * p.splits : p.splits;
+  const int cidx = glu ? cblk_l : cblk;
   if (arrivals > 1) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -536,7 +538,7 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
       v1 += load_coherent(ps + lane + 64);
     }
   };
-  if (!MULTI && !p.glu.on) {
+  if constexpr (!MULTI) {  // the plain single-row epilogue (no SwiGLU edge)
     for (int m = wave; m < M; m += 4 * KW) {
       float v0, v1;
       sum_row(m, cblk * 128, v0, v1);

@@ -1,0 +1,142 @@
+"""Parity at the measurement plan's full shapes (the configurations bench.py
+times), against the CPU oracle.
+
+* C2 (QMM prefill): {4096->14336, 14336->4096} x K{3,5} x M{128, 2048}, 1 %
+  x20 outlier channels.  Rows of a QMM are independent of each other, so the
+  oracle is run on a handful of rows of the full-size call;
+* C5 (verify block, MCG): 5120->27648 and 27648->5120 at M = 4 and 16, K = 2
+  and 4, all rows vs the oracle (these go through the multi-row QMV with its
+  separate prologue launch);
+* C3 (chained dense layers): two chained Llama-style layers
+  (a=rms(x); q,k,v=W a; h=x+W_o rms(q); b=rms(h); u=swiglu(W_g b, W_u b);
+  x'=h+W_d rms(u)) on the GPU against the same chain with the oracle's linears
+  and swiglu.
+Tolerances: the linear's (max-abs <= 2 f16 ulp of max|y|, rel L2 <= 1e-3);
+the chain accumulates rounding differences through rms and f16 casts, so it is
+held to rel L2 <= 5e-3 and max-abs <= 5e-2 of rms(x').
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from mlxl3_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL_REL = 1e-3
+TOL_ULP = 2
+
+
+def torch_mod():
+    import torch
+
+    return torch
+
+
+def dev(a):
+    torch = torch_mod()
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def layer(seed, tid, n_in, n_out, k, cb, out_scale=1.0):
+    import mlxl3_amd
+
+    tr, suh, svh, _ = synth.linear_layer(seed, tid, n_in, n_out, k)
+    if out_scale != 1.0:
+        svh = (svh.astype(np.float32) * out_scale).astype(np.float16)
+    return mlxl3_amd.Exl3Linear(dev(tr), dev(suh), dev(svh), None, k, cb), (tr, suh, svh, k, cb)
+
+
+def check(y, ref, label):
+    y = np.asarray(y, np.float64)
+    r = np.asarray(ref, np.float64)
+    rel = np.linalg.norm(y - r) / np.linalg.norm(r)
+    ulps = np.abs(y - r).max() / float(np.spacing(np.float16(np.abs(r).max())))
+    print(f"{label}: rel_l2={rel:.3e} max_abs={ulps:.2f} ulp", flush=True)
+    assert rel <= TOL_REL and ulps <= TOL_ULP, (label, rel, ulps)
+
+
+@pytest.mark.parametrize("n_in, n_out", [(4096, 14336), (14336, 4096)])
+@pytest.mark.parametrize("k", [3, 5])
+@pytest.mark.parametrize("rows", [128, 2048])
+def test_c2_qmm_full_shape(n_in, n_out, k, rows):
+    torch = torch_mod()
+    print(f"C2 {n_in}x{n_out} K={k} M={rows}", flush=True)
+    lin, (tr, suh, svh, _, _) = layer(2, k, n_in, n_out, k, 0)
+    x = synth.activations(2, rows, rows, n_in, outlier_frac=0.01)
+    y = lin.forward(torch.from_numpy(x).cuda())
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    assert np.isfinite(y).all()
+    pick = np.array([0, rows // 3, rows - 1])
+    ref = oracle.forward(x[pick], tr, suh, svh, k, 0, mode=1)
+    check(y[pick], ref, f"C2 {n_in}x{n_out} K{k} M{rows} rows{pick.tolist()}")
+
+
+@pytest.mark.parametrize("n_in, n_out", [(5120, 27648), (27648, 5120)])
+@pytest.mark.parametrize("k", [2, 4])
+@pytest.mark.parametrize("rows", [4, 16])
+def test_c5_verify_block_full_shape(n_in, n_out, k, rows):
+    torch = torch_mod()
+    print(f"C5 {n_in}x{n_out} K={k} M={rows}", flush=True)
+    lin, (tr, suh, svh, _, _) = layer(5, k, n_in, n_out, k, 1)
+    x = synth.activations(5, rows, rows, n_in)
+    y = lin.forward(torch.from_numpy(x).cuda())
+    torch.cuda.synchronize()
+    check(y.cpu().numpy(), oracle.forward(x, tr, suh, svh, k, 1, mode=1),
+          f"C5 {n_in}x{n_out} K{k} M{rows}")
+
+
+def rms_np(v):
+    v = v.astype(np.float32)
+    return (v / np.sqrt(np.mean(v * v, axis=-1, keepdims=True) + np.float32(1e-6))).astype(np.float16)
+
+
+def test_c3_two_chained_layers():
+    import mlxl3_amd
+
+    torch = torch_mod()
+    hid, inter, kv = 4096, 14336, 1024
+    layers, host = [], []
+    for l in range(2):
+        seed = 3 * 1000 + l
+        q, hq = layer(seed, 1, hid, hid, 4, 0)
+        kk, hk = layer(seed, 2, hid, kv, 4, 0)
+        v, hv = layer(seed, 3, hid, kv, 4, 0)
+        o, ho = layer(seed, 4, hid, hid, 4, 0)
+        g, hg = layer(seed, 5, hid, inter, 4, 0, out_scale=1 / 64)
+        u, hu = layer(seed, 6, hid, inter, 4, 0, out_scale=1 / 64)
+        d, hd = layer(seed, 7, inter, hid, 4, 0)
+        layers.append((mlxl3_amd.Exl3Group([q, kk, v]), o, mlxl3_amd.Exl3Group([g, u]), d))
+        host.append((hq, ho, hg, hu, hd))
+    x0 = synth.activations(3, 0, 1, hid).astype(np.float32)
+
+    def rms_t(t):
+        t = t.float()
+        return (t / torch.sqrt(t.pow(2).mean(-1, keepdim=True) + 1e-6)).half()
+
+    x = torch.from_numpy(x0).cuda()
+    for qkv, o, gu, d in layers:
+        qq, _, _ = qkv(rms_t(x))
+        h = x + o(rms_t(qq)).float()
+        gg, uu = gu(rms_t(h))
+        x = h + d(rms_t(mlxl3_amd.swiglu(gg, uu))).float()
+    torch.cuda.synchronize()
+    y = x.cpu().numpy()
+
+    def lin(xh, p):
+        return oracle.forward(xh, p[0], p[1], p[2], p[3], p[4], mode=1)
+
+    xr = x0.copy()
+    for hq, ho, hg, hu, hd in host:
+        qq = lin(rms_np(xr), hq)
+        h = xr + lin(rms_np(qq), ho).astype(np.float32)
+        b = rms_np(h)
+        xr = h + lin(rms_np(oracle.swiglu(lin(b, hg), lin(b, hu))), hd).astype(np.float32)
+    rel = np.linalg.norm(y - xr) / np.linalg.norm(xr)
+    mx = np.abs(y - xr).max() / np.sqrt(np.mean(xr ** 2))
+    print(f"C3 2-layer chain: rel_l2={rel:.3e} max_abs/rms={mx:.3e}", flush=True)
+    assert np.isfinite(y).all() and rel <= 5e-3 and mx <= 5e-2, (rel, mx)

@@ -240,8 +240,9 @@ __global__ __launch_bounds__(256 * NPROJ) void moe_mm_kernel(MoeMmParams p) {
   const uint32_t* tp =
       p.trellis + ((size_t)(4 * qa + g) * p.tn_total + tcol) * (8 * K) + (size_t)j * K;
   const int prev_off = j == 0 ? 8 * K - 1 : -1;
-  // A loader: each thread moves kPer 16-byte chunks of a step (rows past the
-  // block's end repeat its last row; their sums are never used)
+  // A loader: each thread moves kPer 16-byte chunks of a step.  Only the
+  // block's row groups are moved (rows past the block's end inside its last
+  // group repeat its last row; their sums are never used).
   constexpr int kThreads = 256 * NPROJ, kChunks = NPROJ * kRows * 8;
   constexpr int kPer = (kChunks + kThreads - 1) / kThreads;
   const uint16_t* lsrc[kPer];
@@ -250,7 +251,7 @@ __global__ __launch_bounds__(256 * NPROJ) void moe_mm_kernel(MoeMmParams p) {
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int c = threadIdx.x + i * kThreads;
-    lact[i] = c < kChunks;
+    lact[i] = c < kChunks && (c / 8) % kRows < 16 * groups;
     const int cc = lact[i] ? c : 0;
     const int pj = cc / (kRows * 8), row = (cc / 8) % kRows, ch = cc & 7;
     lsrc[i] = p.xa + ((size_t)pj * p.slots_pad + pos0 + min(row, nrows - 1)) * p.k_in +

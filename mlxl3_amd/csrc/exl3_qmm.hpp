@@ -8,22 +8,22 @@
 // MFMAs of the other:
 //  * producer w decodes, per step of 64 input rows (4 tile rows), the 8 tiles
 //    of output tiles 2w, 2w+1 into MFMA B fragments and stores them in LDS in
-//    fragment order (one ds_write_b128 per fragment, conflict-free); its
-//    trellis slices are loaded two steps ahead;
+//    fragment order (one ds_write_b128 per fragment, conflict-free), and
+//    copies consumer w's A rows (xhat) into LDS; trellis slices are loaded
+//    four steps ahead, A rows two;
 //  * consumer w owns 16*MB rows and multiplies them by all 16 fragments of the
-//    step, with A fragments read from the f16 xhat rows one step ahead.
-// Two LDS buffers and one workgroup barrier per step: producers fill buffer
-// (q+1)&1 while consumers read buffer q&1.  Each weight is decoded once per
-// 64*MB rows.
+//    step, reading the next fragment group while the current group's MFMAs
+//    issue.
+// Three LDS stages and one workgroup barrier per step: producers fill step
+// q+2 while consumers multiply step q.  Each weight is decoded once per 64*MB
+// rows.
 //
-// The accumulators of a consumer hold whole 128-column blocks of its rows, so
-// the output epilogue (f16 -> H128 -> * svh -> cast, linear.rs:1940-1963)
-// runs in registers: column c of the block sits at lane bits (c & 7) and bit 4
-// of c, register index (c >> 3) & 1 and c >> 5, and the Hadamard stages
-// become lane swizzles for strides 1, 2, 4, 16 and register pairs for 8, 32,
-// 64.  With a global split-K the K-ranges leave f32 partials (exchanged with
-// agent-scope relaxed atomics, as in the QMV) and the last workgroup of an
-// output tile adds them in split order, so results do not depend on timing.
+// After the loop the consumers round their accumulators to f16 rows in LDS and
+// all 8 waves run the output epilogue (f16 -> staged H128 -> * svh -> cast,
+// linear.rs:1940-1963) with 8 consecutive columns per lane.  With a global
+// split-K the K-ranges leave f32 partials (exchanged with agent-scope relaxed
+// atomics, as in the QMV) and the last workgroup of an output tile adds them
+// in split order, so results do not depend on timing.
 #pragma once
 
 #include "exl3_device.hpp"

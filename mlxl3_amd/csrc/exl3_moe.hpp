@@ -383,17 +383,34 @@ __global__ __launch_bounds__(256 * NPROJ) void moe_mm_kernel(MoeMmParams p) {
   if (!s_last) return;  // uniform
   if (threadIdx.x == 0)
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // split sums in split order; the loads of kSplitChunk / NPROJ splits go out
+  // together
+  constexpr int kChunk = kSplitChunk / NPROJ;
   for (int m = wave; m < nrows; m += 4 * NPROJ) {
     float v[NPROJ][2] = {};
-    for (int s = 0; s < p.splits; ++s)
+    for (int s0 = 0; s0 < p.splits; s0 += kChunk) {
+      float t[kChunk][NPROJ][2];
 #pragma unroll
-      for (int pj = 0; pj < NPROJ; ++pj) {
-        const float* src = p.partials +
-                           ((size_t)(s * NPROJ + pj) * p.slots_pad + pos0 + m) * p.width +
-                           cblk * 128;
-        v[pj][0] += load_coherent(src + lane);
-        v[pj][1] += load_coherent(src + lane + 64);
+      for (int c = 0; c < kChunk; ++c) {
+        const int s = min(s0 + c, p.splits - 1);  // clamped: always a written split
+#pragma unroll
+        for (int pj = 0; pj < NPROJ; ++pj) {
+          const float* src = p.partials +
+                             ((size_t)(s * NPROJ + pj) * p.slots_pad + pos0 + m) * p.width +
+                             cblk * 128;
+          t[c][pj][0] = load_coherent(src + lane);
+          t[c][pj][1] = load_coherent(src + lane + 64);
+        }
       }
+#pragma unroll
+      for (int c = 0; c < kChunk; ++c)
+        if (s0 + c < p.splits)
+#pragma unroll
+          for (int pj = 0; pj < NPROJ; ++pj) {
+            v[pj][0] += t[c][pj][0];
+            v[pj][1] += t[c][pj][1];
+          }
+    }
     moe_finish_row<GLU>(p, e, pos0 + m, cblk, v[0][0], v[0][1], v[NPROJ - 1][0],
                         v[NPROJ - 1][1], lane);
   }

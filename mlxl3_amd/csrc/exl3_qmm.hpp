@@ -436,24 +436,37 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
       __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // the tile's rows: sum of every split's partial in split order (this
     // workgroup's own included, read back from memory), f16 into LDS; each
-    // wave takes 8*MB rows, each lane 4 consecutive columns... as 2 pairs
+    // wave takes 8*MB rows, each lane 16 consecutive columns of one row.  The
+    // 16 loads of a split go out together, two splits at a time.
     const int colb = cblk * 128;
+    constexpr int kChunk = 2;
     for (int i = 0; i < MB; ++i) {
       const int rl = wave * 8 * MB + 8 * i + (lane >> 3);  // tile row
       const int row = mtile * 64 * MB + rl;
       const int lrow = row < p.M ? row : p.M - 1;  // in-bounds loads for padding rows
       const int c0 = (lane & 7) * 16;
       uint32_t* yw = (uint32_t*)(ys + rl * kYStride + c0);
+      float sum[16];
 #pragma unroll
-      for (int j = 0; j < 16; j += 2) {
-        float s0 = 0.f, s1 = 0.f;
-        for (int s = 0; s < p.splits; ++s) {
-          const float* ps = p.partials + ((size_t)s * p.M + lrow) * TO + colb + c0 + j;
-          s0 += load_coherent(ps);
-          s1 += load_coherent(ps + 1);
+      for (int jj = 0; jj < 16; ++jj) sum[jj] = 0.f;
+      for (int s0 = 0; s0 < p.splits; s0 += kChunk) {
+        float v[kChunk][16];
+#pragma unroll
+        for (int c = 0; c < kChunk; ++c) {
+          const int s = min(s0 + c, p.splits - 1);  // clamped: always a written split
+          const float* ps = p.partials + ((size_t)s * p.M + lrow) * TO + colb + c0;
+#pragma unroll
+          for (int jj = 0; jj < 16; ++jj) v[c][jj] = load_coherent(ps + jj);
         }
-        yw[j >> 1] = (uint32_t)f2h(s0) | ((uint32_t)f2h(s1) << 16);
+#pragma unroll
+        for (int c = 0; c < kChunk; ++c)
+          if (s0 + c < p.splits)
+#pragma unroll
+            for (int jj = 0; jj < 16; ++jj) sum[jj] += v[c][jj];
       }
+#pragma unroll
+      for (int j = 0; j < 16; j += 2)
+        yw[j >> 1] = (uint32_t)f2h(sum[j]) | ((uint32_t)f2h(sum[j + 1]) << 16);
     }
   }
   __syncthreads();

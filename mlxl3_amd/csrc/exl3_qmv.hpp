@@ -30,6 +30,9 @@ namespace exl3 {
 template <int K>
 constexpr int kQmvDepth = K <= 4 ? 4 : 2;
 
+// Split-K sums load this many splits' partials together.
+constexpr int kSplitChunk = 8;
+
 // Split-K partials cross workgroups (and XCDs): agent-scope relaxed atomics.
 __device__ __forceinline__ void store_coherent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -529,13 +532,27 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
     __syncthreads();
   }
   const int colb_l = cblk_l * 128;
+  // Split sums: the loads of kSplitChunk splits go out together (one round
+  // trip to the coherence point per chunk, not per split); the adds stay in
+  // split order.
   auto sum_row = [&](int m, int colg, float& v0, float& v1) {
     v0 = 0.f;
     v1 = 0.f;
-    for (int s = 0; s < p.splits; ++s) {
-      const float* ps = p.partials + ((size_t)s * M + m) * TO + colg;
-      v0 += load_coherent(ps + lane);
-      v1 += load_coherent(ps + lane + 64);
+    for (int s0 = 0; s0 < p.splits; s0 += kSplitChunk) {
+      float a[kSplitChunk], b[kSplitChunk];
+#pragma unroll
+      for (int i = 0; i < kSplitChunk; ++i) {
+        const int s = min(s0 + i, p.splits - 1);  // clamped: always a written split
+        const float* ps = p.partials + ((size_t)s * M + m) * TO + colg;
+        a[i] = load_coherent(ps + lane);
+        b[i] = load_coherent(ps + lane + 64);
+      }
+#pragma unroll
+      for (int i = 0; i < kSplitChunk; ++i)
+        if (s0 + i < p.splits) {
+          v0 += a[i];
+          v1 += b[i];
+        }
     }
   };
   if constexpr (!MULTI) {  // the plain single-row epilogue (no SwiGLU edge)
@@ -547,23 +564,35 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
     return;
   }
   if (!p.glu.on) {
-    // rows in batches of 4 per wave: the split sums of a batch load together
-    // (each row still adds its splits in split order)
-    constexpr int kRows = 4;
+    // rows in batches of 4 per wave: the split sums of a batch load together,
+    // kRowChunk splits at a time (each row still adds its splits in split
+    // order)
+    constexpr int kRows = 4, kRowChunk = kSplitChunk / 2;
     for (int m0 = wave; m0 < M; m0 += kRows * 4 * KW) {
       float v0[kRows], v1[kRows];
 #pragma unroll
       for (int t = 0; t < kRows; ++t) v0[t] = v1[t] = 0.f;
-      for (int sp = 0; sp < p.splits; ++sp) {
+      for (int s0 = 0; s0 < p.splits; s0 += kRowChunk) {
+        float a[kRowChunk][kRows], b[kRowChunk][kRows];
 #pragma unroll
-        for (int t = 0; t < kRows; ++t) {
-          const int m = m0 + t * 4 * KW;
-          if (m < M) {  // wave-uniform
+        for (int i = 0; i < kRowChunk; ++i) {
+          const int sp = min(s0 + i, p.splits - 1);  // clamped: always a written split
+#pragma unroll
+          for (int t = 0; t < kRows; ++t) {
+            const int m = min(m0 + t * 4 * KW, M - 1);  // clamped: always a written row
             const float* ps = p.partials + ((size_t)sp * M + m) * TO + cblk * 128;
-            v0[t] += load_coherent(ps + lane);
-            v1[t] += load_coherent(ps + lane + 64);
+            a[i][t] = load_coherent(ps + lane);
+            b[i][t] = load_coherent(ps + lane + 64);
           }
         }
+#pragma unroll
+        for (int i = 0; i < kRowChunk; ++i)
+          if (s0 + i < p.splits)
+#pragma unroll
+            for (int t = 0; t < kRows; ++t) {
+              v0[t] += a[i][t];
+              v1[t] += b[i][t];
+            }
       }
 #pragma unroll
       for (int t = 0; t < kRows; ++t) {

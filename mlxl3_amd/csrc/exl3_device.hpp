@@ -57,12 +57,6 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 
 enum : int { DT_F16 = 9, DT_F32 = 10, DT_BF16 = 12 };
 
-__device__ __forceinline__ float load_act(const void* p, int dt, size_t i) {
-  if (dt == DT_F16) return h2f(((const uint16_t*)p)[i]);
-  if (dt == DT_BF16) return bf2f(((const uint16_t*)p)[i]);
-  return ((const float*)p)[i];
-}
-
 // Output conversion of the linear epilogue (linear.rs:992-997): the f16 value
 // is cast to the activation dtype, then the f16 bias is added in that dtype.
 __device__ __forceinline__ void store_out(void* p, int dt, size_t i, float v16, const uint16_t* bias,

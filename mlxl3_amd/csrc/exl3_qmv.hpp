@@ -86,48 +86,11 @@ __device__ __forceinline__ void load_slice_prev_s(const char* sbase, uint32_t lo
   }
 }
 
-// Load the K words of this lane's slice of a tile.
-template <int K>
-__device__ __forceinline__ void load_slice(const uint32_t* __restrict__ p, uint32_t (&w)[K]) {
-  if constexpr (K == 4) {
-    u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
-    w[0] = v[0], w[1] = v[1], w[2] = v[2], w[3] = v[3];
-  } else if constexpr (K == 8) {
-    u32x4 v0 = __builtin_nontemporal_load((const u32x4*)p);
-    u32x4 v1 = __builtin_nontemporal_load((const u32x4*)p + 1);
-    w[0] = v0[0], w[1] = v0[1], w[2] = v0[2], w[3] = v0[3];
-    w[4] = v1[0], w[5] = v1[1], w[6] = v1[2], w[7] = v1[3];
-  } else {
-#pragma unroll
-    for (int i = 0; i < K; ++i) w[i] = __builtin_nontemporal_load(p + i);
-  }
-}
-
 // Decode the 4 B fragments of one 8-tile load and run the 4 MFMAs.  B[0] is
 // the previous lane's last word of the same tile, B[1..K] the lane's words.
 template <int K, int CB>
 __device__ __forceinline__ void qmv_step_prev(const uint32_t (&B)[K + 1], half8 a0, half8 a1,
                                               float4v& acc0, float4v& acc1) {
-  uint32_t src[32];
-  extract_states<K>(B, src);
-  half8 b00 = decode_fragment<CB, K, 0, 0>(src);
-  half8 b01 = decode_fragment<CB, K, 0, 1>(src);
-  acc0 = mfma16(a0, b00, acc0);
-  acc1 = mfma16(a0, b01, acc1);
-  half8 b10 = decode_fragment<CB, K, 1, 0>(src);
-  half8 b11 = decode_fragment<CB, K, 1, 1>(src);
-  acc0 = mfma16(a1, b10, acc0);
-  acc1 = mfma16(a1, b11, acc1);
-}
-
-// Decode the 4 B fragments of one 8-tile load and run the 4 MFMAs.
-template <int K, int CB>
-__device__ __forceinline__ void qmv_step(const uint32_t (&w)[K], int lane, half8 a0, half8 a1,
-                                         float4v& acc0, float4v& acc1) {
-  uint32_t B[K + 1];
-  B[0] = prev_word(w[K - 1], lane);
-#pragma unroll
-  for (int i = 0; i < K; ++i) B[i + 1] = w[i];
   uint32_t src[32];
   extract_states<K>(B, src);
   half8 b00 = decode_fragment<CB, K, 0, 0>(src);
@@ -220,11 +183,6 @@ __device__ __forceinline__ void prologue_finish(const PrologueIn& in, int x_dtyp
   h128_wave<true>(v0, v1, lane);
   v0 = round_f16(v0 * kHadScale);
   v1 = round_f16(v1 * kHadScale);
-}
-__device__ __forceinline__ void prepare_row128(const void* x, int x_dtype, size_t off,
-                                               const uint16_t* __restrict__ suh, int e0, int lane,
-                                               float& v0, float& v1) {
-  prologue_finish(prologue_load(x, x_dtype, off, suh, e0, lane), x_dtype, lane, v0, v1);
 }
 
 // Prologue in the pair layout (lane holds elements 2*lane and 2*lane+1 of a

@@ -14,7 +14,10 @@ Protocol:
 * value = algorithmic bytes per step / time per step, bytes =
   in*out*K/8 + M*in*2 + M*out*2 + in*2 + out*2 (each tensor once);
 * cpu_baseline: the C oracle (oracle/, decode-at-use GEMV, OpenMP) on the same
-  shape on this host's cores, over a bounded sample.
+  shape on this host's cores, over a bounded sample;
+* ceilings (reference only): this GPU's measured streaming-read bandwidth over
+  4 GiB and a dense fp16 GEMM (M=512) / GEMV (M=1) at the same shape through
+  torch's library kernels, next to the spec peaks the roofline fractions use.
 
     python bench.py [--gpus 1] [--steps 2000] [--warmup 200]
 """
@@ -549,6 +552,58 @@ def _c5_layers(gen, steps, warmup):
     return res
 
 
+def ceilings_leg(n_in, n_out):
+    """Measured ceilings of this GPU, reported next to the spec peaks as
+    reference only (library kernels through torch, not this build's code): a
+    streaming read of 4 GiB (a reduction), a dense fp16 GEMM at the QMM shape
+    (M=512, hipBLASLt) and a dense fp16 GEMV at the batch-1 shape, the latter
+    rotating over weight copies that together exceed the 256 MB last-level
+    cache so every call streams its weights from HBM."""
+    import torch
+
+    def timed(fn, reps):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        b.synchronize()
+        return a.elapsed_time(b) / reps  # ms
+
+    big = torch.ones(2 << 30, dtype=torch.float16, device="cuda")  # 4 GiB
+    as_i64 = big.view(torch.int64)
+    read_ms = min(timed(lambda: big.sum(dtype=torch.float32), 10),
+                  timed(lambda: torch.amax(as_i64), 10))  # the faster of two reductions
+    read_gbs = big.numel() * 2 / (read_ms * 1e-3) / 1e9
+    del big, as_i64
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    w = torch.randn(n_in, n_out, device="cuda", generator=gen).half()
+    xm = torch.randn(512, n_in, device="cuda", generator=gen).half()
+    gemm_ms = timed(lambda: torch.matmul(xm, w), 50)
+    copies = [w] + [torch.randn(n_in, n_out, device="cuda", generator=gen).half() for _ in range(3)]
+    x1 = torch.randn(1, n_in, device="cuda", generator=gen).half()
+    state = {"i": 0}
+
+    def gemv():
+        state["i"] = (state["i"] + 1) % len(copies)
+        torch.matmul(x1, copies[state["i"]])
+
+    gemv_ms = timed(gemv, 200)
+    res = {
+        "stream_read_gbs": round(read_gbs, 1),
+        "fp16_gemm_m512_tflops": round(2.0 * 512 * n_in * n_out / (gemm_ms * 1e-3) / 1e12, 1),
+        "fp16_gemv_m1_gbs": round(n_in * n_out * 2 / (gemv_ms * 1e-3) / 1e9, 1),
+        "shape": f"{n_in}x{n_out}",
+        "source": "torch reduction / hipBLASLt GEMM and GEMV, reference only",
+    }
+    del w, xm, copies, x1
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -560,6 +615,8 @@ def main():
     ap.add_argument("--no-mlp", action="store_true", help="skip the dense SwiGLU MLP leg")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the C1/C2-sweep/C3/C5 configuration legs")
+    ap.add_argument("--no-ceilings", action="store_true",
+                    help="skip the measured stream-read / fp16 GEMM / GEMV reference ceilings")
     ap.add_argument("--k", type=int, default=4)
     ap.add_argument("--cb", type=int, default=0)
     ap.add_argument("--in-features", type=int, default=4096)
@@ -660,6 +717,8 @@ def main():
         result["mlp_m512"] = mlp_leg(max(24, args.steps // 40), max(4, args.warmup // 40), rows=512)
     if not args.no_configs:
         result["configs"] = configs_leg(args.steps, args.warmup)
+    if not args.no_ceilings:
+        result["ceilings"] = ceilings_leg(n_in, n_out)
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(n_in, n_out, k, cb, rows)

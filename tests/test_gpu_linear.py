@@ -243,6 +243,31 @@ def test_c1_full_size_qmv():
     check(y, oracle.forward(x, tr, suh, svh, 4, 0, mode=0), TOL_MODE0_REL, TOL_MODE0_ULP, "C1 mode0")
 
 
+@pytest.mark.parametrize("rows", [1, 5, 16, 17, 40])
+@pytest.mark.parametrize("k,cb", [(4, 0), (2, 1), (3, 2)])
+def test_smallest_shape(rows, k, cb):
+    """in = out = 128: one Hadamard block, one column block, one K-split, on
+    both sides of the QMV/QMM boundary (M = 16 / 17)."""
+    lin, (tr, suh, svh, _) = make_layer(6200 + rows + k, 128, 128, k, cb)
+    x = synth.activations(10, rows + k, rows, 128)
+    y = run(lin, x).cpu().numpy()
+    check(y, oracle.forward(x, tr, suh, svh, k, cb, mode=1), TOL_MODE1_REL, TOL_MODE1_ULP,
+          f"128x128 M={rows} k{k} cb{cb}")
+
+
+def test_qmm_long_prefill_rows():
+    """NS shape at M = 4096 (16 row tiles of 256 rows, 1792 workgroups): rows at
+    the start, a tile boundary and the end vs the oracle."""
+    lin, (tr, suh, svh, _) = make_layer(6300, 4096, 14336, 4, 0)
+    rows = 4096
+    x = synth.activations(11, 0, rows, 4096, outlier_frac=0.01)
+    y = run(lin, x).cpu().numpy()
+    assert np.isfinite(y).all()
+    pick = np.array([0, 255, 256, 2049, rows - 1])
+    check(y[pick], oracle.forward(x[pick], tr, suh, svh, 4, 0, mode=1), TOL_MODE1_REL,
+          TOL_MODE1_ULP, f"NS M={rows} rows {pick.tolist()}")
+
+
 def test_invalid_input_raises_without_launch():
     import mlxl3_amd
 

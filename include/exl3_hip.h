@@ -111,6 +111,13 @@ int exl3_group_forward(const exl3_linear* const* parts, int32_t count, const voi
 int exl3_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t count,
                 void* stream);
 
+/* Array::geglu, native/ffi/mlx_bridge.cpp:764-774: out[i] =
+ * (0.5g * (1 + tanh(0.7978845608 * (g + 0.044715 * g^3)))) * u of f16
+ * gate[i], up[i] with f16 constants, every operation rounded to f16 (pow and
+ * tanh rounded once from their binary64 values). */
+int exl3_geglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t count,
+               void* stream);
+
 /* Dense SwiGLU MLP of a decoder layer, qwen35.rs:303-307 (Exl3Group of
  * gate/up, Array::swiglu, down Exl3Linear::forward): y[rows][down.out] =
  * down(swiglu(gate(x), up(x))), f16 x and y; gate and up share in, out, K and
@@ -133,6 +140,18 @@ int exl3_moe_create(const uint16_t* gu_trellis, const uint16_t* gu_suh, const ui
                     const uint16_t* down_trellis, const uint16_t* down_suh,
                     const uint16_t* down_svh, int32_t in, int32_t hidden, int32_t experts,
                     int32_t top_k, int32_t k, int32_t cb, exl3_moe** out_handle);
+/* Exl3SwitchGlu::new_with_activation with GluActivation::Gelu (moe.rs:838-903,
+ * as from_gemma_checkpoint builds it, :663-680): the same bank layout;
+ * exl3_moe_forward then follows forward_gelu (moe.rs:1087-1153) -- gate and up
+ * as the linear's outputs (staged Hadamard, *svh), Array::geglu, GEGLU
+ * outputs of columns >= logical_hidden set to zero, the down projection's
+ * input prepared as the linear's prologue.  logical_hidden >= hidden zeroes
+ * nothing; logical_hidden <= 0 is rejected. */
+int exl3_moe_create_gelu(const uint16_t* gu_trellis, const uint16_t* gu_suh,
+                         const uint16_t* gu_svh, const uint16_t* down_trellis,
+                         const uint16_t* down_suh, const uint16_t* down_svh, int32_t in,
+                         int32_t hidden, int32_t experts, int32_t top_k, int32_t k, int32_t cb,
+                         int32_t logical_hidden, exl3_moe** out_handle);
 void exl3_moe_destroy(exl3_moe* handle);
 size_t exl3_moe_workspace_bytes(const exl3_moe* handle, int64_t rows);
 
@@ -235,6 +254,12 @@ int exl3_linear_load(const exl3_checkpoint* ckpt, const char* prefix, exl3_linea
  * handle. */
 int exl3_moe_load(const exl3_checkpoint* ckpt, const char* prefix, int32_t experts, int32_t top_k,
                   const char* gate, const char* up, const char* down, exl3_moe** out_handle);
+
+/* Exl3SwitchGlu::from_gemma_checkpoint (moe.rs:663-680): exl3_moe_load with
+ * the gate_proj/up_proj/down_proj names, building a GELU bank as
+ * exl3_moe_create_gelu does. */
+int exl3_moe_load_gemma(const exl3_checkpoint* ckpt, const char* prefix, int32_t experts,
+                        int32_t top_k, int32_t logical_hidden, exl3_moe** out_handle);
 
 #ifdef __cplusplus
 }

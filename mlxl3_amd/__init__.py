@@ -82,11 +82,17 @@ _SIGNATURES = {
     "exl3_group_workspace_bytes": (_sz, [_vp, _i32, _i64]),
     "exl3_group_forward": (_i32, [_vp, _i32, _vp, _i32, _i64, _vp, _vp, _sz, _vp]),
     "exl3_swiglu": (_i32, [_vp, _vp, _vp, _i64, _vp]),
+    "exl3_geglu": (_i32, [_vp, _vp, _vp, _i64, _vp]),
     "exl3_mlp_workspace_bytes": (_sz, [_vp, _vp, _vp, _i64]),
     "exl3_mlp_forward": (_i32, [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _sz, _vp]),
     "exl3_moe_create": (
         _i32,
         [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_vp)],
+    ),
+    "exl3_moe_create_gelu": (
+        _i32,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+         ctypes.POINTER(_vp)],
     ),
     "exl3_moe_destroy": (None, [_vp]),
     "exl3_moe_workspace_bytes": (_sz, [_vp, _i64]),
@@ -113,6 +119,9 @@ _SIGNATURES = {
         _i32,
         [_vp, ctypes.c_char_p, _i32, _i32, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
          ctypes.POINTER(_vp)],
+    ),
+    "exl3_moe_load_gemma": (
+        _i32, [_vp, ctypes.c_char_p, _i32, _i32, _i32, ctypes.POINTER(_vp)],
     ),
 }
 
@@ -470,6 +479,20 @@ def swiglu(gate, up):
     return out
 
 
+def geglu(gate, up):
+    """Array::geglu (native/ffi/mlx_bridge.cpp:764-774): the tanh GELU of gate
+    times up in f16 arithmetic, for f16 device tensors of one shape."""
+    torch = _torch()
+    gate = _require_device(gate, "gate", (torch.float16,))
+    up = _require_device(up, "up", (torch.float16,))
+    if gate.shape != up.shape:
+        raise Exl3Error(-1, "GEGLU operands differ in shape")
+    out = torch.empty_like(gate)
+    _check(load_library().exl3_geglu(_ptr(gate), _ptr(up), _ptr(out), gate.numel(),
+                                     _stream_ptr(gate.device)))
+    return out
+
+
 class Exl3Mlp:
     """The dense SwiGLU MLP of a decoder layer (qwen35.rs:303-307: an Exl3Group
     of gate/up, Array::swiglu, the down Exl3Linear), with the SwiGLU and the
@@ -506,10 +529,14 @@ class Exl3Mlp:
 
 
 class Exl3SwitchGlu:
-    """Exl3SwitchGlu (native/src/moe.rs:611-1085), SiLU experts, grouped expert QMM."""
+    """Exl3SwitchGlu (native/src/moe.rs:611-1153), grouped expert QMM.
+    activation "silu" (new, from_checkpoint, from_lfm_checkpoint) or "gelu"
+    (from_gemma_checkpoint: forward_gelu, GEGLU outputs of the columns from
+    logical_hidden on set to zero; None = the whole hidden width)."""
 
     def __init__(self, gu_trellis, gu_suh, gu_svh, down_trellis, down_suh, down_svh, top_k: int,
-                 k: int, cb: int = Codebook.DEFAULT):
+                 k: int, cb: int = Codebook.DEFAULT, activation: str = "silu",
+                 logical_hidden: Optional[int] = None):
         torch = _torch()
         lib = load_library()
         in_tiles, gu_cols, k16 = gu_trellis.shape
@@ -517,6 +544,10 @@ class Exl3SwitchGlu:
         hidden = gu_svh.shape[-1]
         self.input, self.hidden, self.experts, self.top_k = in_tiles * 16, hidden, experts, int(top_k)
         self.k, self.cb = int(k), int(cb)
+        if activation not in ("silu", "gelu"):
+            raise Exl3Error(-1, f"unknown GLU activation {activation!r}")
+        self.activation = activation
+        self.logical_hidden = hidden if logical_hidden is None else int(logical_hidden)
         self.tensors = [
             _require_device(gu_trellis, "gu_trellis"),
             _require_device(gu_suh, "gu_suh").to(torch.float16).contiguous(),
@@ -526,27 +557,45 @@ class Exl3SwitchGlu:
             _require_device(down_svh, "down_svh").to(torch.float16).contiguous(),
         ]
         h = _vp()
-        _check(
-            lib.exl3_moe_create(
-                *[_ptr(t) for t in self.tensors], self.input, self.hidden, self.experts, self.top_k,
-                self.k, self.cb, ctypes.byref(h),
+        if activation == "gelu":
+            _check(
+                lib.exl3_moe_create_gelu(
+                    *[_ptr(t) for t in self.tensors], self.input, self.hidden, self.experts,
+                    self.top_k, self.k, self.cb, self.logical_hidden, ctypes.byref(h),
+                )
             )
-        )
+        else:
+            _check(
+                lib.exl3_moe_create(
+                    *[_ptr(t) for t in self.tensors], self.input, self.hidden, self.experts,
+                    self.top_k, self.k, self.cb, ctypes.byref(h),
+                )
+            )
         self._handle = h
         self._ws = _Workspace()
 
     @classmethod
     def from_checkpoint(cls, checkpoint: "Checkpoint", prefix: str, experts: int, top_k: int,
-                        names=("gate_proj", "up_proj", "down_proj"), device=None) -> "Exl3SwitchGlu":
+                        names=("gate_proj", "up_proj", "down_proj"), device=None,
+                        logical_hidden: Optional[int] = None) -> "Exl3SwitchGlu":
         """Exl3SwitchGlu::from_checkpoint (moe.rs:629-645, :681-800): experts
-        {prefix}.{e}.{gate,up,down}, assembled into one bank on `device`."""
+        {prefix}.{e}.{gate,up,down}, assembled into one bank on `device`
+        (logical_hidden given: a GELU bank, as from_gemma_checkpoint)."""
         torch = _torch()
         device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
-        gate, up, down = (n.encode() for n in names)
         h = _vp()
         with torch.cuda.device(device):
-            _check(load_library().exl3_moe_load(checkpoint.handle, prefix.encode(), int(experts),
-                                                 int(top_k), gate, up, down, ctypes.byref(h)))
+            if logical_hidden is None:
+                gate, up, down = (n.encode() for n in names)
+                _check(load_library().exl3_moe_load(checkpoint.handle, prefix.encode(),
+                                                     int(experts), int(top_k), gate, up, down,
+                                                     ctypes.byref(h)))
+            else:
+                if tuple(names) != ("gate_proj", "up_proj", "down_proj"):
+                    raise Exl3Error(-1, "GELU banks use the gate_proj/up_proj/down_proj names")
+                _check(load_library().exl3_moe_load_gemma(checkpoint.handle, prefix.encode(),
+                                                          int(experts), int(top_k),
+                                                          int(logical_hidden), ctypes.byref(h)))
         self = cls.__new__(cls)
         self._handle = h
         self._ws = _Workspace()
@@ -558,7 +607,18 @@ class Exl3SwitchGlu:
         base = f"{prefix}.0.{names[0]}"
         self.cb = (Codebook.MUL1 if base + ".mul1" in checkpoint
                    else Codebook.MCG if base + ".mcg" in checkpoint else Codebook.DEFAULT)
+        self.activation = "silu" if logical_hidden is None else "gelu"
+        self.logical_hidden = self.hidden if logical_hidden is None else min(int(logical_hidden),
+                                                                             self.hidden)
         return self
+
+    @classmethod
+    def from_gemma_checkpoint(cls, checkpoint: "Checkpoint", prefix: str, experts: int,
+                              top_k: int, logical_hidden: int, device=None) -> "Exl3SwitchGlu":
+        """Exl3SwitchGlu::from_gemma_checkpoint (moe.rs:663-680): GELU experts
+        whose GEGLU outputs from column logical_hidden on are zero."""
+        return cls.from_checkpoint(checkpoint, prefix, experts, top_k, device=device,
+                                   logical_hidden=logical_hidden)
 
     @classmethod
     def from_lfm_checkpoint(cls, checkpoint: "Checkpoint", prefix: str, experts: int, top_k: int,

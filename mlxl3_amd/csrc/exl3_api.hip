@@ -78,9 +78,9 @@ static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
   // splits 13.9 us)
   s = std::min(s, std::max(1, nb / 4));
   s = std::max(s, min_splits);
-  if (const char* env = getenv("EXL3_QMV_SPLITS")) {  // tuning: any split count
-    int v = atoi(env);
-    if (v >= 1) s = v;
+  if (const char* env = getenv("EXL3_QMV_SPLITS")) {  // tuning: any split count that
+    int v = atoi(env);                                 // keeps xhat within its LDS bound
+    if (v >= 1) s = std::max(v, min_splits);
   }
   s = std::max(1, std::min(s, nb));
   *splits_out = s;
@@ -489,10 +489,8 @@ size_t exl3_mlp_workspace_bytes(const exl3_linear* gate, const exl3_linear* up,
 
 int exl3_workspace_init(void* workspace, size_t bytes, void* stream) {
   if (!workspace || bytes % 4) return fail(EXL3_EINVAL, "workspace must be non-null, 4-byte sized");
-  size_t words = bytes / 4;
-  unsigned blocks = (unsigned)std::min<size_t>((words + 255) / 256, 4096);
-  if (blocks == 0) return EXL3_OK;
-  (void)blocks;
+  const size_t words = bytes / 4;
+  if (words == 0) return EXL3_OK;
   launch_fill_zero((uint32_t*)workspace, words, (hipStream_t)stream);
   return check_launch("workspace init");
 }
@@ -528,8 +526,17 @@ int exl3_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t
   if (count < 0) return fail(EXL3_EINVAL, "negative element count");
   if (count == 0) return EXL3_OK;
   if (!gate || !up || !out) return fail(EXL3_EINVAL, "null SwiGLU buffer");
-  launch_swiglu(gate, up, out, count, (hipStream_t)stream);
+  launch_glu(gate, up, out, count, false, (hipStream_t)stream);
   return check_launch("SwiGLU launch");
+}
+
+int exl3_geglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t count,
+               void* stream) {
+  if (count < 0) return fail(EXL3_EINVAL, "negative element count");
+  if (count == 0) return EXL3_OK;
+  if (!gate || !up || !out) return fail(EXL3_EINVAL, "null GEGLU buffer");
+  launch_glu(gate, up, out, count, true, (hipStream_t)stream);
+  return check_launch("GEGLU launch");
 }
 
 int exl3_decode_tiles(const uint16_t* packed, int64_t tiles, int32_t k, int32_t cb,

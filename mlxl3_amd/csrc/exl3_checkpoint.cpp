@@ -9,6 +9,8 @@
 //                          native/src/linear.rs:454-575
 //   exl3_moe_load          Exl3SwitchGlu::from_checkpoint_names
 //                          native/src/moe.rs:629-800
+//   exl3_moe_load_gemma    Exl3SwitchGlu::from_gemma_checkpoint (GELU)
+//                          native/src/moe.rs:663-680
 //
 // The inspection validates every header before any weight is read (same
 // checks and messages as the reference); payloads are read on request with
@@ -597,8 +599,9 @@ Error load_linear(const exl3_checkpoint* c, const std::string& prefix, exl3_line
 // on the host: gate trellises of experts 0..E-1 then up trellises concatenated
 // along the output-tile axis, down trellises likewise; scales stacked per
 // expert ([E][2][in], [E][2][H], [E][H], [E][in]).
+// logical_hidden > 0: a GELU bank (from_gemma_checkpoint, moe.rs:663-680).
 Error load_moe(const exl3_checkpoint* c, const std::string& prefix, int experts, int top_k,
-               const char* const proj[3], exl3_moe** out) {
+               const char* const proj[3], int logical_hidden, exl3_moe** out) {
   if (!(experts > 0 && top_k > 0 && top_k <= experts &&
         (uint64_t)experts <= c->tensors.size() / 3))
     return invalid("invalid expert count or incomplete expert bank");
@@ -704,8 +707,11 @@ Error load_moe(const exl3_checkpoint* c, const std::string& prefix, int experts,
   if (Error er = up.run(dev)) return er;
   exl3_moe* h = nullptr;
   auto P = [&](int i) { return (const uint16_t*)(dev + o[i]); };
-  int st = exl3_moe_create(P(0), P(1), P(2), P(3), P(4), P(5), (int)in, (int)hidden, experts,
-                           top_k, (int)k, cb, &h);
+  int st = logical_hidden > 0
+               ? exl3_moe_create_gelu(P(0), P(1), P(2), P(3), P(4), P(5), (int)in, (int)hidden,
+                                      experts, top_k, (int)k, cb, logical_hidden, &h)
+               : exl3_moe_create(P(0), P(1), P(2), P(3), P(4), P(5), (int)in, (int)hidden,
+                                 experts, top_k, (int)k, cb, &h);
   if (st != EXL3_OK) {
     (void)hipFree(dev);
     return err(st, exl3_last_error());
@@ -839,7 +845,23 @@ int exl3_moe_load(const exl3_checkpoint* c, const char* prefix, int32_t experts,
   const char* proj[3] = {gate ? gate : "gate_proj", up ? up : "up_proj", down ? down : "down_proj"};
   Error e;
   try {
-    e = load_moe(c, prefix, experts, top_k, proj, out);
+    e = load_moe(c, prefix, experts, top_k, proj, 0, out);
+  } catch (const std::bad_alloc&) {
+    e = err(EXL3_ENOMEM, "out of host memory");
+  }
+  return e ? raise(e) : EXL3_OK;
+}
+
+int exl3_moe_load_gemma(const exl3_checkpoint* c, const char* prefix, int32_t experts,
+                        int32_t top_k, int32_t logical_hidden, exl3_moe** out) {
+  if (!out) return fail(EXL3_EINVAL, "null output handle pointer");
+  *out = nullptr;
+  if (!c || !prefix) return fail(EXL3_EINVAL, "null checkpoint argument");
+  if (logical_hidden <= 0) return fail(EXL3_EINVAL, "invalid logical GLU width");
+  const char* proj[3] = {"gate_proj", "up_proj", "down_proj"};
+  Error e;
+  try {
+    e = load_moe(c, prefix, experts, top_k, proj, logical_hidden, out);
   } catch (const std::bad_alloc&) {
     e = err(EXL3_ENOMEM, "out of host memory");
   }

@@ -37,9 +37,10 @@ void launch_qmv_inner(const uint16_t* values, const uint16_t* x, int rows, int c
 // xhat = the down projection's prologue of swiglu(gate, up), [rows][H].
 void launch_swiglu_prepare(const uint16_t* gate, const uint16_t* up, const uint16_t* down_suh,
                            int H, int rows, uint16_t* xhat, hipStream_t s);
-// out[i] = swiglu(gate[i], up[i]) in f16 (Array::swiglu).
-void launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,
-                   hipStream_t s);
+// out[i] = swiglu(gate[i], up[i]) (Array::swiglu) or geglu(gate[i], up[i])
+// (Array::geglu) in f16.
+void launch_glu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n, bool gelu,
+                hipStream_t s);
 void launch_fill_zero(uint32_t* p, size_t words, hipStream_t s);
 
 // Records the thread-local error message and returns `code`.

@@ -48,7 +48,9 @@ struct exl3_moe {
   const uint16_t *gu_trellis, *gu_suh, *gu_svh;
   const uint16_t *down_trellis, *down_suh, *down_svh;
   int in, hidden, experts, top_k, k, cb;
-  int force_splits;  // EXL3_MOE_SPLITS at create (0: by slot count)
+  int gelu;            // GluActivation::Gelu (forward_gelu) instead of SiLU
+  int logical_hidden;  // GELU: GEGLU outputs of columns >= logical_hidden are zero
+  int force_splits;    // EXL3_MOE_SPLITS at create (0: by slot count)
   void* owned;       // device memory freed with the handle (checkpoint loads), or null
 };
 
@@ -136,9 +138,28 @@ int exl3_moe_create(const uint16_t* gu_trellis, const uint16_t* gu_suh, const ui
   exl3_moe* h = new (std::nothrow) exl3_moe;
   if (!h) return fail(EXL3_ENOMEM, "out of host memory");
   *h = exl3_moe{gu_trellis, gu_suh, gu_svh, down_trellis, down_suh, down_svh,
-                in,         hidden, experts, top_k,       k,        cb,       0, nullptr};
+                in,         hidden, experts, top_k,       k,        cb,
+                0,          hidden, 0,       nullptr};
   if (const char* env = getenv("EXL3_MOE_SPLITS")) h->force_splits = std::max(0, atoi(env));
   *out_handle = h;
+  return EXL3_OK;
+}
+
+int exl3_moe_create_gelu(const uint16_t* gu_trellis, const uint16_t* gu_suh,
+                         const uint16_t* gu_svh, const uint16_t* down_trellis,
+                         const uint16_t* down_suh, const uint16_t* down_svh, int32_t in,
+                         int32_t hidden, int32_t experts, int32_t top_k, int32_t k, int32_t cb,
+                         int32_t logical_hidden, exl3_moe** out_handle) {
+  if (!out_handle) return fail(EXL3_EINVAL, "out_handle is null");
+  *out_handle = nullptr;
+  // forward_gelu zeroes the columns from logical_hidden on only when it is
+  // below hidden (moe.rs:1125-1137); a width of zero or less has no meaning
+  if (logical_hidden <= 0) return fail(EXL3_EINVAL, "invalid logical GLU width");
+  if (int rc = exl3_moe_create(gu_trellis, gu_suh, gu_svh, down_trellis, down_suh, down_svh, in,
+                               hidden, experts, top_k, k, cb, out_handle))
+    return rc;
+  (*out_handle)->gelu = 1;
+  (*out_handle)->logical_hidden = std::min(logical_hidden, hidden);
   return EXL3_OK;
 }
 
@@ -214,6 +235,8 @@ int exl3_moe_forward(const exl3_moe* h, const uint16_t* x, int64_t rows,
   q.gu_svh = h->gu_svh;
   q.down_suh = h->down_suh;
   q.xd = (uint16_t*)(ws + L.xd);
+  q.gelu = h->gelu;
+  q.logical_hidden = h->logical_hidden;
   gateup<<<L.max_blocks * q.col_blocks * q.splits, 512, 0, s>>>(q);
   if (int rc = check_launch("moe gate/up")) return rc;
 

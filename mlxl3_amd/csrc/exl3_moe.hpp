@@ -14,7 +14,8 @@
 //               the QMV -- and multiplies them with the block's rows; the
 //               epilogue is the whole of glu_down_input (moe.rs:435-563): f16,
 //               f32 Hadamard, *scale*svh, SiLU(g)*u, *down_suh, f32 Hadamard,
-//               *scale -> the down projection's xhat;
+//               *scale -> the down projection's xhat (GELU banks,
+//               forward_gelu: staged Hadamards and GEGLU instead);
 //   4. down:    the same kernel with 4 waves over the down bank; the epilogue is
 //               finish_and_reduce's per-slot part (moe.rs:586-609): f16, staged
 //               Hadamard, *svh, *score, stored per slot;
@@ -153,6 +154,8 @@ struct MoeMmParams {
   const uint16_t* gu_svh;   // [E][2][width]
   const uint16_t* down_suh; // [E][width]
   uint16_t* xd;             // [slots_pad][width]
+  int gelu;                 // 0: SiLU (glu_down_input), 1: GELU (forward_gelu)
+  int logical_hidden;       // GELU: outputs of columns >= logical_hidden are zero
   // down epilogue
   const uint16_t* down_svh; // [E][width]
   const uint16_t* scores;   // [slots]
@@ -167,12 +170,34 @@ __device__ __forceinline__ void moe_finish_row(const MoeMmParams& p, int e, int 
                                                int lane) {
   const int col0 = cblk * 128;
   if constexpr (GLU) {
-    // gate and up: f16(raw) -> f32 Hadamard -> f16(v * scale * svh)
-    g0 = round_f16(g0), g1 = round_f16(g1), u0 = round_f16(u0), u1 = round_f16(u1);
-    h128_wave<false>(g0, g1, lane);
-    h128_wave<false>(u0, u1, lane);
     const uint16_t* gsv = p.gu_svh + ((size_t)e * 2) * p.width + col0;
     const uint16_t* usv = gsv + p.width;
+    const uint16_t* dsu = p.down_suh + (size_t)e * p.width + col0;
+    uint16_t* dst = p.xd + (size_t)pos * p.width + col0;
+    g0 = round_f16(g0), g1 = round_f16(g1), u0 = round_f16(u0), u1 = round_f16(u1);
+    if (p.gelu) {  // uniform
+      // forward_gelu (moe.rs:1087-1153): gate and up as expert_mapped returns
+      // them (linear.rs:3325-3331: f16, staged Hadamard, f16(* scale),
+      // f16(* svh)), GEGLU with zeros from logical_hidden on, then the down
+      // input as expert_mapped prepares it (linear.rs:3131-3137: f16(h *
+      // down_suh), staged Hadamard, f16(* scale))
+      h128_wave<true>(g0, g1, lane);
+      h128_wave<true>(u0, u1, lane);
+      g0 = round_f16(round_f16(g0 * kHadScale) * h2f(gsv[lane]));
+      g1 = round_f16(round_f16(g1 * kHadScale) * h2f(gsv[lane + 64]));
+      u0 = round_f16(round_f16(u0 * kHadScale) * h2f(usv[lane]));
+      u1 = round_f16(round_f16(u1 * kHadScale) * h2f(usv[lane + 64]));
+      const float a0 = col0 + lane < p.logical_hidden ? geglu_f16(g0, u0) : 0.f;
+      const float a1 = col0 + lane + 64 < p.logical_hidden ? geglu_f16(g1, u1) : 0.f;
+      float d0 = round_f16(a0 * h2f(dsu[lane])), d1 = round_f16(a1 * h2f(dsu[lane + 64]));
+      h128_wave<true>(d0, d1, lane);
+      dst[lane] = f2h(d0 * kHadScale);
+      dst[lane + 64] = f2h(d1 * kHadScale);
+      return;
+    }
+    // gate and up: f16(raw) -> f32 Hadamard -> f16(v * scale * svh)
+    h128_wave<false>(g0, g1, lane);
+    h128_wave<false>(u0, u1, lane);
     g0 = round_f16(g0 * kHadScale * h2f(gsv[lane]));
     g1 = round_f16(g1 * kHadScale * h2f(gsv[lane + 64]));
     u0 = round_f16(u0 * kHadScale * h2f(usv[lane]));
@@ -180,10 +205,8 @@ __device__ __forceinline__ void moe_finish_row(const MoeMmParams& p, int e, int 
     // SiLU(g) * u, then * down_suh, f32 Hadamard, f16(v * scale)
     const float a0 = round_f16((g0 / (1.0f + expf(-g0))) * u0);
     const float a1 = round_f16((g1 / (1.0f + expf(-g1))) * u1);
-    const uint16_t* dsu = p.down_suh + (size_t)e * p.width + col0;
     float d0 = round_f16(a0 * h2f(dsu[lane])), d1 = round_f16(a1 * h2f(dsu[lane + 64]));
     h128_wave<false>(d0, d1, lane);
-    uint16_t* dst = p.xd + (size_t)pos * p.width + col0;
     dst[lane] = f2h(d0 * kHadScale);
     dst[lane + 64] = f2h(d1 * kHadScale);
   } else {

@@ -12,12 +12,17 @@ namespace exl3 {
   template __global__ void qmm_kernel<K, CB, 4>(QmmParams);
 EXL3_INSTANTIATE(EXL3_QMM_INST)
 
-// out = swiglu(gate, up) elementwise in f16, eight elements per thread
-// where the buffers allow 16-byte access.
-__global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict__ g,
-                                                     const uint16_t* __restrict__ u,
-                                                     uint16_t* __restrict__ o, int64_t n,
-                                                     int vec) {
+// out = swiglu(gate, up) or geglu(gate, up) elementwise in f16, eight
+// elements per thread where the buffers allow 16-byte access.
+template <bool GELU>
+__device__ __forceinline__ float glu_f16(float g, float u) {
+  if constexpr (GELU) return geglu_f16(g, u);
+  else return swiglu_f16(g, u);
+}
+template <bool GELU>
+__global__ __launch_bounds__(256) void glu_kernel(const uint16_t* __restrict__ g,
+                                                  const uint16_t* __restrict__ u,
+                                                  uint16_t* __restrict__ o, int64_t n, int vec) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (vec) {
@@ -26,16 +31,20 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict_
       u32x4 ov;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float lo = swiglu_f16(h2f((uint16_t)gv[j]), h2f((uint16_t)uv[j]));
-        const float hi = swiglu_f16(h2f((uint16_t)(gv[j] >> 16)), h2f((uint16_t)(uv[j] >> 16)));
+        const float lo = glu_f16<GELU>(h2f((uint16_t)gv[j]), h2f((uint16_t)uv[j]));
+        const float hi = glu_f16<GELU>(h2f((uint16_t)(gv[j] >> 16)), h2f((uint16_t)(uv[j] >> 16)));
         ov[j] = (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
       }
       ((u32x4*)o)[i] = ov;
     }
     i = n / 8 * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   }
-  for (; i < n; i += stride) o[i] = f2h(swiglu_f16(h2f(g[i]), h2f(u[i])));
+  for (; i < n; i += stride) o[i] = f2h(glu_f16<GELU>(h2f(g[i]), h2f(u[i])));
 }
+template __global__ void glu_kernel<false>(const uint16_t*, const uint16_t*, uint16_t*, int64_t,
+                                           int);
+template __global__ void glu_kernel<true>(const uint16_t*, const uint16_t*, uint16_t*, int64_t,
+                                          int);
 
 __global__ void fill_zero_kernel(uint32_t* p, size_t words) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -70,12 +79,15 @@ void launch_prologue(const PrologueParams& p, int members, hipStream_t s) {
                      dim3(256), 0, s, p);
 }
 
-void launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,
-                   hipStream_t s) {
+void launch_glu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n, bool gelu,
+                hipStream_t s) {
   const int vec = ((((uintptr_t)gate | (uintptr_t)up | (uintptr_t)out) & 15) == 0) ? 1 : 0;
   const int64_t work = vec ? n / 8 + 8 : n;
   const unsigned blocks = (unsigned)std::min<int64_t>((work + 255) / 256, 4096);
-  hipLaunchKernelGGL(swiglu_kernel, dim3(blocks), dim3(256), 0, s, gate, up, out, n, vec);
+  if (gelu)
+    hipLaunchKernelGGL(glu_kernel<true>, dim3(blocks), dim3(256), 0, s, gate, up, out, n, vec);
+  else
+    hipLaunchKernelGGL(glu_kernel<false>, dim3(blocks), dim3(256), 0, s, gate, up, out, n, vec);
 }
 
 void launch_swiglu_prepare(const uint16_t* gate, const uint16_t* up, const uint16_t* down_suh,

@@ -144,6 +144,34 @@ __device__ __forceinline__ float swiglu_f16(float g, float u) {
   return round_f16(round_f16(g * sigmoid_f16(g)) * u);
 }
 
+// binary64 -> binary16 rounded once to nearest even: round to odd into
+// binary32 (24 >= 11 + 2 bits, so the nearest-even binary32 -> binary16 step
+// that follows cannot round twice).
+__device__ __forceinline__ float round_f16_f64(double d) {
+  float f = (float)d;
+  if ((double)f != d) {
+    uint32_t b = __builtin_bit_cast(uint32_t, f);
+    if (!(b & 1u)) b = fabs((double)f) > fabs(d) ? b - 1u : b + 1u;  // the odd neighbour
+    f = __builtin_bit_cast(float, b);
+  }
+  return round_f16(f);
+}
+
+// GEGLU of f16 operands in f16 arithmetic, the compiled MLX expression of
+// Array::geglu (native/ffi/mlx_bridge.cpp:764-774):
+// (0.5g * (1 + tanh(0.7978845608 * (g + 0.044715 * g^3)))) * u with f16
+// constants; every operation rounds to f16, pow(g, 3) (exact in binary64) and
+// tanh are rounded once from binary64.
+__device__ __forceinline__ float geglu_f16(float g, float u) {
+  const double gd = g;
+  const float cube = round_f16_f64(gd * gd * gd);
+  const float t = round_f16(g + round_f16(round_f16(0.044715f) * cube));
+  const float inner = round_f16(round_f16(0.7978845608028654f) * t);
+  const float th = round_f16_f64(tanh((double)inner));
+  const float gelu = round_f16(round_f16(0.5f * g) * round_f16(1.0f + th));
+  return round_f16(gelu * u);
+}
+
 // Prologue for one row of one 128-input block, split into its loads and its
 // arithmetic so callers can put other memory traffic between the two:
 // xhat = f16(H128(f16(f16(x) * suh)) / sqrt(128)) for elements (lane, lane+64).

@@ -51,6 +51,8 @@ def lib():
         L.exl3o_f32_to_bf16.argtypes = [ctypes.c_float]
         L.exl3o_swiglu.restype = None
         L.exl3o_swiglu.argtypes = [_u16p, _u16p, _u16p, ctypes.c_int64]
+        L.exl3o_geglu.restype = None
+        L.exl3o_geglu.argtypes = [_u16p, _u16p, _u16p, ctypes.c_int64]
         L.exl3o_codeword.restype = ctypes.c_uint16
         L.exl3o_codeword.argtypes = [ctypes.c_uint16, ctypes.c_int]
         L.exl3o_codebook.restype = None
@@ -78,7 +80,7 @@ def lib():
         L.exl3o_moe_forward.argtypes = [_u16p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         _u16p, _u16p, _u16p, _u16p, _u16p, _u16p, _u32p, _u16p,
-                                        _u16p, ctypes.c_int]
+                                        _u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         _lib = L
     return _lib
 
@@ -190,18 +192,26 @@ def forward(x, trellis, suh, svh, k: int, cb: int, bias=None, mode: int = 1, thr
 
 
 def moe_forward(x, selected, scores, gu_trellis, gu_suh, gu_svh, down_trellis, down_suh,
-                down_svh, k: int, cb: int, threads: int = 0) -> np.ndarray:
+                down_svh, k: int, cb: int, threads: int = 0, activation: str = "silu",
+                logical_hidden=None) -> np.ndarray:
+    """Exl3SwitchGlu::forward (moe.rs:905-975) for activation "silu", and
+    forward_gelu (moe.rs:1087-1153) for "gelu" with GEGLU outputs from column
+    logical_hidden on set to zero (None: the whole hidden width)."""
     x = _u16(x)
     rows, n_in = x.shape
     experts, hidden = gu_svh.shape[0], gu_svh.shape[-1]
     top_k = selected.shape[1]
+    if activation not in ("silu", "gelu"):
+        raise ValueError(f"unknown GLU activation {activation!r}")
+    gelu = activation == "gelu"
+    logical = hidden if logical_hidden is None else int(logical_hidden)
     y = np.empty((rows, n_in), np.uint16)
     rc = lib().exl3o_moe_forward(x.ravel(), rows, n_in, hidden, experts, top_k, k, cb,
                                  _u16(gu_trellis).ravel(), _u16(gu_suh).ravel(),
                                  _u16(gu_svh).ravel(), _u16(down_trellis).ravel(),
                                  _u16(down_suh).ravel(), _u16(down_svh).ravel(),
                                  np.ascontiguousarray(selected, np.uint32).ravel(),
-                                 _u16(scores).ravel(), y.ravel(), threads)
+                                 _u16(scores).ravel(), y.ravel(), int(gelu), logical, threads)
     if rc:
         raise ValueError(f"oracle MoE forward failed ({rc})")
     return y.view(np.float16)
@@ -214,6 +224,16 @@ def swiglu(gate, up) -> np.ndarray:
     assert g.shape == u.shape
     out = np.empty_like(g)
     lib().exl3o_swiglu(g.reshape(-1), u.reshape(-1), out.reshape(-1), g.size)
+    return out.view(np.float16)
+
+
+def geglu(gate, up) -> np.ndarray:
+    """Array::geglu (mlx_bridge.cpp:764-774) on f16 arrays of one shape."""
+    g = np.ascontiguousarray(np.asarray(gate, dtype=np.float16)).view(np.uint16)
+    u = np.ascontiguousarray(np.asarray(up, dtype=np.float16)).view(np.uint16)
+    assert g.shape == u.shape
+    out = np.empty_like(g)
+    lib().exl3o_geglu(g.reshape(-1), u.reshape(-1), out.reshape(-1), g.size)
     return out.view(np.float16)
 
 

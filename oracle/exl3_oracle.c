@@ -460,14 +460,35 @@ static void expert_gemv(const float* xin, const uint16_t* trellis, int in, int t
  * f16(silu(g)*u), f16(a*down_suh), f32 H128, f16(v*s)), then finish_and_reduce
  * (moe.rs:586-609: f16(raw) -> MLX f16 H128 -> *svh (f16) -> *score (f16) ->
  * f32 sum over top-k -> f16). */
+/* One element of Array::geglu (native/ffi/mlx_bridge.cpp:764-774): the
+ * compiled MLX expression 0.5g * (1 + tanh(0.7978845608 * (g + 0.044715 g^3)))
+ * * u on float16 arrays.  Every operation rounds to f16 (the constants are
+ * f16 scalars); pow(g, 3) and tanh are rounded once from binary64 (g^3 is
+ * exact there). */
+static float geglu1(float g, float u) {
+    const double gd = g;
+    const float cube = h2f(exl3o_f64_to_f16(gd * gd * gd));
+    const float t = rh(g + rh(rh(0.044715f) * cube));
+    const float inner = rh(rh(0.7978845608028654f) * t);
+    const float th = h2f(exl3o_f64_to_f16(tanh((double)inner)));
+    const float gelu = rh(rh(0.5f * g) * rh(1.0f + th));
+    return rh(gelu * u);
+}
+
+void exl3o_geglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = f2h(geglu1(h2f(gate[i]), h2f(up[i])));
+}
+
 int exl3o_moe_forward(const uint16_t* x, int64_t rows, int in, int hidden, int experts,
                       int top_k, int k, int cb, const uint16_t* gu_trellis,
                       const uint16_t* gu_suh, const uint16_t* gu_svh,
                       const uint16_t* down_trellis, const uint16_t* down_suh,
                       const uint16_t* down_svh, const uint32_t* selected,
-                      const uint16_t* scores, uint16_t* y, int threads) {
+                      const uint16_t* scores, uint16_t* y, int gelu, int logical_hidden,
+                      int threads) {
     if (k < 1 || k > 8 || cb < 0 || cb > 2 || rows < 1 || top_k < 1 || experts < 1) return -1;
     if (in % 128 || hidden % 128 || in <= 0 || hidden <= 0) return -1;
+    if (gelu && logical_hidden <= 0) return -1; /* >= hidden: nothing is zeroed */
     for (int64_t i = 0; i < rows * top_k; ++i)
         if (selected[i] >= (uint32_t)experts) return -1;
     const uint16_t* table = codebook_table(cb);
@@ -505,23 +526,45 @@ int exl3o_moe_forward(const uint16_t* x, int64_t rows, int in, int hidden, int e
                 expert_gemv(xin, gu_trellis, in, gu_tn, (int)((p * experts + e) * hidden / 16),
                             hidden, k, table, perm, p ? u : g);
             }
-            for (int p = 0; p < 2; ++p) {
-                float* v = p ? u : g;
-                const uint16_t* sv = gu_svh + ((size_t)e * 2 + p) * hidden;
-                for (int i = 0; i < hidden; ++i) v[i] = rh(v[i]);
-                for (int b = 0; b < hidden; b += 128)
-                    for (int stride = 1; stride < 128; stride <<= 1) butterfly_stage(v + b, stride);
-                for (int i = 0; i < hidden; ++i) v[i] = rh(v[i] * s * h2f(sv[i]));
-            }
             const uint16_t* dsu = down_suh + (size_t)e * hidden;
-            for (int i = 0; i < hidden; ++i) {
-                float gv = g[i], uv = u[i];
-                float act = rh((gv / (1.0f + expf(-gv))) * uv);
-                xin[i] = rh(act * h2f(dsu[i]));
+            if (gelu) {
+                /* forward_gelu (moe.rs:1087-1153): gate and up as expert_mapped
+                 * returns them (linear.rs:3325-3331: f16, staged H128, *svh in
+                 * f16), GEGLU, zeros from logical_hidden on, and the down input
+                 * as expert_mapped prepares it (linear.rs:3131-3137). */
+                for (int p = 0; p < 2; ++p) {
+                    float* v = p ? u : g;
+                    const uint16_t* sv = gu_svh + ((size_t)e * 2 + p) * hidden;
+                    for (int i = 0; i < hidden; ++i) v[i] = rh(v[i]);
+                    exl3o_h128_staged(v, hidden);
+                    for (int i = 0; i < hidden; ++i) v[i] = rh(v[i] * h2f(sv[i]));
+                }
+                for (int i = 0; i < hidden; ++i) {
+                    const float act = i < logical_hidden ? geglu1(g[i], u[i]) : 0.0f;
+                    xin[i] = rh(act * h2f(dsu[i]));
+                }
+                exl3o_h128_staged(xin, hidden);
+            } else {
+                /* glu_down_input (moe.rs:435-563), SiLU */
+                for (int p = 0; p < 2; ++p) {
+                    float* v = p ? u : g;
+                    const uint16_t* sv = gu_svh + ((size_t)e * 2 + p) * hidden;
+                    for (int i = 0; i < hidden; ++i) v[i] = rh(v[i]);
+                    for (int b = 0; b < hidden; b += 128)
+                        for (int stride = 1; stride < 128; stride <<= 1)
+                            butterfly_stage(v + b, stride);
+                    for (int i = 0; i < hidden; ++i) v[i] = rh(v[i] * s * h2f(sv[i]));
+                }
+                for (int i = 0; i < hidden; ++i) {
+                    float gv = g[i], uv = u[i];
+                    float act = rh((gv / (1.0f + expf(-gv))) * uv);
+                    xin[i] = rh(act * h2f(dsu[i]));
+                }
+                for (int b = 0; b < hidden; b += 128)
+                    for (int stride = 1; stride < 128; stride <<= 1)
+                        butterfly_stage(xin + b, stride);
+                for (int i = 0; i < hidden; ++i) xin[i] = rh(xin[i] * s);
             }
-            for (int b = 0; b < hidden; b += 128)
-                for (int stride = 1; stride < 128; stride <<= 1) butterfly_stage(xin + b, stride);
-            for (int i = 0; i < hidden; ++i) xin[i] = rh(xin[i] * s);
             expert_gemv(xin, down_trellis, hidden, down_tn, (int)(e * in / 16), in, k, table, perm,
                         d);
             for (int i = 0; i < in; ++i) d[i] = rh(d[i]);

@@ -77,13 +77,17 @@ int exl3o_prologue(const void* x, int x_dtype, int64_t rows, int in, const uint1
  * gu_suh [E][2][in], gu_svh [E][2][H], down_suh [E][H], down_svh [E][in] f16.
  * selected [rows][top_k] u32, scores [rows][top_k] f16.  x, y: rows*in f16.
  * Each routed slot: gate = lin(x), up = lin(x) (f16 outputs), act =
- * f16(silu(gate) * up), down = lin(act) (f16), y = f16(sum_t f32(score*down)). */
+ * f16(silu(gate) * up), down = lin(act) (f16), y = f16(sum_t f32(score*down)).
+ * gelu != 0: forward_gelu (moe.rs:1087-1153) -- gate/up and the down input
+ * in the linear's engine glue (staged H128), act = geglu(gate, up) for
+ * columns < logical_hidden and 0 beyond. */
 int exl3o_moe_forward(const uint16_t* x, int64_t rows, int in, int hidden, int experts,
                       int top_k, int k, int cb, const uint16_t* gu_trellis,
                       const uint16_t* gu_suh, const uint16_t* gu_svh,
                       const uint16_t* down_trellis, const uint16_t* down_suh,
                       const uint16_t* down_svh, const uint32_t* selected,
-                      const uint16_t* scores, uint16_t* y, int threads);
+                      const uint16_t* scores, uint16_t* y, int gelu, int logical_hidden,
+                      int threads);
 
 /* ---- dense SwiGLU (Array::swiglu, native/ffi/mlx_bridge.cpp:745-749) ----
  * out[i] = (g * sigmoid(g)) * u for f16 g, u in f16 arithmetic: the compiled
@@ -92,6 +96,12 @@ int exl3o_moe_forward(const uint16_t* x, int64_t rows, int in, int hidden, int e
  * x < 0 ? 1 - y : y.  Every operation rounds to f16; exp is evaluated in f32
  * (expf) and rounded. */
 void exl3o_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n);
+
+/* ---- dense GEGLU (Array::geglu, native/ffi/mlx_bridge.cpp:764-774) ----
+ * out[i] = f16 evaluation of 0.5g(1 + tanh(0.7978845608(g + 0.044715g^3)))u:
+ * every operation rounds to f16, pow(g, 3) and tanh are rounded once from
+ * binary64. */
+void exl3o_geglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n);
 
 #ifdef __cplusplus
 }

@@ -168,6 +168,39 @@ def test_moe_create_workspace_and_forward_rejects():
         lib.exl3_moe_destroy(h)
 
 
+def test_moe_create_gelu_validates_the_logical_width():
+    """forward_gelu zeroes GEGLU outputs from logical_hidden on (moe.rs:1125-1137):
+    widths <= 0 are rejected, widths past hidden zero nothing; the bank checks
+    are those of exl3_moe_create (K=7 has no SwitchGLU layout, contracts.rs:51)."""
+    lib = mlxl3_amd.load_library()
+
+    def gelu_create(logical, k=3):
+        h = ctypes.c_void_p()
+        rc = lib.exl3_moe_create_gelu(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 256, 256, 8, 2, k, 0,
+                                      logical, ctypes.byref(h))
+        return rc, h, lib.exl3_last_error().decode()
+
+    for logical in (0, -128):
+        rc, h, err = gelu_create(logical)
+        assert rc == -1 and not h.value and "invalid logical GLU width" in err
+    rc, h, err = gelu_create(128, k=7)
+    assert rc == -1 and not h.value and "invalid or overflowing SwitchGLU dimensions" in err
+    for logical in (1, 200, 256, 4096):
+        rc, h, err = gelu_create(logical)
+        assert rc == 0 and h.value, err
+        assert lib.exl3_moe_workspace_bytes(h, 3) > 0
+        lib.exl3_moe_destroy(h)
+
+
+def test_geglu_rejects_before_launch():
+    lib = mlxl3_amd.load_library()
+    assert lib.exl3_geglu(FAKE, FAKE, FAKE, -1, None) == -1
+    assert "negative element count" in lib.exl3_last_error().decode()
+    assert lib.exl3_geglu(None, FAKE, FAKE, 8, None) == -1
+    assert "null GEGLU buffer" in lib.exl3_last_error().decode()
+    assert lib.exl3_geglu(None, None, None, 0, None) == 0
+
+
 def test_group_and_mlp_reject_before_launch():
     lib = mlxl3_amd.load_library()
     hs = [create(n_in=256, n_out=256)[1] for _ in range(9)]

@@ -232,6 +232,39 @@ def test_moe_load_equals_create(tmp_path, names, k, cb, experts, top_k, in_f, hi
     ck.close()
 
 
+def test_moe_load_gemma_equals_create_gelu(tmp_path):
+    """Exl3SwitchGlu::from_gemma_checkpoint (moe.rs:663-680): the GELU bank loaded
+    from a checkpoint equals the one created from the same tensors, bit for bit,
+    and both follow the oracle's forward_gelu."""
+    import mlxl3_amd
+
+    torch = torch_mod()
+    names = ("gate_proj", "up_proj", "down_proj")
+    experts, top_k, in_f, hidden, k, cb, rows, logical = 4, 2, 256, 384, 3, 0, 12, 320
+    print(f"moe load gemma k={k} E={experts} logical={logical}", flush=True)
+    tensors, layers = _bank_tensors("model.layers.1.experts", experts, in_f, hidden, k, cb, names)
+    storage = {n.removesuffix(".trellis"): {"quant_format": "exl3"} for n in tensors if n.endswith(".trellis")}
+    root = synth.write_checkpoint(tmp_path / "g", [tensors], storage)
+    ck = mlxl3_amd.Checkpoint(root)
+    loaded = mlxl3_amd.Exl3SwitchGlu.from_gemma_checkpoint(ck, "model.layers.1.experts", experts,
+                                                           top_k, logical)
+    assert (loaded.activation, loaded.logical_hidden) == ("gelu", logical)
+    bank = _numpy_bank(layers)
+    made = mlxl3_amd.Exl3SwitchGlu(*[dev(a) for a in bank], top_k=top_k, k=k, cb=cb,
+                                   activation="gelu", logical_hidden=logical)
+    x = synth.activations(33, 1, rows, in_f)
+    sel, sc = synth.moe_routes(33, 2, rows, experts, top_k)
+    y_load = loaded.forward(dev(x), dev(sel), dev(sc))
+    y_made = made.forward(dev(x), dev(sel), dev(sc))
+    torch.cuda.synchronize()
+    y_load = y_load.cpu().numpy()
+    assert np.array_equal(y_load.view(np.uint16), y_made.cpu().numpy().view(np.uint16))
+    _moe_check(y_load, oracle.moe_forward(x, sel, sc, *bank, k, cb, activation="gelu",
+                                          logical_hidden=logical), "moe load gemma")
+    del loaded, made
+    ck.close()
+
+
 @pytest.mark.parametrize("name, names", [("qwen-moe", ("gate_proj", "up_proj", "down_proj")),
                                          ("lfm-moe", ("w1", "w3", "w2"))])
 def test_moe_bank_with_real_expert_tiles(golden, tmp_path, name, names):

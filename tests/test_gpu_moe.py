@@ -1,5 +1,6 @@
-"""GPU SwitchGLU (grouped expert QMM, Exl3SwitchGlu::forward, native/src/moe.rs:905-975)
-through the C ABI, against the CPU oracle on the same seeded inputs.
+"""GPU SwitchGLU (grouped expert QMM, Exl3SwitchGlu::forward, native/src/moe.rs:905-975,
+and the GELU banks' forward_gelu, :1087-1153) through the C ABI, against the CPU
+oracle on the same seeded inputs.
 
 Tolerance (stated): the GPU and the oracle differ only in the f32 summation
 order of the four inner products per slot (MFMA blocks vs sequential tiles), and
@@ -38,10 +39,10 @@ def dev(a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
-def make_moe(layer, top_k, k, cb):
+def make_moe(layer, top_k, k, cb, **kw):
     import mlxl3_amd
 
-    return mlxl3_amd.Exl3SwitchGlu(*[dev(a) for a in layer], top_k=top_k, k=k, cb=cb)
+    return mlxl3_amd.Exl3SwitchGlu(*[dev(a) for a in layer], top_k=top_k, k=k, cb=cb, **kw)
 
 
 def run(moe, x, sel, sc):
@@ -141,3 +142,70 @@ def test_moe_c4_full_shape():
     pick = np.arange(0, 256, 8)
     ref = oracle.moe_forward(x[pick], sel[pick], sc[pick], *layer, 3, 0)
     check(y[pick], ref, "moe C4")
+
+
+# ---- GELU banks (from_gemma_checkpoint, forward_gelu) ----
+
+
+@pytest.mark.parametrize("k,cb,logical", [(3, 0, 384), (2, 1, 300), (4, 2, 128), (5, 0, 1000)])
+def test_moe_gelu_small(k, cb, logical):
+    print(f"moe gelu k={k} cb={cb} logical={logical}", flush=True)
+    layer, x, sel, sc = case(256, 384, 6, 2, 5, k, 60 + k)
+    moe = make_moe(layer, 2, k, cb, activation="gelu", logical_hidden=logical)
+    y = run(moe, x, sel, sc)
+    ref = oracle.moe_forward(x, sel, sc, *layer, k, cb, activation="gelu", logical_hidden=logical)
+    check(y, ref, f"moe gelu k={k} cb={cb} logical={logical}")
+
+
+@pytest.mark.parametrize("block_rows", ["16", "64"])
+@pytest.mark.parametrize("splits", ["1", "3"])
+def test_moe_gelu_blocks_and_splits(block_rows, splits, monkeypatch):
+    print(f"moe gelu {block_rows}-row blocks, splits={splits}", flush=True)
+    monkeypatch.setenv("EXL3_MOE_BLOCK_ROWS", block_rows)
+    monkeypatch.setenv("EXL3_MOE_SPLITS", splits)
+    in_f, hidden, experts, top_k, rows, k = 512, 256, 5, 2, 96, 3
+    layer, x, _, _ = case(in_f, hidden, experts, top_k, rows, k, 88)
+    sel, sc = synth.moe_routes(88, 530, rows, 3, top_k)
+    moe = make_moe(layer, top_k, k, 0, activation="gelu", logical_hidden=192)
+    y = run(moe, x, sel, sc)
+    pick = np.arange(0, rows, 3)
+    ref = oracle.moe_forward(x[pick], sel[pick], sc[pick], *layer, k, 0, activation="gelu",
+                             logical_hidden=192)
+    check(y[pick], ref, f"moe gelu blocks={block_rows} splits={splits}")
+
+
+def test_moe_gelu_decode_and_silu_differs():
+    print("moe gelu decode top-8", flush=True)
+    layer, x, sel, sc = case(512, 256, 16, 8, 1, 3, 93)
+    gelu = make_moe(layer, 8, 3, 0, activation="gelu", logical_hidden=200)
+    y = run(gelu, x, sel, sc)
+    check(y, oracle.moe_forward(x, sel, sc, *layer, 3, 0, activation="gelu", logical_hidden=200),
+          "moe gelu decode")
+    silu = run(make_moe(layer, 8, 3, 0), x, sel, sc)
+    assert np.linalg.norm(silu.astype(np.float64) - y) > 0.05 * np.linalg.norm(y.astype(np.float64))
+
+
+def test_geglu_every_f16_gate():
+    """exl3_geglu against the oracle for every finite f16 gate and three up
+    values: bit-exact (both round pow and tanh once from binary64)."""
+    import mlxl3_amd
+
+    torch = torch_mod()
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    g = bits.view(np.float16)
+    g = g[np.isfinite(g)]
+    for u in (1.0, -0.75, 3.5):
+        uu = np.full_like(g, u)
+        out = mlxl3_amd.geglu(torch.from_numpy(g).cuda(), torch.from_numpy(uu).cuda())
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        want = oracle.geglu(g, uu)
+        same = (got.view(np.uint16) == want.view(np.uint16)) | (np.isnan(got) & np.isnan(want))
+        print(f"geglu u={u}: {int((~same).sum())} of {g.size} differ", flush=True)
+        assert same.all(), (g[~same][:5], got[~same][:5], want[~same][:5])
+    # odd length and an unaligned view take the scalar path
+    odd = torch.from_numpy(g[1:1001].copy()).cuda()
+    out = mlxl3_amd.geglu(odd, odd)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint16),
+                                  oracle.geglu(g[1:1001], g[1:1001]).view(np.uint16))

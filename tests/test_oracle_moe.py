@@ -129,3 +129,80 @@ def test_oracle_moe_rejects_out_of_bank_routes():
     bad[0, 0] = 6
     with pytest.raises(ValueError):
         oracle.moe_forward(x, bad, sc, *layer, 3, 0)
+
+
+# ---- GELU banks (forward_gelu, moe.rs:1087-1153) ----
+# The second composition is built from the linear oracle (engine glue, mode 1:
+# expert_mapped is that linear on the expert's tile columns with its scales,
+# linear.rs:3125-3137, :3325-3331) and the dense GEGLU, both pinned on their
+# own; each slot's output is f16(down * score) and the top-k sum is taken in
+# f32 and rounded once, as the SiLU path's finish_and_reduce.
+
+
+def gelu_composition(x, sel, sc, layer, k, cb, logical, mutant=None):
+    gu, gu_suh, gu_svh, down, down_suh, down_svh = layer
+    experts, _, n_in = gu_suh.shape
+    hidden = gu_svh.shape[-1]
+    ht, it = hidden // 16, n_in // 16
+    rows, top_k = sel.shape
+    y = np.zeros((rows, n_in), np.float32)
+    for r in range(rows):
+        acc = np.zeros(n_in, np.float32)
+        for t in range(top_k):
+            e = int(sel[r, t])
+            proj = []
+            for p in range(2):
+                cols = slice((p * experts + e) * ht, (p * experts + e + 1) * ht)
+                proj.append(oracle.forward(x[r:r + 1], gu[:, cols], gu_suh[e, p], gu_svh[e, p],
+                                           k, cb, mode=1)[0])
+            g, u = proj
+            if mutant == "swap_glu":
+                g, u = u, g
+            act = oracle.swiglu(g, u) if mutant == "silu" else oracle.geglu(g, u)
+            if mutant != "no_mask":
+                act = act.copy()
+                act[logical:] = 0
+            d = oracle.forward(act[None], down[:, e * it:(e + 1) * it], down_suh[e], down_svh[e],
+                               k, cb, mode=1)[0]
+            acc += f16(d.astype(np.float32) * np.float32(sc[r, t]))
+        y[r] = acc
+    return y.astype(F16)
+
+
+@pytest.mark.parametrize("k,cb,logical", [(3, 0, 200), (2, 1, 256), (4, 2, 96)])
+def test_oracle_gelu_moe_matches_linear_composition(k, cb, logical):
+    x, sel, sc, layer = case(k=k)
+    got = oracle.moe_forward(x, sel, sc, *layer, k, cb, activation="gelu", logical_hidden=logical)
+    want = gelu_composition(x, sel, sc, layer, k, cb, logical)
+    # the same arithmetic apart from the GEMV's summation order (tile walk vs
+    # dense): rare f16 flips before the glue
+    assert rel_l2(got, want) < 1e-3
+    rms = np.sqrt(np.mean(want.astype(np.float64) ** 2))
+    assert np.abs(got.astype(np.float64) - want).max() < 1e-2 * rms
+
+
+@pytest.mark.parametrize("mutant", ["swap_glu", "silu", "no_mask"])
+def test_gelu_composition_detects_planted_mistakes(mutant):
+    x, sel, sc, layer = case()
+    got = oracle.moe_forward(x, sel, sc, *layer, 3, 0, activation="gelu", logical_hidden=128)
+    wrong = gelu_composition(x, sel, sc, layer, 3, 0, 128, mutant=mutant)
+    assert rel_l2(wrong, got) > 0.05
+
+
+def test_oracle_gelu_logical_width_masks_columns():
+    # logical_hidden = hidden zeroes nothing (the default); a narrower width
+    # changes the output; a bank whose GEGLU outputs past the width are zero
+    # anyway (down_suh zero there) cannot tell the two apart
+    x, sel, sc, layer = case()
+    gu, gu_suh, gu_svh, down, down_suh, down_svh = layer
+    full = oracle.moe_forward(x, sel, sc, *layer, 3, 0, activation="gelu")
+    same = oracle.moe_forward(x, sel, sc, *layer, 3, 0, activation="gelu", logical_hidden=256)
+    np.testing.assert_array_equal(full, same)
+    narrow = oracle.moe_forward(x, sel, sc, *layer, 3, 0, activation="gelu", logical_hidden=128)
+    assert rel_l2(narrow, full) > 0.05
+    dsu = down_suh.copy()
+    dsu[:, 128:] = 0
+    layer2 = (gu, gu_suh, gu_svh, down, dsu, down_svh)
+    a = oracle.moe_forward(x, sel, sc, *layer2, 3, 0, activation="gelu", logical_hidden=128)
+    b = oracle.moe_forward(x, sel, sc, *layer2, 3, 0, activation="gelu")
+    np.testing.assert_array_equal(a, b)

@@ -162,6 +162,18 @@ int exl3_moe_forward(const exl3_moe* handle, const uint16_t* x, int64_t rows,
                      const uint32_t* selected, const uint16_t* scores, uint16_t* y,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* The input prologue of every EXL3 projection as an op of its own,
+ * exl3_prepare128 (exl3.metal:204-216; the `metal-prepare128` codec op,
+ * main.rs:1338-1342, gpu.rs:1537-1558): out[i] = f16(H128(f16(x[i] * s)) /
+ * sqrt(128)) over consecutive 128-element blocks of f16 rows of `width`
+ * elements, with the Hadamard's f16 staging, s = scales[i % width]
+ * (scale_count == width) or scales[i] (scale_count == elements).  Rejects, as
+ * prepare128_blocks (contracts.rs:2146-2159), widths that are not positive
+ * multiples of 128, incomplete rows, other scale counts and more than 2^32 - 1
+ * elements; zero elements is a no-op. */
+int exl3_prepare128(const uint16_t* x, int64_t elements, int32_t width, const uint16_t* scales,
+                    int64_t scale_count, uint16_t* out, void* stream);
+
 /* Decode hook, the reference's `metal-decode` codec op (exl3.metal:102-109,
  * main.rs:945-967): for every tile, states[t*256 + i] (nullable) and the f16
  * bits values[t*256 + i] of state index i, in the tile's stored order. */

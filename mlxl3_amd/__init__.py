@@ -97,6 +97,7 @@ _SIGNATURES = {
     "exl3_moe_destroy": (None, [_vp]),
     "exl3_moe_workspace_bytes": (_sz, [_vp, _i64]),
     "exl3_moe_forward": (_i32, [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "exl3_prepare128": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _vp]),
     "exl3_decode_tiles": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _vp]),
     "exl3_codewords": (_i32, [_vp, _i64, _i32, _vp, _vp]),
     "exl3_qmv_inner_workspace_bytes": (_sz, [_i32, _i32]),
@@ -476,6 +477,20 @@ def swiglu(gate, up):
     out = torch.empty_like(gate)
     _check(load_library().exl3_swiglu(_ptr(gate), _ptr(up), _ptr(out), gate.numel(),
                                       _stream_ptr(gate.device)))
+    return out
+
+
+def prepare128(x, scales):
+    """The EXL3 input prologue as an op (exl3_prepare128, exl3.metal:204-216):
+    f16(H128(f16(x * scales)) / sqrt(128)) per 128-column block of the f16
+    rows of x; scales f16 of shape [width] (per column) or x's shape."""
+    torch = _torch()
+    x = _require_device(x, "x", (torch.float16,))
+    scales = _require_device(scales, "scales", (torch.float16,))
+    width = x.shape[-1] if x.dim() else 0
+    out = torch.empty_like(x)
+    _check(load_library().exl3_prepare128(_ptr(x), x.numel(), int(width), _ptr(scales),
+                                          scales.numel(), _ptr(out), _stream_ptr(x.device)))
     return out
 
 

@@ -539,6 +539,27 @@ int exl3_geglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t 
   return check_launch("GEGLU launch");
 }
 
+int exl3_prepare128(const uint16_t* x, int64_t elements, int32_t width, const uint16_t* scales,
+                    int64_t scale_count, uint16_t* out, void* stream) {
+  // prepare128_blocks (contracts.rs:2146-2159): u32 extents, complete rows of
+  // a 128-aligned width, one scale per column or per element
+  if (elements < 0 || elements > (int64_t)UINT32_MAX || width <= 0 || width % 128 ||
+      elements % width || (scale_count != width && scale_count != elements))
+    return fail(EXL3_EINVAL, "expected complete 128-aligned rows and column or element scales");
+  if (elements == 0) return EXL3_OK;
+  if (!x || !scales || !out) return fail(EXL3_EINVAL, "null prepare128 buffer");
+  PrologueParams pp{};
+  pp.x = x;
+  pp.x_dtype = EXL3_F16;
+  pp.in = width;
+  pp.rows = (int)(elements / width);
+  pp.suh[0] = scales;
+  pp.xhat[0] = out;
+  pp.suh_stride = scale_count == elements ? (size_t)width : 0;
+  launch_prologue(pp, 1, (hipStream_t)stream);
+  return check_launch("EXL3 prepare128 launch");
+}
+
 int exl3_decode_tiles(const uint16_t* packed, int64_t tiles, int32_t k, int32_t cb,
                       uint16_t* states, uint16_t* values, void* stream) {
   if (k < 1 || k > 8) return fail(EXL3_EINVAL, "K must be in 1..=8, got %d", k);

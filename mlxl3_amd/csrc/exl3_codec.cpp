@@ -11,6 +11,7 @@
 //   codebook                          GPU codewords (exl3_codewords)
 //   metal-qmv                         GPU inner QMV (exl3_qmv_inner)
 //   metal-swiglu                      GPU SwiGLU (exl3_swiglu)
+//   metal-prepare128                  GPU input prologue (exl3_prepare128)
 //   mlx-linear, mlx-group             GPU Exl3Linear / Exl3Group forward
 // Any other op answers "unknown or unavailable codec operation <op>", as a
 // reference build without the feature does.  The GPU is initialised on the
@@ -259,6 +260,18 @@ std::string run(const Request& r) {
     DeviceBuffer g(r.x), u(r.data), o(r.x.size() * 2);
     lib_check(exl3_swiglu(g.as<uint16_t>(), u.as<uint16_t>(), o.as<uint16_t>(),
                           (int64_t)r.x.size(), nullptr));
+    return json_list(o.read<uint16_t>(r.x.size()));
+  }
+  if (r.op == "metal-prepare128") {  // main.rs:1338-1342, gpu.rs:1537-1558
+    // extents checked before any upload, as prepare128_blocks (contracts.rs:2146-2159)
+    const uint64_t n = r.x.size(), w = r.cols;
+    if (n > UINT32_MAX || w == 0 || w > INT32_MAX || w % 128 || n % w ||
+        (r.data.size() != w && r.data.size() != n))
+      bail("expected complete 128-aligned rows and column or element scales");
+    if (n == 0) return "[]";
+    DeviceBuffer x(r.x), sc(r.data), o(r.x.size() * 2);
+    lib_check(exl3_prepare128(x.as<uint16_t>(), (int64_t)n, (int)w, sc.as<uint16_t>(),
+                              (int64_t)r.data.size(), o.as<uint16_t>(), nullptr));
     return json_list(o.read<uint16_t>(r.x.size()));
   }
   if (r.op == "mlx-linear") {  // main.rs:310-334

@@ -59,6 +59,7 @@ struct PrologueParams {
   int x_dtype, in, rows;
   const uint16_t* suh[kMaxMembers];
   uint16_t* xhat[kMaxMembers];  // [rows][in] f16 each
+  size_t suh_stride;            // scale elements per row: 0 (one scale per column) or in
 };
 
 // The member owning global column block `cblk`, chosen with compile-time

@@ -35,6 +35,7 @@ namespace exl3 {
 // xhat[i] = prologue(x, suh[i]) for all rows of each member i (grid.y): one
 // wave per (row, run of eight 128-input blocks), pair layout with the run's
 // loads in flight together.  grid (ceil(rows * runs / 4), members), 256 threads.
+// suh_stride = in gives every row its own scales (exl3_prepare128).
 __global__ __launch_bounds__(256) void prologue_kernel(PrologueParams p) {
   const int nb = p.in >> 7, runs = (nb + 7) >> 3;
   const int job = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -48,8 +49,8 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueParams p) {
       suh = p.suh[i];
       xhat = p.xhat[i];
     }
-  pair_prologue_row(p.x, p.x_dtype, (size_t)row * p.in, suh, 8 * run, min(8 * run + 8, nb),
-                    threadIdx.x & 63, xhat + (size_t)row * p.in);
+  pair_prologue_row(p.x, p.x_dtype, (size_t)row * p.in, suh + (size_t)row * p.suh_stride,
+                    8 * run, min(8 * run + 8, nb), threadIdx.x & 63, xhat + (size_t)row * p.in);
 }
 
 // The SwiGLU edge between a (gate, up) group and its down projection:

@@ -55,6 +55,15 @@ def test_pack_golden_and_oracle(golden):
         ({"op": "metal-qmv", "k": 2, "x": [0] * 16, "cols": 16, "data": [0] * 31},
          "invalid trellis size or Metal index overflow"),
         ({"op": "metal-swiglu", "x": [1, 2], "data": [1]}, "invalid SwiGLU input extents"),
+        # the invalid requests of the reference's tests/physical_prepare128.py
+        ({"op": "metal-prepare128", "cols": 127, "x": [0] * 127, "data": [0] * 127},
+         "expected complete 128-aligned rows"),
+        ({"op": "metal-prepare128", "cols": 128, "x": [0] * 128, "data": [0] * 127},
+         "expected complete 128-aligned rows"),
+        ({"op": "metal-prepare128", "cols": 128, "x": [0] * 127, "data": [0] * 128},
+         "expected complete 128-aligned rows"),
+        ({"op": "metal-prepare128", "cols": 0, "x": [], "data": []},
+         "expected complete 128-aligned rows"),
         ({"op": "mlx-linear", "k": 2, "suh": [], "x": [1]}, "invalid linear input rows"),
         ({"op": "mlx-group", "k": 2, "widths": []}, "missing group widths"),
         ({"op": "mlx-group", "k": 7, "widths": [128, 128], "suh": [0] * 256, "x": [0] * 128},
@@ -71,6 +80,13 @@ def test_errors_are_lines(req, message):
     rows = run([req, {"op": "permutation"}])
     assert list(rows[0]) == ["error"] and message in rows[0]["error"], rows[0]
     assert "data" in rows[1]  # the stream continues
+
+
+def test_prepare128_empty_batch_needs_no_gpu():
+    # physical_prepare128.py: an empty batch of a valid width answers [] (and
+    # prepare128_blocks(0, 128, 0) == Some(0), contracts.rs:2163)
+    (row,) = run([{"op": "metal-prepare128", "cols": 128, "x": [], "data": []}])
+    assert row == {"data": []}
 
 
 def test_malformed_lines_and_defaults():

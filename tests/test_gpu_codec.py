@@ -116,3 +116,55 @@ def test_linear_group_swiglu_ops():
     assert rows[0] == {"data": bits(y)}
     assert rows[1] == {"data": [bits(y), bits(y2)]}
     assert rows[2] == {"data": bits(oracle.swiglu(g, u))}
+
+
+def prepare128_cases():
+    """The cases of the reference's tests/physical_prepare128.py (its f16 ones):
+    the 128 basis rows with unit scales, normal rows of widths 128/640/2560 with
+    column or element scales, and subnormal / signed-zero rows."""
+    rng = np.random.default_rng(75)
+    cases = [("all-128-basis-rows", np.eye(128, dtype=np.float16),
+              np.ones((1, 128), dtype=np.float16))]
+    for rows in (1, 3, 20):
+        for width in (128, 640, 2560):
+            x = rng.normal(0, 1.125, (rows, width)).astype(np.float16)
+            for scale_rows in sorted({1, rows}):
+                s = rng.normal(0, 0.75, (scale_rows, width)).astype(np.float16)
+                cases.append((f"mixed-{rows}x{width}-scale-rows-{scale_rows}", x, s))
+    bits = np.array([0x0000, 0x8000, 1, 0x8001, 0x3C00, 0xBC00, 0x0400, 0x8400], dtype=np.uint16)
+    special = np.resize(bits, (3, 128)).view(np.float16)
+    special[1] = np.float16(-0.0)
+    special[2] = np.resize(bits[::-1], 128).view(np.float16)
+    cases.append(("subnormal-signed-zero", special, np.ones_like(special)))
+    return cases
+
+
+def prepare128_oracle(x, s):
+    if s.shape[0] == 1:
+        return oracle.prologue(x, s[0])
+    return np.concatenate([oracle.prologue(x[r:r + 1], s[r]) for r in range(x.shape[0])])
+
+
+def test_prepare128_codec_and_abi_match_the_oracle():
+    import torch
+
+    import mlxl3_amd
+
+    cases = prepare128_cases()
+    reqs = [{"op": "metal-prepare128", "cols": int(x.shape[1]),
+             "x": x.view(np.uint16).ravel().tolist(), "data": s.view(np.uint16).ravel().tolist()}
+            for _, x, s in cases]
+    rows = run(reqs)
+    for (name, x, s), row in zip(cases, rows):
+        want = np.asarray(prepare128_oracle(x, s)).view(np.uint16).ravel()
+        got = np.array(row["data"], dtype=np.uint16)
+        bad = np.flatnonzero(got != want)
+        print(f"prepare128 {name}: {bad.size} of {want.size} differ", flush=True)
+        assert bad.size == 0, (name, bad[:5])
+        out = mlxl3_amd.prepare128(torch.from_numpy(x).cuda(),
+                                   torch.from_numpy(np.ascontiguousarray(s if s.shape[0] > 1 else s[0])).cuda())
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out.cpu().numpy().view(np.uint16).ravel(), want)
+    # basis rows: xhat is the normalised Sylvester row (exact in f16)
+    basis = np.asarray(prepare128_oracle(*cases[0][1:])).astype(np.float64)
+    assert np.all(np.abs(np.abs(basis) - 2 ** -3.5) < 2 ** -14)

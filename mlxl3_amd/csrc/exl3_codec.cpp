@@ -13,6 +13,8 @@
 //   metal-swiglu                      GPU SwiGLU (exl3_swiglu)
 //   metal-prepare128                  GPU input prologue (exl3_prepare128)
 //   mlx-linear, mlx-group             GPU Exl3Linear / Exl3Group forward
+//   mlx-switch                        GPU Exl3SwitchGlu forward (bank in the request)
+//   mlx-checkpoint-switch/-group      the same on projections of a checkpoint
 // Any other op answers "unknown or unavailable codec operation <op>", as a
 // reference build without the feature does.  The GPU is initialised on the
 // first request that needs it.
@@ -44,9 +46,31 @@ struct Request {
   uint64_t k = 4;  // default_k, main.rs:273-275
   uint64_t mode = 0;
   uint64_t cols = 0;
-  std::vector<uint16_t> data, x, suh, svh;
+  uint64_t key_heads = 0, top_k = 0;
+  std::vector<uint16_t> data, x, suh, svh, beta, down_data, down_suh, down_svh;
+  std::vector<uint32_t> selected;
   std::vector<uint64_t> widths;
+  std::string path, prefix;
+  std::vector<std::string> prefixes;
 };
+
+std::vector<uint32_t> u32_array(const Value* v, const char* field) {
+  std::vector<uint32_t> out;
+  if (!v) return out;
+  if (!v->is_array()) bail(std::string("invalid codec request: ") + field + " must be an array");
+  for (const Value& e : v->arr) {
+    if (!e.is_number() || !e.is_uint || e.u > 0xFFFFFFFFull)
+      bail(std::string("invalid codec request: ") + field + " must hold u32 values");
+    out.push_back((uint32_t)e.u);
+  }
+  return out;
+}
+
+std::string string_field(const Value* v, const char* field) {
+  if (!v) return "";
+  if (!v->is_string()) bail(std::string("invalid codec request: ") + field + " must be a string");
+  return v->str;
+}
 
 std::vector<uint16_t> u16_array(const Value* v, const char* field) {
   std::vector<uint16_t> out;
@@ -87,6 +111,19 @@ Request parse_request(const std::string& line) {
   if (const Value* w = v.find("widths")) {
     if (!w->is_array()) bail("invalid codec request: widths must be an array");
     for (const Value& e : w->arr) r.widths.push_back(uint_field(&e, "widths", 0, UINT64_MAX));
+  }
+  r.key_heads = uint_field(v.find("key_heads"), "key_heads", 0, UINT64_MAX);
+  r.top_k = uint_field(v.find("top_k"), "top_k", 0, UINT64_MAX);
+  r.selected = u32_array(v.find("selected"), "selected");
+  r.beta = u16_array(v.find("beta"), "beta");
+  r.down_data = u16_array(v.find("down_data"), "down_data");
+  r.down_suh = u16_array(v.find("down_suh"), "down_suh");
+  r.down_svh = u16_array(v.find("down_svh"), "down_svh");
+  r.path = string_field(v.find("path"), "path");
+  r.prefix = string_field(v.find("prefix"), "prefix");
+  if (const Value* ps = v.find("prefixes")) {
+    if (!ps->is_array()) bail("invalid codec request: prefixes must be an array");
+    for (const Value& e : ps->arr) r.prefixes.push_back(string_field(&e, "prefixes"));
   }
   return r;
 }
@@ -205,6 +242,48 @@ void decode(const std::vector<uint16_t>& packed, int k, int cb, std::vector<uint
                               val.as<uint16_t>(), nullptr));
   if (states) *states = st.read<uint16_t>(tiles * 256);
   if (values) *values = val.read<uint16_t>(tiles * 256);
+}
+
+// switch_glu_route_rows / switch_glu_layout (contracts.rs:4-44)
+int64_t route_rows(const std::vector<uint32_t>& ids, uint64_t experts, uint64_t top_k) {
+  if (experts == 0 || experts > INT32_MAX || top_k == 0 || top_k > experts || ids.empty() ||
+      ids.size() > (size_t)INT32_MAX / 2 || ids.size() % top_k)
+    return -1;
+  for (uint32_t id : ids)
+    if (id >= experts) return -1;
+  return (int64_t)(ids.size() / top_k);
+}
+bool glu_layout_ok(uint64_t experts, uint64_t top_k, uint64_t input, uint64_t hidden, uint64_t k) {
+  return experts > 0 && experts <= INT32_MAX && top_k > 0 && top_k <= experts && input > 0 &&
+         input <= INT32_MAX && hidden > 0 && hidden <= INT32_MAX && input % 128 == 0 &&
+         hidden % 128 == 0 && k >= 1 && k <= 8 && k != 7 &&
+         experts * hidden <= INT32_MAX && experts * input <= INT32_MAX;
+}
+// Array::from_bytes's check (array.rs:884-888) for each tensor of a request
+void expect_len(size_t got, uint64_t want) {
+  if (got != want) bail("tensor byte count does not match shape and dtype");
+}
+
+struct MoeGuard {
+  exl3_moe* h = nullptr;
+  ~MoeGuard() { exl3_moe_destroy(h); }
+};
+struct CheckpointGuard {
+  exl3_checkpoint* c = nullptr;
+  ~CheckpointGuard() { exl3_checkpoint_close(c); }
+};
+
+// y[rows][in] of a SwitchGLU handle on f16 x, u32 routes and f16 scores
+std::vector<uint16_t> moe_run(exl3_moe* h, const std::vector<uint16_t>& xv,
+                              const std::vector<uint32_t>& sel, const std::vector<uint16_t>& sc,
+                              int64_t rows) {
+  DeviceBuffer x(xv), s(sel), b(sc), y(xv.size() * 2);
+  const size_t wb = exl3_moe_workspace_bytes(h, rows);
+  if (wb == 0) bail("MoE slot overflow");
+  DeviceBuffer ws(wb);
+  lib_check(exl3_moe_forward(h, x.as<uint16_t>(), rows, s.as<uint32_t>(), b.as<uint16_t>(),
+                             y.as<uint16_t>(), ws.p, wb, nullptr));
+  return y.read<uint16_t>(xv.size());
 }
 
 // ---- operations ------------------------------------------------------------
@@ -362,6 +441,110 @@ std::string run(const Request& r) {
       out += json_list(ys[i]->read<uint16_t>(m * r.widths[i]));
     }
     return out + "]";
+  }
+  if (r.op == "mlx-switch") {  // validate_moe_codec main.rs:211-229, run :627-675
+    const uint64_t experts = r.key_heads, top_k = r.top_k > 0 ? r.top_k : r.selected.size();
+    const int64_t rows = route_rows(r.selected, experts, top_k);
+    if (rows < 0) bail("invalid SwitchGLU routes");
+    if (r.x.size() % (uint64_t)rows) bail("invalid SwitchGLU rows");
+    const uint64_t input = r.x.size() / rows, hidden = r.cols;
+    if (!glu_layout_ok(experts, top_k, input, hidden, r.k)) bail("invalid SwitchGLU layout");
+    const uint64_t k16 = 16 * r.k;
+    expect_len(r.data.size(), input / 16 * (experts * hidden / 8) * k16);
+    expect_len(r.down_data.size(), hidden / 16 * (experts * input / 16) * k16);
+    expect_len(r.suh.size(), experts * 2 * input);
+    expect_len(r.svh.size(), experts * 2 * hidden);
+    expect_len(r.down_suh.size(), experts * hidden);
+    expect_len(r.down_svh.size(), experts * input);
+    expect_len(r.beta.size(), (uint64_t)rows * top_k);
+    DeviceBuffer gu(r.data), gs(r.suh), gv(r.svh), dn(r.down_data), ds(r.down_suh),
+        dv(r.down_svh);
+    MoeGuard g;
+    lib_check(exl3_moe_create(gu.as<uint16_t>(), gs.as<uint16_t>(), gv.as<uint16_t>(),
+                              dn.as<uint16_t>(), ds.as<uint16_t>(), dv.as<uint16_t>(), (int)input,
+                              (int)hidden, (int)experts, (int)top_k, (int)r.k, cb, &g.h));
+    return json_list(moe_run(g.h, r.x, r.selected, r.beta, rows));
+  }
+  if (r.op == "mlx-checkpoint-switch") {  // validate_moe_codec main.rs:230-238, run :701-725
+    if (r.x.empty()) bail("empty SwitchGLU input");
+    if (route_rows(r.selected, r.key_heads, r.selected.size()) < 0)
+      bail("invalid checkpoint SwitchGLU routes");
+    expect_len(r.beta.size(), r.selected.size());
+    CheckpointGuard c;
+    lib_check(exl3_checkpoint_open(r.path.c_str(), &c.c));
+    const bool lfm = std::strcmp(exl3_checkpoint_model_type(c.c), "lfm2_moe") == 0;
+    MoeGuard g;
+    lib_check(exl3_moe_load(c.c, r.prefix.c_str(), (int)r.key_heads, (int)r.selected.size(),
+                            lfm ? "w1" : nullptr, lfm ? "w3" : nullptr, lfm ? "w2" : nullptr,
+                            &g.h));
+    return json_list(moe_run(g.h, r.x, r.selected, r.beta, 1));
+  }
+  if (r.op == "mlx-checkpoint-group") {  // main.rs:677-700
+    CheckpointGuard c;
+    lib_check(exl3_checkpoint_open(r.path.c_str(), &c.c));
+    if (r.prefixes.empty()) bail("empty projection bundle");
+    std::vector<exl3_linear*> parts;
+    struct Cleanup {
+      std::vector<exl3_linear*>& parts;
+      ~Cleanup() {
+        for (auto* h : parts) exl3_linear_destroy(h);
+      }
+    } cleanup{parts};
+    // K and codebook of each projection, as Exl3Linear::from_checkpoint reads them
+    std::vector<std::pair<int64_t, int>> kinds;
+    for (const std::string& p : r.prefixes) {
+      exl3_linear* h = nullptr;
+      lib_check(exl3_linear_load(c.c, p.c_str(), &h));
+      parts.push_back(h);
+      exl3_tensor_info info;
+      lib_check(exl3_checkpoint_tensor(c.c, (p + ".trellis").c_str(), &info));
+      const int kcb = exl3_checkpoint_tensor(c.c, (p + ".mul1").c_str(), &info) == EXL3_OK ? 2
+                      : exl3_checkpoint_tensor(c.c, (p + ".mcg").c_str(), &info) == EXL3_OK ? 1
+                                                                                             : 0;
+      exl3_checkpoint_tensor(c.c, (p + ".trellis").c_str(), &info);
+      kinds.emplace_back(info.shape[info.ndim - 1] / 16, kcb);
+    }
+    const int32_t in = exl3_linear_in_features(parts[0]);
+    if ((uint64_t)in != r.x.size()) bail("invalid linear input rows");
+    // Exl3Group::compatible (linear.rs:2303-2311)
+    bool grouped = parts.size() >= 2 && kinds[0].first != 7;
+    for (size_t i = 0; i < parts.size(); ++i)
+      grouped = grouped && exl3_linear_in_features(parts[i]) == in && kinds[i] == kinds[0];
+    DeviceBuffer x(r.x);
+    std::vector<DeviceBuffer*> ys;
+    struct YCleanup {
+      std::vector<DeviceBuffer*>& ys;
+      ~YCleanup() {
+        for (auto* b : ys) delete b;
+      }
+    } ycleanup{ys};
+    std::vector<void*> yp;
+    for (auto* h : parts) {
+      ys.push_back(new DeviceBuffer((size_t)exl3_linear_out_features(h) * 2));
+      yp.push_back(ys.back()->p);
+    }
+    if (grouped && parts.size() <= 8) {
+      const size_t wb = exl3_group_workspace_bytes(parts.data(), (int)parts.size(), 1);
+      DeviceBuffer ws(wb);
+      zero_workspace(ws);
+      lib_check(exl3_group_forward(parts.data(), (int)parts.size(), x.p, EXL3_F16, 1, yp.data(),
+                                   ws.p, wb, nullptr));
+    } else {
+      for (size_t i = 0; i < parts.size(); ++i) {
+        const size_t wb = exl3_linear_workspace_bytes(parts[i], 1);
+        DeviceBuffer ws(wb);
+        zero_workspace(ws);
+        lib_check(exl3_linear_forward(parts[i], x.p, EXL3_F16, 1, yp[i], EXL3_F16, ws.p, wb,
+                                      nullptr));
+      }
+    }
+    std::string out = std::string("{\"grouped\":") + (grouped ? "true" : "false") +
+                      ",\"outputs\":[";
+    for (size_t i = 0; i < ys.size(); ++i) {
+      if (i) out += ',';
+      out += json_list(ys[i]->read<uint16_t>(exl3_linear_out_features(parts[i])));
+    }
+    return out + "]}";
   }
   bail("unknown or unavailable codec operation " + r.op);
 }

@@ -65,6 +65,23 @@ def test_pack_golden_and_oracle(golden):
         ({"op": "metal-prepare128", "cols": 0, "x": [], "data": []},
          "expected complete 128-aligned rows"),
         ({"op": "mlx-linear", "k": 2, "suh": [], "x": [1]}, "invalid linear input rows"),
+        # the rejected requests of main.rs:5670-5680 (routes checked before any GPU
+        # or checkpoint work), then a valid route with a missing bank
+        ({"op": "mlx-switch", "key_heads": 2, "cols": 128, "top_k": 1}, "invalid SwitchGLU routes"),
+        ({"op": "mlx-switch", "key_heads": 2, "cols": 128, "selected": [2]},
+         "invalid SwitchGLU routes"),
+        ({"op": "mlx-switch", "key_heads": 2, "cols": 128, "selected": [0, 1, 0], "top_k": 2},
+         "invalid SwitchGLU routes"),
+        ({"op": "mlx-checkpoint-switch", "key_heads": 256, "selected": [256], "x": [0],
+          "path": "/missing"}, "invalid checkpoint SwitchGLU routes"),
+        ({"op": "mlx-checkpoint-switch", "key_heads": 256, "x": [0], "path": "/missing"},
+         "invalid checkpoint SwitchGLU routes"),
+        ({"op": "mlx-switch", "key_heads": 2, "cols": 128, "selected": [1], "x": [0] * 128},
+         "tensor byte count does not match shape and dtype"),
+        ({"op": "mlx-switch", "key_heads": 2, "cols": 128, "selected": [1], "x": [0] * 100},
+         "invalid SwitchGLU layout"),
+        ({"op": "mlx-switch", "key_heads": 2, "cols": 128, "selected": [1], "x": [0] * 128,
+          "k": 7}, "invalid SwitchGLU layout"),
         ({"op": "mlx-group", "k": 2, "widths": []}, "missing group widths"),
         ({"op": "mlx-group", "k": 7, "widths": [128, 128], "suh": [0] * 256, "x": [0] * 128},
          "unsupported group"),

@@ -297,3 +297,89 @@ def test_moe_bank_with_real_expert_tiles(golden, tmp_path, name, names):
                f"moe real-tile bank {name}")
     del moe
     ck.close()
+
+
+# ---- codec ops over banks and checkpoints (main.rs:627-725) ----
+
+
+def test_codec_mlx_switch_equals_the_api():
+    import mlxl3_amd
+    from codec_client import run
+
+    torch = torch_mod()
+    in_f, hidden, experts, top_k, rows, k, cb = 256, 256, 6, 2, 5, 3, 1
+    layer = synth.moe_layer(9, 500, in_f, hidden, experts, k)
+    x = synth.activations(9, 510, rows, in_f)
+    sel, sc = synth.moe_routes(9, 520, rows, experts, top_k)
+    gu, gu_suh, gu_svh, dn, dsu, dsv = layer
+    u16 = lambda a: np.ascontiguousarray(a).view(np.uint16).ravel().tolist()
+    req = {"op": "mlx-switch", "key_heads": experts, "top_k": top_k, "cols": hidden, "k": k,
+           "mode": cb, "selected": sel.ravel().tolist(), "beta": u16(sc), "x": u16(x),
+           "data": u16(gu), "down_data": u16(dn), "suh": u16(gu_suh), "svh": u16(gu_svh),
+           "down_suh": u16(dsu), "down_svh": u16(dsv)}
+    (row,) = run([req])
+    got = np.array(row["data"], np.uint16).reshape(rows, in_f)
+    moe = mlxl3_amd.Exl3SwitchGlu(*[dev(a) for a in layer], top_k=top_k, k=k, cb=cb)
+    y = moe.forward(dev(x), dev(sel), dev(sc))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got, y.cpu().numpy().view(np.uint16))
+    _moe_check(got.view(np.float16), oracle.moe_forward(x, sel, sc, *layer, k, cb), "codec mlx-switch")
+
+
+@pytest.mark.parametrize("model_type, names", [("qwen3_moe", ("gate_proj", "up_proj", "down_proj")),
+                                               ("lfm2_moe", ("w1", "w3", "w2"))])
+def test_codec_mlx_checkpoint_switch_equals_the_loader(tmp_path, model_type, names):
+    import mlxl3_amd
+    from codec_client import run
+
+    torch = torch_mod()
+    experts, top_k, in_f, hidden, k, cb = 4, 2, 256, 256, 2, 0
+    prefix = "model.layers.0.mlp.experts"
+    tensors, layers = _bank_tensors(prefix, experts, in_f, hidden, k, cb, names)
+    storage = {n.removesuffix(".trellis"): {"quant_format": "exl3"} for n in tensors if n.endswith(".trellis")}
+    root = synth.write_checkpoint(tmp_path / model_type, [tensors], storage, model_type=model_type)
+    x = synth.activations(41, 1, 1, in_f)
+    sel, sc = synth.moe_routes(41, 2, 1, experts, top_k)
+    req = {"op": "mlx-checkpoint-switch", "path": str(root), "prefix": prefix,
+           "key_heads": experts, "selected": sel.ravel().tolist(),
+           "beta": sc.view(np.uint16).ravel().tolist(), "x": x.view(np.uint16).ravel().tolist()}
+    (row,) = run([req])
+    ck = mlxl3_amd.Checkpoint(root)
+    loaded = mlxl3_amd.Exl3SwitchGlu.from_checkpoint(ck, prefix, experts, top_k, names)
+    y = loaded.forward(dev(x), dev(sel), dev(sc))
+    torch.cuda.synchronize()
+    print(f"codec mlx-checkpoint-switch {model_type}: {len(row['data'])} values", flush=True)
+    np.testing.assert_array_equal(np.array(row["data"], np.uint16), y.cpu().numpy().view(np.uint16).ravel())
+    del loaded
+    ck.close()
+
+
+def test_codec_mlx_checkpoint_group(tmp_path):
+    import mlxl3_amd
+    from codec_client import run
+
+    torch = torch_mod()
+    tensors, want = {}, {}
+    specs = {"q": (256, 256, 3), "k": (256, 128, 3), "v": (256, 128, 3), "o": (256, 256, 2)}
+    for i, (name, (n_in, n_out, k)) in enumerate(specs.items()):
+        t, suh, svh, _ = synth.linear_layer(12, 200 + i, n_in, n_out, k)
+        tensors.update(synth.exl3_tensors(f"model.layers.0.attn.{name}_proj", t, suh, svh))
+    storage = {n.removesuffix(".trellis"): {"quant_format": "exl3"} for n in tensors if n.endswith(".trellis")}
+    root = synth.write_checkpoint(tmp_path / "g", [tensors], storage)
+    x = synth.activations(12, 9, 1, 256)
+    xs = x.view(np.uint16).ravel().tolist()
+    pre = lambda names: [f"model.layers.0.attn.{n}_proj" for n in names]
+    rows = run([{"op": "mlx-checkpoint-group", "path": str(root), "prefixes": pre("qkv"), "x": xs},
+                {"op": "mlx-checkpoint-group", "path": str(root), "prefixes": pre("qo"), "x": xs},
+                {"op": "mlx-checkpoint-group", "path": str(root), "prefixes": [], "x": xs}])
+    assert rows[0]["data"]["grouped"] is True and rows[1]["data"]["grouped"] is False
+    assert "empty projection bundle" in rows[2]["error"]
+    ck = mlxl3_amd.Checkpoint(root)
+    for row, names in ((rows[0], "qkv"), (rows[1], "qo")):
+        for out, p in zip(row["data"]["outputs"], pre(names)):
+            lin = mlxl3_amd.Exl3Linear.from_checkpoint(ck, p)
+            y = lin.forward(torch.from_numpy(x).cuda())
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(np.array(out, np.uint16), y.cpu().numpy().view(np.uint16).ravel())
+            del lin
+    ck.close()

@@ -180,6 +180,13 @@ int exl3_prepare128(const uint16_t* x, int64_t elements, int32_t width, const ui
 int exl3_decode_tiles(const uint16_t* packed, int64_t tiles, int32_t k, int32_t cb,
                       uint16_t* states, uint16_t* values, void* stream);
 
+/* Packing hook, the reference's `metal-pack` codec op (exl3_pack,
+ * exl3.metal:85-100; codec::pack, codec.rs:73-100): packed[t*16k + i] = the
+ * trellis tile of the low k bits of states[t*256 .. +255], the inverse of
+ * exl3_decode_tiles' states. */
+int exl3_pack_tiles(const uint16_t* states, int64_t tiles, int32_t k, uint16_t* packed,
+                    void* stream);
+
 /* Codewords of arbitrary states, the `codebook` codec op (main.rs:301-307,
  * decode_codeword codec.rs:52-71): values[i] = f16 bits of codeword(states[i]). */
 int exl3_codewords(const uint16_t* states, int64_t count, int32_t cb, uint16_t* values,

@@ -100,6 +100,7 @@ _SIGNATURES = {
     "exl3_prepare128": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _vp]),
     "exl3_decode_tiles": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _vp]),
     "exl3_codewords": (_i32, [_vp, _i64, _i32, _vp, _vp]),
+    "exl3_pack_tiles": (_i32, [_vp, _i64, _i32, _vp, _vp]),
     "exl3_qmv_inner_workspace_bytes": (_sz, [_i32, _i32]),
     "exl3_qmv_inner": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "exl3_checkpoint_open": (_i32, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
@@ -668,6 +669,23 @@ class Exl3SwitchGlu:
         return y
 
     __call__ = forward
+
+
+def pack_tiles(states, k: int):
+    """Trellis tiles of 256-state blocks on the GPU (the `metal-pack` codec op,
+    exl3.metal:85-100): int16/uint16 device tensor of whole tiles -> int16
+    tensor of 16*k words per tile."""
+    torch = _torch()
+    states = _require_device(states, "states")
+    if states.element_size() != 2:
+        raise Exl3Error(-1, "states must be 16-bit integers")
+    if states.numel() % 256:
+        raise Exl3Error(-1, "expected whole 256-state tiles")
+    tiles = states.numel() // 256
+    out = torch.empty(tiles * 16 * int(k), dtype=torch.int16, device=states.device)
+    _check(load_library().exl3_pack_tiles(_ptr(states), tiles, int(k), _ptr(out),
+                                          _stream_ptr(states.device)))
+    return out
 
 
 def codewords(states, cb: int):

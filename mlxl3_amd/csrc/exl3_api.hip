@@ -574,6 +574,17 @@ int exl3_decode_tiles(const uint16_t* packed, int64_t tiles, int32_t k, int32_t 
   return check_launch("EXL3 decode launch");
 }
 
+int exl3_pack_tiles(const uint16_t* states, int64_t tiles, int32_t k, uint16_t* packed,
+                    void* stream) {
+  if (k < 1 || k > 8) return fail(EXL3_EINVAL, "K must be in 1..=8, got %d", k);
+  if (tiles < 0) return fail(EXL3_EINVAL, "negative tile count");
+  if (tiles == 0) return EXL3_OK;
+  if (!states || !packed) return fail(EXL3_EINVAL, "null pack buffer");
+  if ((tiles * 16 * k + 255) / 256 > INT32_MAX) return fail(EXL3_EINVAL, "too many tiles");
+  launch_pack_tiles(states, tiles, k, packed, (hipStream_t)stream);
+  return check_launch("EXL3 pack launch");
+}
+
 int exl3_codewords(const uint16_t* states, int64_t count, int32_t cb, uint16_t* values,
                    void* stream) {
   if (cb < 0 || cb > 2) return fail(EXL3_EINVAL, "invalid EXL3 codebook %d", cb);

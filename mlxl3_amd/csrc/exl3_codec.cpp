@@ -8,6 +8,7 @@
 // {"data": ...} or {"error": "..."}.  Operations:
 //   pack, permutation                 host (codec.rs:73-100, :126-138)
 //   unpack, metal-decode              GPU tile decode (exl3_decode_tiles)
+//   metal-pack                        GPU tile pack (exl3_pack_tiles)
 //   codebook                          GPU codewords (exl3_codewords)
 //   metal-qmv                         GPU inner QMV (exl3_qmv_inner)
 //   metal-swiglu                      GPU SwiGLU (exl3_swiglu)
@@ -340,6 +341,15 @@ std::string run(const Request& r) {
     lib_check(exl3_swiglu(g.as<uint16_t>(), u.as<uint16_t>(), o.as<uint16_t>(),
                           (int64_t)r.x.size(), nullptr));
     return json_list(o.read<uint16_t>(r.x.size()));
+  }
+  if (r.op == "metal-pack") {  // main.rs:1343, gpu.rs:1470-1495
+    check_k(r.k);
+    if (r.data.size() % 256) bail("expected whole 256-state tiles");
+    if (r.data.empty()) return "[]";
+    const int64_t tiles = (int64_t)(r.data.size() / 256);
+    DeviceBuffer st(r.data), out((size_t)tiles * 16 * r.k * 2);
+    lib_check(exl3_pack_tiles(st.as<uint16_t>(), tiles, (int)r.k, out.as<uint16_t>(), nullptr));
+    return json_list(out.read<uint16_t>((size_t)tiles * 16 * r.k));
   }
   if (r.op == "metal-prepare128") {  // main.rs:1338-1342, gpu.rs:1537-1558
     // extents checked before any upload, as prepare128_blocks (contracts.rs:2146-2159)

@@ -31,6 +31,9 @@ extern const QmmFn kQmm[3][8][3];  // [log2 MB]: 64, 128 or 256 rows per workgro
 void launch_prologue(const PrologueParams& p, int members, hipStream_t s);
 // values[i] = codeword(states[i], cb).
 void launch_codewords(const uint16_t* states, int64_t n, int cb, uint16_t* values, hipStream_t s);
+// packed[t][16k] = the trellis tile of states[t][256] (low k bits of each).
+void launch_pack_tiles(const uint16_t* states, int64_t tiles, int k, uint16_t* packed,
+                       hipStream_t s);
 // y = f16(x . W) over decoded tiles (no glue).
 void launch_qmv_inner(const uint16_t* values, const uint16_t* x, int rows, int cols, uint16_t* y,
                       hipStream_t s);

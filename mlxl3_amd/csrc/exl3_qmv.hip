@@ -18,6 +18,29 @@ template __global__ void codewords_kernel<0>(const uint16_t*, int64_t, uint16_t*
 template __global__ void codewords_kernel<1>(const uint16_t*, int64_t, uint16_t*);
 template __global__ void codewords_kernel<2>(const uint16_t*, int64_t, uint16_t*);
 
+// Packing, the inverse of the tile decode on the low K bits of each state
+// (codec::pack, codec.rs:73-100; GPU form exl3_pack, exl3.metal:85-100): the
+// stored word at index i of a tile holds logical word i ^ 1 (the u32 halves
+// swapped), whose 16 bits are the stream bits 16*(l % K) .. +15 of the span
+// l / K of 16 states, taken most significant first.  One thread per stored
+// word; the tile's 256 states (512 bytes) sit in L1 for its 16K threads.
+__global__ __launch_bounds__(256) void pack_tiles_kernel(const uint16_t* __restrict__ states,
+                                                         int64_t words, int k,
+                                                         uint16_t* __restrict__ packed) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= words) return;
+  const int64_t tile = i / (16 * k);
+  const int logical = (int)(i - tile * 16 * k) ^ 1;
+  const uint16_t* span = states + tile * 256 + (logical / k) * 16;
+  const int first = (logical % k) * 16;  // first stream bit of this word
+  uint32_t word = 0;
+  for (int bit = 0; bit < 16; ++bit) {
+    const int sb = first + bit;
+    word = (word << 1) | ((span[sb / k] >> (k - 1 - sb % k)) & 1u);
+  }
+  packed[i] = (uint16_t)word;
+}
+
 // Inner product of a decoded trellis without glue (the reference's serial
 // exl3_qmv, exl3.metal:118-142): y[n] = f16(sum_r x[r] * W[r][n]), W read from
 // the decoded tiles `values` ([tile][256] in stored order) through the tile
@@ -81,6 +104,13 @@ void launch_codewords(const uint16_t* states, int64_t n, int cb, uint16_t* value
   if (cb == 0) hipLaunchKernelGGL((codewords_kernel<0>), grid, dim3(256), 0, s, states, n, values);
   else if (cb == 1) hipLaunchKernelGGL((codewords_kernel<1>), grid, dim3(256), 0, s, states, n, values);
   else hipLaunchKernelGGL((codewords_kernel<2>), grid, dim3(256), 0, s, states, n, values);
+}
+
+void launch_pack_tiles(const uint16_t* states, int64_t tiles, int k, uint16_t* packed,
+                       hipStream_t s) {
+  const int64_t words = tiles * 16 * k;
+  hipLaunchKernelGGL(pack_tiles_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, s,
+                     states, words, k, packed);
 }
 
 void launch_qmv_inner(const uint16_t* values, const uint16_t* x, int rows, int cols, uint16_t* y,

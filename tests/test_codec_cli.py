@@ -49,6 +49,8 @@ def test_pack_golden_and_oracle(golden):
         ({"op": "pack", "k": 3, "data": [1] * 255}, "encoded length must be a multiple of 256"),
         ({"op": "unpack", "k": 2, "data": [1] * 31}, "packed length is not a whole tile"),
         ({"op": "metal-decode", "k": 0, "data": []}, "K must be in 1..=8, got 0"),
+        ({"op": "metal-pack", "k": 9, "data": []}, "K must be in 1..=8, got 9"),
+        ({"op": "metal-pack", "k": 2, "data": [0] * 255}, "expected whole 256-state tiles"),
         ({"op": "metal-decode", "k": 2, "data": [0] * 33}, "expected whole packed tiles"),
         ({"op": "metal-qmv", "k": 2, "x": [0] * 15, "cols": 16, "data": []},
          "expected positive 16-aligned dimensions"),

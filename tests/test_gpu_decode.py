@@ -68,3 +68,58 @@ def test_real_tiles_on_gpu(golden, name):
     s, v = gpu_decode(packed, k, cb)
     assert np.array_equal(s, np.asarray([t["states"] for t in fix["tiles"]], np.uint16))
     assert np.array_equal(v, np.asarray([t["f16_bits"] for t in fix["tiles"]], np.uint16))
+
+
+# ---- packing (exl3_pack_tiles, the metal-pack codec op) ----
+
+
+def gpu_pack(states_u16: np.ndarray, k: int):
+    import torch
+
+    import mlxl3_amd
+
+    t = torch.from_numpy(states_u16.view(np.int16).ravel().copy()).cuda()
+    out = mlxl3_amd.pack_tiles(t, k)
+    torch.cuda.synchronize()
+    return out.cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("k", range(1, 9))
+def test_pack_matches_oracle_and_inverts_decode(k):
+    """Pack of random full 16-bit states uses their low k bits (codec.rs:34-38);
+    decoding the packed tiles gives back those k bits as the low bits of every
+    state."""
+    print(f"pack random tiles k={k}", flush=True)
+    rng = np.random.default_rng(500 + k)
+    states = rng.integers(0, 65536, (777, 256), dtype=np.uint16)
+    packed = gpu_pack(states, k)
+    assert np.array_equal(packed, oracle.pack(states, k).ravel())
+    back, _ = gpu_decode(packed.reshape(-1, 16 * k), k, 0)
+    mask = np.uint16((1 << k) - 1)
+    assert np.array_equal(back.ravel() & mask, states.ravel() & mask)
+
+
+@pytest.mark.parametrize("k", range(2, 9))
+@pytest.mark.parametrize("cb", [0, 1, 2])
+def test_pack_quantizer_corpus_on_gpu(golden, k, cb):
+    d = golden / "quantizer"
+    packed = np.fromfile(d / f"oracle-{k}-{cb}-packed.u16", "<u2")
+    states = np.fromfile(d / f"oracle-{k}-{cb}-states.u16", "<u2")
+    assert np.array_equal(gpu_pack(states, k), packed)
+
+
+def test_metal_pack_codec_op():
+    from codec_client import run
+
+    rng = np.random.default_rng(9)
+    states = rng.integers(0, 65536, 3 * 256, dtype=np.uint16)
+    rows = run([{"op": "metal-pack", "k": 3, "data": states.tolist()},
+                {"op": "metal-pack", "k": 3, "data": []},
+                {"op": "metal-pack", "k": 3, "data": [0] * 255},
+                {"op": "metal-pack", "k": 7, "data": states.tolist()},
+                {"op": "metal-pack", "k": 0, "data": []}])
+    assert rows[0] == {"data": oracle.pack(states, 3).ravel().tolist()}
+    assert rows[1] == {"data": []}
+    assert "expected whole 256-state tiles" in rows[2]["error"]
+    assert rows[3] == {"data": oracle.pack(states, 7).ravel().tolist()}
+    assert "K must be in 1..=8, got 0" in rows[4]["error"]

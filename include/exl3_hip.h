@@ -174,6 +174,22 @@ int exl3_moe_forward(const exl3_moe* handle, const uint16_t* x, int64_t rows,
 int exl3_prepare128(const uint16_t* x, int64_t elements, int32_t width, const uint16_t* scales,
                     int64_t scale_count, uint16_t* out, void* stream);
 
+/* The SwitchGLU glue steps as ops of their own (the exl3_moe_forward
+ * epilogues compute the same per slot):
+ * swiglu_down_input (moe.rs:569-583, glu_down_input :435-563 with SiLU):
+ * gate_up f32 [slots*2][hidden] (gate row 2s, up row 2s+1), gu_svh f16
+ * [experts][2][hidden], down_suh f16 [experts][hidden], selected u32 [slots]
+ * -> xhat f16 [slots][hidden], the down projection's input (slots routed to
+ * ids >= experts get zeros).  finish_and_reduce (moe.rs:586-609): raw f32
+ * [rows*top_k][width], svh f16 [rows*top_k][width], scores f16 [rows][top_k]
+ * -> y f16 [rows][width]. */
+int exl3_swiglu_down_input(const float* gate_up, const uint16_t* gu_svh, const uint16_t* down_suh,
+                           const uint32_t* selected, int64_t slots, int32_t hidden,
+                           int32_t experts, uint16_t* xhat, void* stream);
+int exl3_finish_and_reduce(const float* raw, const uint16_t* svh, const uint16_t* scores,
+                           int64_t rows, int32_t top_k, int32_t width, uint16_t* y,
+                           void* stream);
+
 /* Decode hook, the reference's `metal-decode` codec op (exl3.metal:102-109,
  * main.rs:945-967): for every tile, states[t*256 + i] (nullable) and the f16
  * bits values[t*256 + i] of state index i, in the tile's stored order. */

@@ -97,6 +97,8 @@ _SIGNATURES = {
     "exl3_moe_destroy": (None, [_vp]),
     "exl3_moe_workspace_bytes": (_sz, [_vp, _i64]),
     "exl3_moe_forward": (_i32, [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "exl3_swiglu_down_input": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp]),
+    "exl3_finish_and_reduce": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp]),
     "exl3_prepare128": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _vp]),
     "exl3_decode_tiles": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _vp]),
     "exl3_codewords": (_i32, [_vp, _i64, _i32, _vp, _vp]),
@@ -479,6 +481,44 @@ def swiglu(gate, up):
     _check(load_library().exl3_swiglu(_ptr(gate), _ptr(up), _ptr(out), gate.numel(),
                                       _stream_ptr(gate.device)))
     return out
+
+
+def swiglu_down_input(gate_up, gu_svh, down_suh, selected):
+    """swiglu_down_input (moe.rs:569-583) on device tensors: f32 gate_up
+    [slots*2, hidden], f16 gu_svh [E, 2, hidden], f16 down_suh [E, hidden],
+    int32 selected [slots] -> f16 [slots, hidden]."""
+    torch = _torch()
+    gate_up = _require_device(gate_up, "gate_up", (torch.float32,))
+    gu_svh = _require_device(gu_svh, "gu_svh", (torch.float16,))
+    down_suh = _require_device(down_suh, "down_suh", (torch.float16,))
+    selected = _require_device(selected, "selected", (torch.int32,))
+    hidden = gate_up.shape[-1]
+    out = torch.empty(selected.numel(), hidden, dtype=torch.float16, device=gate_up.device)
+    if gate_up.numel() != 2 * selected.numel() * hidden:
+        raise Exl3Error(-1, "invalid fused SwiGLU dimensions")
+    _check(load_library().exl3_swiglu_down_input(_ptr(gate_up), _ptr(gu_svh), _ptr(down_suh),
+                                                 _ptr(selected), selected.numel(), hidden,
+                                                 gu_svh.shape[0], _ptr(out),
+                                                 _stream_ptr(gate_up.device)))
+    return out
+
+
+def finish_and_reduce(raw, svh, scores):
+    """finish_and_reduce (moe.rs:586-609) on device tensors: f32 raw
+    [rows*top_k, width], f16 svh of the same shape, f16 scores [rows, top_k]
+    -> f16 [rows, width]."""
+    torch = _torch()
+    raw = _require_device(raw, "raw", (torch.float32,))
+    svh = _require_device(svh, "svh", (torch.float16,))
+    scores = _require_device(scores, "scores", (torch.float16,))
+    rows, top_k = scores.shape
+    width = raw.shape[-1]
+    if raw.numel() != rows * top_k * width or svh.shape != raw.shape:
+        raise Exl3Error(-1, "invalid expert reduction dimensions")
+    y = torch.empty(rows, width, dtype=torch.float16, device=raw.device)
+    _check(load_library().exl3_finish_and_reduce(_ptr(raw), _ptr(svh), _ptr(scores), rows, top_k,
+                                                 width, _ptr(y), _stream_ptr(raw.device)))
+    return y
 
 
 def prepare128(x, scales):

@@ -16,6 +16,7 @@
 //   mlx-linear, mlx-group             GPU Exl3Linear / Exl3Group forward
 //   mlx-switch                        GPU Exl3SwitchGlu forward (bank in the request)
 //   mlx-checkpoint-switch/-group      the same on projections of a checkpoint
+//   mlx-swiglu-prepare, mlx-expert-reduce   the SwitchGLU glue steps
 // Any other op answers "unknown or unavailable codec operation <op>", as a
 // reference build without the feature does.  The GPU is initialised on the
 // first request that needs it.
@@ -50,6 +51,7 @@ struct Request {
   uint64_t key_heads = 0, top_k = 0;
   std::vector<uint16_t> data, x, suh, svh, beta, down_data, down_suh, down_svh;
   std::vector<uint32_t> selected;
+  std::vector<float> state;
   std::vector<uint64_t> widths;
   std::string path, prefix;
   std::vector<std::string> prefixes;
@@ -116,6 +118,13 @@ Request parse_request(const std::string& line) {
   r.key_heads = uint_field(v.find("key_heads"), "key_heads", 0, UINT64_MAX);
   r.top_k = uint_field(v.find("top_k"), "top_k", 0, UINT64_MAX);
   r.selected = u32_array(v.find("selected"), "selected");
+  if (const Value* st = v.find("state")) {
+    if (!st->is_array()) bail("invalid codec request: state must be an array");
+    for (const Value& e : st->arr) {
+      if (!e.is_number()) bail("invalid codec request: state must hold numbers");
+      r.state.push_back((float)e.num);
+    }
+  }
   r.beta = u16_array(v.find("beta"), "beta");
   r.down_data = u16_array(v.find("down_data"), "down_data");
   r.down_suh = u16_array(v.find("down_suh"), "down_suh");
@@ -474,6 +483,34 @@ std::string run(const Request& r) {
                               dn.as<uint16_t>(), ds.as<uint16_t>(), dv.as<uint16_t>(), (int)input,
                               (int)hidden, (int)experts, (int)top_k, (int)r.k, cb, &g.h));
     return json_list(moe_run(g.h, r.x, r.selected, r.beta, rows));
+  }
+  if (r.op == "mlx-swiglu-prepare") {  // validate_moe_codec main.rs:239-252, run :598-613
+    const uint64_t hidden = r.cols, width = hidden * 2;
+    if (width == 0 || hidden > INT32_MAX) bail("invalid gate/up width");
+    if (r.suh.size() % width) bail("invalid gate/up scales");
+    const uint64_t experts = r.suh.size() / width;
+    if (route_rows(r.selected, experts, 1) < 0) bail("invalid SwiGLU routes");
+    const uint64_t slots = r.selected.size();
+    expect_len(r.state.size(), slots * 2 * hidden);
+    expect_len(r.svh.size(), experts * hidden);
+    if (hidden % 128) bail("invalid fused SwiGLU dimensions");
+    DeviceBuffer gu(r.state), sv(r.suh), ds(r.svh), sel(r.selected), out(slots * hidden * 2);
+    lib_check(exl3_swiglu_down_input(gu.as<float>(), sv.as<uint16_t>(), ds.as<uint16_t>(),
+                                     sel.as<uint32_t>(), (int64_t)slots, (int)hidden,
+                                     (int)experts, out.as<uint16_t>(), nullptr));
+    return json_list(out.read<uint16_t>(slots * hidden));
+  }
+  if (r.op == "mlx-expert-reduce") {  // main.rs:615-625
+    const uint64_t width = r.cols, slots = r.beta.size();
+    if (width == 0 || width > INT32_MAX || width % 128)
+      bail("invalid expert reduction dimensions");
+    expect_len(r.state.size(), slots * width);
+    expect_len(r.svh.size(), slots * width);
+    if (slots == 0) return json_list(std::vector<uint16_t>(width, 0));  // an empty sum
+    DeviceBuffer raw(r.state), sv(r.svh), sc(r.beta), y(width * 2);
+    lib_check(exl3_finish_and_reduce(raw.as<float>(), sv.as<uint16_t>(), sc.as<uint16_t>(), 1,
+                                     (int)slots, (int)width, y.as<uint16_t>(), nullptr));
+    return json_list(y.read<uint16_t>(width));
   }
   if (r.op == "mlx-checkpoint-switch") {  // validate_moe_codec main.rs:230-238, run :701-725
     if (r.x.empty()) bail("empty SwitchGLU input");

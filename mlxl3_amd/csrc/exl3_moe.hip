@@ -174,6 +174,38 @@ size_t exl3_moe_workspace_bytes(const exl3_moe* h, int64_t rows) {
   return L.total;
 }
 
+int exl3_swiglu_down_input(const float* gate_up, const uint16_t* gu_svh, const uint16_t* down_suh,
+                           const uint32_t* selected, int64_t slots, int32_t hidden,
+                           int32_t experts, uint16_t* xhat, void* stream) {
+  // glu_down_input's checks (moe.rs:459-467)
+  if (slots <= 0 || slots > INT32_MAX || hidden <= 0 || hidden % 128)
+    return fail(EXL3_EINVAL, "invalid fused SwiGLU dimensions");
+  if (experts <= 0 || !gu_svh || !down_suh || !selected)
+    return fail(EXL3_EINVAL, "invalid fused SwiGLU scales/routes");
+  if (!gate_up || !xhat) return fail(EXL3_EINVAL, "null SwiGLU buffer");
+  MoeMmParams q{};
+  q.width = hidden;
+  q.experts = experts;
+  q.gu_svh = gu_svh;
+  q.down_suh = down_suh;
+  q.xd = xhat;
+  swiglu_down_input_kernel<<<dim3((unsigned)slots, hidden / 128), 64, 0, (hipStream_t)stream>>>(
+      q, gate_up, selected);
+  return check_launch("swiglu_down_input launch");
+}
+
+int exl3_finish_and_reduce(const float* raw, const uint16_t* svh, const uint16_t* scores,
+                           int64_t rows, int32_t top_k, int32_t width, uint16_t* y,
+                           void* stream) {
+  // finish_and_reduce's checks (moe.rs:596-602)
+  if (rows <= 0 || rows > INT32_MAX || top_k <= 0 || width <= 0 || width % 128)
+    return fail(EXL3_EINVAL, "invalid expert reduction dimensions");
+  if (!raw || !svh || !scores || !y) return fail(EXL3_EINVAL, "null expert reduction buffer");
+  finish_and_reduce_kernel<<<dim3((unsigned)rows, width / 128), 64, 0, (hipStream_t)stream>>>(
+      raw, svh, scores, top_k, width, y);
+  return check_launch("finish_and_reduce launch");
+}
+
 int exl3_moe_forward(const exl3_moe* h, const uint16_t* x, int64_t rows,
                      const uint32_t* selected, const uint16_t* scores, uint16_t* y,
                      void* workspace, size_t workspace_bytes, void* stream) {

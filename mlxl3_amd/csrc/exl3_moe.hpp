@@ -439,6 +439,48 @@ __global__ __launch_bounds__(256 * NPROJ) void moe_mm_kernel(MoeMmParams p) {
   }
 }
 
+// swiglu_down_input (moe.rs:569-583) as an op: the SiLU glue of
+// moe_finish_row on f32 gate/up rows [2s], [2s+1] of slot s.  One wave per
+// (slot, 128-column block); grid (slots, hidden / 128).  Slots routed to an
+// expert id >= experts get zeros (the reference reads out of its bank).
+__global__ __launch_bounds__(64) void swiglu_down_input_kernel(MoeMmParams p,
+                                                               const float* __restrict__ gate_up,
+                                                               const uint32_t* selected) {
+  const int slot = blockIdx.x, cblk = blockIdx.y, lane = threadIdx.x;
+  const uint32_t e = selected[slot];
+  const size_t off = (size_t)2 * slot * p.width + cblk * 128;
+  if (e >= (uint32_t)p.experts) {
+    p.xd[(size_t)slot * p.width + cblk * 128 + lane] = 0;
+    p.xd[(size_t)slot * p.width + cblk * 128 + lane + 64] = 0;
+    return;
+  }
+  moe_finish_row<true>(p, (int)e, slot, cblk, gate_up[off + lane], gate_up[off + lane + 64],
+                       gate_up[off + p.width + lane], gate_up[off + p.width + lane + 64], lane);
+}
+
+// finish_and_reduce (moe.rs:586-609) as an op: y[row] = f16(sum_t f32(
+// f16(f16(H(f16(raw)) * svh) * score))) over slots row*top_k + t in t order,
+// H the staged Hadamard with f16(v * scale), svh one row per slot.  One wave
+// per (row, 128-column block); grid (rows, width / 128).
+__global__ __launch_bounds__(64) void finish_and_reduce_kernel(const float* __restrict__ raw,
+                                                               const uint16_t* __restrict__ svh,
+                                                               const uint16_t* __restrict__ scores,
+                                                               int top_k, int width,
+                                                               uint16_t* __restrict__ y) {
+  const int row = blockIdx.x, col = blockIdx.y * 128 + threadIdx.x, lane = threadIdx.x;
+  float a0 = 0.f, a1 = 0.f;
+  for (int t = 0; t < top_k; ++t) {
+    const size_t slot = (size_t)row * top_k + t;
+    float v0 = round_f16(raw[slot * width + col]), v1 = round_f16(raw[slot * width + col + 64]);
+    h128_wave<true>(v0, v1, lane);
+    const float sc = h2f(scores[slot]);
+    a0 += round_f16(round_f16(round_f16(v0 * kHadScale) * h2f(svh[slot * width + col])) * sc);
+    a1 += round_f16(round_f16(round_f16(v1 * kHadScale) * h2f(svh[slot * width + col + 64])) * sc);
+  }
+  y[(size_t)row * width + col] = f2h(a0);
+  y[(size_t)row * width + col + 64] = f2h(a1);
+}
+
 // y[row][i] = f16(sum_t f32(z[row*top_k + t][i])) in t order; slots routed to
 // no valid expert contribute zero.  grid (rows, ceil(width/256)).
 __global__ __launch_bounds__(256) void moe_reduce_kernel(const uint16_t* __restrict__ z,

@@ -51,6 +51,12 @@ def lib():
         L.exl3o_f32_to_bf16.argtypes = [ctypes.c_float]
         L.exl3o_swiglu.restype = None
         L.exl3o_swiglu.argtypes = [_u16p, _u16p, _u16p, ctypes.c_int64]
+        L.exl3o_swiglu_down_input.restype = ctypes.c_int
+        L.exl3o_swiglu_down_input.argtypes = [_f32p, _u16p, _u16p, _u32p, ctypes.c_int64,
+                                              ctypes.c_int, ctypes.c_int, _u16p]
+        L.exl3o_finish_and_reduce.restype = ctypes.c_int
+        L.exl3o_finish_and_reduce.argtypes = [_f32p, _u16p, _u16p, ctypes.c_int64, ctypes.c_int,
+                                              ctypes.c_int, _u16p]
         L.exl3o_geglu.restype = None
         L.exl3o_geglu.argtypes = [_u16p, _u16p, _u16p, ctypes.c_int64]
         L.exl3o_codeword.restype = ctypes.c_uint16
@@ -225,6 +231,35 @@ def swiglu(gate, up) -> np.ndarray:
     out = np.empty_like(g)
     lib().exl3o_swiglu(g.reshape(-1), u.reshape(-1), out.reshape(-1), g.size)
     return out.view(np.float16)
+
+
+def swiglu_down_input(gate_up, gu_svh, down_suh, selected) -> np.ndarray:
+    """swiglu_down_input (moe.rs:569-583): f32 [slots*2, hidden] -> f16 [slots, hidden]."""
+    gu = np.ascontiguousarray(gate_up, np.float32)
+    hidden = gu.shape[-1]
+    sel = np.ascontiguousarray(selected, np.uint32).ravel()
+    out = np.empty((sel.size, hidden), np.uint16)
+    rc = lib().exl3o_swiglu_down_input(gu.ravel(), _u16(gu_svh).ravel(), _u16(down_suh).ravel(),
+                                       sel, sel.size, hidden, np.asarray(gu_svh).shape[0],
+                                       out.ravel())
+    if rc:
+        raise ValueError(f"oracle swiglu_down_input failed ({rc})")
+    return out.view(np.float16)
+
+
+def finish_and_reduce(raw, svh, scores) -> np.ndarray:
+    """finish_and_reduce (moe.rs:586-609): raw f32 [rows*top_k, width], svh f16
+    of the same shape, scores f16 [rows, top_k] -> f16 [rows, width]."""
+    raw = np.ascontiguousarray(raw, np.float32)
+    sc = np.asarray(scores)
+    rows, top_k = sc.shape
+    width = raw.shape[-1]
+    y = np.empty((rows, width), np.uint16)
+    rc = lib().exl3o_finish_and_reduce(raw.ravel(), _u16(svh).ravel(), _u16(sc).ravel(), rows,
+                                       top_k, width, y.ravel())
+    if rc:
+        raise ValueError(f"oracle finish_and_reduce failed ({rc})")
+    return y.view(np.float16)
 
 
 def geglu(gate, up) -> np.ndarray:

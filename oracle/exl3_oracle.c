@@ -579,6 +579,70 @@ int exl3o_moe_forward(const uint16_t* x, int64_t rows, int in, int hidden, int e
     return err;
 }
 
+/* glu_down_input, SiLU (moe.rs:435-563, swiglu_down_input :569-583): per slot
+ * s and 128-column block, gate = f16(raw[2s]) and up = f16(raw[2s+1]) through
+ * an f32 H128 and f16(v * scale * svh[e][p]), act = f16(silu(gate) * up),
+ * f16(act * down_suh[e]), an f32 H128 and f16(v * scale). */
+int exl3o_swiglu_down_input(const float* gate_up, const uint16_t* gu_svh,
+                            const uint16_t* down_suh, const uint32_t* selected, int64_t slots,
+                            int hidden, int experts, uint16_t* xhat) {
+    if (slots < 1 || hidden <= 0 || hidden % 128 || experts < 1) return -1;
+    for (int64_t i = 0; i < slots; ++i)
+        if (selected[i] >= (uint32_t)experts) return -1;
+    const float s = had_scale();
+    float g[128], u[128], d[128];
+    for (int64_t sl = 0; sl < slots; ++sl) {
+        const uint32_t e = selected[sl];
+        for (int b = 0; b < hidden; b += 128) {
+            for (int i = 0; i < 128; ++i) {
+                g[i] = rh(gate_up[(2 * sl) * hidden + b + i]);
+                u[i] = rh(gate_up[(2 * sl + 1) * hidden + b + i]);
+            }
+            for (int stride = 1; stride < 128; stride <<= 1) {
+                butterfly_stage(g, stride);
+                butterfly_stage(u, stride);
+            }
+            for (int i = 0; i < 128; ++i) {
+                const float gv = rh(g[i] * s * h2f(gu_svh[((size_t)e * 2) * hidden + b + i]));
+                const float uv = rh(u[i] * s * h2f(gu_svh[((size_t)e * 2 + 1) * hidden + b + i]));
+                const float act = rh((gv / (1.0f + expf(-gv))) * uv);
+                d[i] = rh(act * h2f(down_suh[(size_t)e * hidden + b + i]));
+            }
+            for (int stride = 1; stride < 128; stride <<= 1) butterfly_stage(d, stride);
+            for (int i = 0; i < 128; ++i) xhat[sl * hidden + b + i] = f2h(d[i] * s);
+        }
+    }
+    return 0;
+}
+
+/* finish_and_reduce (moe.rs:586-609): y[r] = f16(sum_t f32(f16(f16(H(f16(raw)))
+ * * svh) * score)) over the top_k slots r*top_k + t, H the staged H128 with
+ * f16(v * scale). */
+int exl3o_finish_and_reduce(const float* raw, const uint16_t* svh, const uint16_t* scores,
+                            int64_t rows, int top_k, int width, uint16_t* y) {
+    if (rows < 1 || top_k < 1 || width <= 0 || width % 128) return -1;
+    float* v = (float*)malloc(sizeof(float) * (size_t)width);
+    float* acc = (float*)malloc(sizeof(float) * (size_t)width);
+    if (!v || !acc) {
+        free(v), free(acc);
+        return -3;
+    }
+    for (int64_t r = 0; r < rows; ++r) {
+        for (int i = 0; i < width; ++i) acc[i] = 0.0f;
+        for (int t = 0; t < top_k; ++t) {
+            const int64_t sl = r * top_k + t;
+            for (int i = 0; i < width; ++i) v[i] = rh(raw[sl * width + i]);
+            exl3o_h128_staged(v, width);
+            const float sc = h2f(scores[sl]);
+            for (int i = 0; i < width; ++i)
+                acc[i] += rh(rh(v[i] * h2f(svh[sl * width + i])) * sc);
+        }
+        for (int i = 0; i < width; ++i) y[r * width + i] = f2h(acc[i]);
+    }
+    free(v), free(acc);
+    return 0;
+}
+
 /* ---- dense SwiGLU: mlx_bridge.cpp:745-749 (MLX Sigmoid on float16) ---- */
 void exl3o_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) {

@@ -89,6 +89,18 @@ int exl3o_moe_forward(const uint16_t* x, int64_t rows, int in, int hidden, int e
                       const uint16_t* scores, uint16_t* y, int gelu, int logical_hidden,
                       int threads);
 
+/* glu_down_input with SiLU (moe.rs:435-583): gate_up f32 [slots*2][hidden]
+ * (gate row 2s, up row 2s+1), gu_svh [E][2][hidden], down_suh [E][hidden],
+ * selected [slots] -> xhat f16 [slots][hidden]. */
+int exl3o_swiglu_down_input(const float* gate_up, const uint16_t* gu_svh,
+                            const uint16_t* down_suh, const uint32_t* selected, int64_t slots,
+                            int hidden, int experts, uint16_t* xhat);
+
+/* finish_and_reduce (moe.rs:586-609): raw f32 [rows*top_k][width], svh f16
+ * [rows*top_k][width], scores f16 [rows][top_k] -> y f16 [rows][width]. */
+int exl3o_finish_and_reduce(const float* raw, const uint16_t* svh, const uint16_t* scores,
+                            int64_t rows, int top_k, int width, uint16_t* y);
+
 /* ---- dense SwiGLU (Array::swiglu, native/ffi/mlx_bridge.cpp:745-749) ----
  * out[i] = (g * sigmoid(g)) * u for f16 g, u in f16 arithmetic: the compiled
  * MLX expression evaluated on float16 arrays (MLX 0.32.2, the version the

@@ -80,6 +80,14 @@ def test_pack_golden_and_oracle(golden):
          "invalid checkpoint SwitchGLU routes"),
         ({"op": "mlx-switch", "key_heads": 2, "cols": 128, "selected": [1], "x": [0] * 128},
          "tensor byte count does not match shape and dtype"),
+        ({"op": "mlx-swiglu-prepare", "cols": 128, "suh": [0] * 256, "selected": [1]},
+         "invalid SwiGLU routes"),
+        ({"op": "mlx-swiglu-prepare", "cols": 0, "selected": [0]}, "invalid gate/up width"),
+        ({"op": "mlx-swiglu-prepare", "cols": 128, "selected": [1], "suh": [0] * 512},
+         "tensor byte count does not match shape and dtype"),
+        ({"op": "mlx-expert-reduce", "cols": 100, "beta": [0]}, "invalid expert reduction dimensions"),
+        ({"op": "mlx-expert-reduce", "cols": 128, "beta": [0], "state": [0.5] * 127},
+         "tensor byte count does not match shape and dtype"),
         ({"op": "mlx-switch", "key_heads": 2, "cols": 128, "selected": [1], "x": [0] * 100},
          "invalid SwitchGLU layout"),
         ({"op": "mlx-switch", "key_heads": 2, "cols": 128, "selected": [1], "x": [0] * 128,

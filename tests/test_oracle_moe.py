@@ -206,3 +206,42 @@ def test_oracle_gelu_logical_width_masks_columns():
     a = oracle.moe_forward(x, sel, sc, *layer2, 3, 0, activation="gelu", logical_hidden=128)
     b = oracle.moe_forward(x, sel, sc, *layer2, 3, 0, activation="gelu")
     np.testing.assert_array_equal(a, b)
+
+
+# ---- the glue steps as ops (swiglu_down_input, finish_and_reduce) ----
+
+
+def test_oracle_finish_and_reduce_matches_staged_composition():
+    # built from the pinned staged Hadamard: f16(f16(H(f16(raw)) * svh) * score),
+    # summed in f32 over top-k in slot order and rounded once
+    rng = np.random.default_rng(11)
+    rows, top_k, width = 4, 3, 256
+    raw = (rng.normal(0, 30, (rows * top_k, width))).astype(np.float32)
+    svh = rng.uniform(0.5, 1.5, (rows * top_k, width)).astype(F16)
+    sc = rng.uniform(0, 1, (rows, top_k)).astype(F16)
+    got = oracle.finish_and_reduce(raw, svh, sc)
+    v = oracle.h128_staged(f16(raw))
+    part = f16(f16(v * svh.astype(np.float32)) * sc.reshape(-1, 1).astype(np.float32))
+    want = part.reshape(rows, top_k, width).sum(axis=1, dtype=np.float32).astype(F16)
+    np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+def test_oracle_swiglu_down_input_matches_f32_glue_composition():
+    # glu_down_input with SiLU from the pinned f32 Hadamard: numpy's f32 exp may
+    # differ from expf in the last bit, so the match is near-total, not exact
+    rng = np.random.default_rng(12)
+    slots, hidden, experts = 6, 256, 3
+    gate_up = rng.normal(0, 40, (slots * 2, hidden)).astype(np.float32)
+    gu_svh = (rng.uniform(0.5, 1.5, (experts, 2, hidden)) / 16).astype(F16)
+    down_suh = rng.choice([-1.0, 1.0], (experts, hidden)).astype(F16)
+    sel = rng.integers(0, experts, slots).astype(np.uint32)
+    got = oracle.swiglu_down_input(gate_up, gu_svh, down_suh, sel).astype(np.float32)
+    want = np.empty_like(got)
+    for s in range(slots):
+        e = sel[s]
+        g = f16(oracle.h128_f32(f16(gate_up[2 * s])) * gu_svh[e, 0].astype(np.float32))
+        u = f16(oracle.h128_f32(f16(gate_up[2 * s + 1])) * gu_svh[e, 1].astype(np.float32))
+        act = f16((g / (np.float32(1) + np.exp(-g))) * u)
+        want[s] = f16(oracle.h128_f32(f16(act * down_suh[e].astype(np.float32))))
+    assert rel_l2(got, want) < 1e-3
+    assert np.mean(got == want) > 0.99

@@ -180,6 +180,8 @@ int exl3_swiglu_down_input(const float* gate_up, const uint16_t* gu_svh, const u
   // glu_down_input's checks (moe.rs:459-467)
   if (slots <= 0 || slots > INT32_MAX || hidden <= 0 || hidden % 128)
     return fail(EXL3_EINVAL, "invalid fused SwiGLU dimensions");
+  if (hidden / 128 > 65535)  // grid.y holds the column blocks
+    return fail(EXL3_EUNSUPPORTED, "SwiGLU width %d is too large", hidden);
   if (experts <= 0 || !gu_svh || !down_suh || !selected)
     return fail(EXL3_EINVAL, "invalid fused SwiGLU scales/routes");
   if (!gate_up || !xhat) return fail(EXL3_EINVAL, "null SwiGLU buffer");
@@ -199,6 +201,10 @@ int exl3_finish_and_reduce(const float* raw, const uint16_t* svh, const uint16_t
                            void* stream) {
   // finish_and_reduce's checks (moe.rs:596-602)
   if (rows <= 0 || rows > INT32_MAX || top_k <= 0 || width <= 0 || width % 128)
+    return fail(EXL3_EINVAL, "invalid expert reduction dimensions");
+  if (width / 128 > 65535)  // grid.y holds the column blocks
+    return fail(EXL3_EUNSUPPORTED, "expert reduction width %d is too large", width);
+  if (rows * (int64_t)top_k > INT32_MAX)
     return fail(EXL3_EINVAL, "invalid expert reduction dimensions");
   if (!raw || !svh || !scores || !y) return fail(EXL3_EINVAL, "null expert reduction buffer");
   finish_and_reduce_kernel<<<dim3((unsigned)rows, width / 128), 64, 0, (hipStream_t)stream>>>(

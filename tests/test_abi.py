@@ -201,6 +201,25 @@ def test_geglu_rejects_before_launch():
     assert lib.exl3_geglu(None, None, None, 0, None) == 0
 
 
+def test_standalone_ops_reject_before_launch():
+    lib = mlxl3_amd.load_library()
+    err = lambda: lib.exl3_last_error().decode()
+    # prepare128_blocks (contracts.rs:2146-2159)
+    for elements, width, scales in ((128, 127, 127), (641, 640, 640), (1920, 640, 1919), (0, 0, 0)):
+        assert lib.exl3_prepare128(FAKE, elements, width, FAKE, scales, FAKE, None) == -1
+        assert "expected complete 128-aligned rows and column or element scales" in err()
+    assert lib.exl3_prepare128(None, 0, 128, None, 0, None, None) == 0
+    assert lib.exl3_pack_tiles(FAKE, 1, 0, FAKE, None) == -1 and "K must be in 1..=8" in err()
+    assert lib.exl3_pack_tiles(None, 0, 3, None, None) == 0
+    assert lib.exl3_swiglu_down_input(FAKE, FAKE, FAKE, FAKE, 4, 100, 2, FAKE, None) == -1
+    assert "invalid fused SwiGLU dimensions" in err()
+    assert lib.exl3_swiglu_down_input(FAKE, None, FAKE, FAKE, 4, 128, 2, FAKE, None) == -1
+    assert "invalid fused SwiGLU scales/routes" in err()
+    assert lib.exl3_finish_and_reduce(FAKE, FAKE, FAKE, 2, 2, 100, FAKE, None) == -1
+    assert "invalid expert reduction dimensions" in err()
+    assert lib.exl3_finish_and_reduce(FAKE, FAKE, FAKE, 2, 0, 128, FAKE, None) == -1
+
+
 def test_group_and_mlp_reject_before_launch():
     lib = mlxl3_amd.load_library()
     hs = [create(n_in=256, n_out=256)[1] for _ in range(9)]

@@ -12,7 +12,8 @@
 //   codebook                          GPU codewords (exl3_codewords)
 //   metal-qmv                         GPU inner QMV (exl3_qmv_inner)
 //   metal-swiglu                      GPU SwiGLU (exl3_swiglu)
-//   metal-prepare128                  GPU input prologue (exl3_prepare128)
+//   metal-prepare128, -prepare-view   GPU input prologue (exl3_prepare128), the
+//                                     latter on strided f16/f32 views
 //   mlx-linear, mlx-group             GPU Exl3Linear / Exl3Group forward
 //   mlx-switch                        GPU Exl3SwitchGlu forward (bank in the request)
 //   mlx-checkpoint-switch/-group      the same on projections of a checkpoint
@@ -51,7 +52,15 @@ struct Request {
   uint64_t key_heads = 0, top_k = 0;
   std::vector<uint16_t> data, x, suh, svh, beta, down_data, down_suh, down_svh;
   std::vector<uint32_t> selected;
-  std::vector<float> state;
+  std::vector<float> state, x_f32;
+  bool has_x_f32 = false;
+  // MatrixLayout (tensor_layout.rs:6-10) of x and of the scales, when given
+  struct Layout {
+    bool given = false;
+    uint32_t shape[2] = {0, 0};
+    int64_t strides[2] = {0, 0};
+    int64_t offset = 0;
+  } x_layout, scale_layout;
   std::vector<uint64_t> widths;
   std::string path, prefix;
   std::vector<std::string> prefixes;
@@ -67,6 +76,50 @@ std::vector<uint32_t> u32_array(const Value* v, const char* field) {
     out.push_back((uint32_t)e.u);
   }
   return out;
+}
+
+uint64_t uint_field(const Value* v, const char* field, uint64_t dflt, uint64_t max);
+
+int64_t i64_value(const Value& e, const char* field) {
+  if (e.is_number() && e.is_uint && e.u <= (uint64_t)INT64_MAX) return (int64_t)e.u;
+  if (e.is_number() && !e.is_uint && e.num < 0 && e.num >= -9.2233720368547758e18 &&
+      e.num == (double)(int64_t)e.num)
+    return (int64_t)e.num;
+  bail(std::string("invalid codec request: ") + field + " must hold i64 values");
+}
+
+Request::Layout layout_field(const Value* v, const char* field) {
+  Request::Layout l;
+  if (!v || v->kind == exl3::json::Kind::Null) return l;
+  const Value* shape = v->find("shape");
+  const Value* strides = v->find("strides");
+  const Value* offset = v->find("offset");
+  if (!v->is_object() || !shape || !shape->is_array() || shape->arr.size() != 2 || !strides ||
+      !strides->is_array() || strides->arr.size() != 2 || !offset)
+    bail(std::string("invalid codec request: ") + field + " must be a matrix layout");
+  for (int i = 0; i < 2; ++i) {
+    l.shape[i] = (uint32_t)uint_field(&shape->arr[i], field, 0, UINT32_MAX);
+    l.strides[i] = i64_value(strides->arr[i], field);
+  }
+  l.offset = i64_value(*offset, field);
+  l.given = true;
+  return l;
+}
+
+// MatrixLayout::fits (tensor_layout.rs:67-85): both extrema of the view inside
+// `elements`; an empty view may start one element past the end.
+bool layout_fits(const Request::Layout& l, uint64_t elements) {
+  if (elements > (uint64_t)INT64_MAX) return false;
+  const __int128 limit = (__int128)elements;
+  if (l.offset < 0 || l.offset > limit) return false;
+  if (l.shape[0] == 0 || l.shape[1] == 0) return true;
+  __int128 first = l.offset, last = l.offset;
+  for (int i = 0; i < 2; ++i) {
+    const __int128 reach = (__int128)(l.shape[i] - 1) * l.strides[i];
+    first += reach < 0 ? reach : 0;
+    last += reach > 0 ? reach : 0;
+  }
+  return first >= 0 && last < limit;
 }
 
 std::string string_field(const Value* v, const char* field) {
@@ -118,6 +171,16 @@ Request parse_request(const std::string& line) {
   r.key_heads = uint_field(v.find("key_heads"), "key_heads", 0, UINT64_MAX);
   r.top_k = uint_field(v.find("top_k"), "top_k", 0, UINT64_MAX);
   r.selected = u32_array(v.find("selected"), "selected");
+  if (const Value* xf = v.find("x_f32"); xf && xf->kind != exl3::json::Kind::Null) {
+    if (!xf->is_array()) bail("invalid codec request: x_f32 must be an array");
+    r.has_x_f32 = true;
+    for (const Value& e : xf->arr) {
+      if (!e.is_number()) bail("invalid codec request: x_f32 must hold numbers");
+      r.x_f32.push_back((float)e.num);
+    }
+  }
+  r.x_layout = layout_field(v.find("x_layout"), "x_layout");
+  r.scale_layout = layout_field(v.find("scale_layout"), "scale_layout");
   if (const Value* st = v.find("state")) {
     if (!st->is_array()) bail("invalid codec request: state must be an array");
     for (const Value& e : st->arr) {
@@ -359,6 +422,36 @@ std::string run(const Request& r) {
     DeviceBuffer st(r.data), out((size_t)tiles * 16 * r.k * 2);
     lib_check(exl3_pack_tiles(st.as<uint16_t>(), tiles, (int)r.k, out.as<uint16_t>(), nullptr));
     return json_list(out.read<uint16_t>((size_t)tiles * 16 * r.k));
+  }
+  if (r.op == "metal-prepare-view") {  // main.rs:1294-1302, gpu/view.rs:181-195, :257-272
+    // input_view (main.rs:261-270), TensorStorage::matrix (gpu/view.rs:30-41)
+    if (!r.x_layout.given) bail("missing input matrix layout");
+    if (r.has_x_f32 && !r.x.empty()) bail("conflicting input buffer dtypes");
+    if (!layout_fits(r.x_layout, r.has_x_f32 ? r.x_f32.size() : r.x.size()))
+      bail("matrix view outside initialized storage");
+    if (!r.scale_layout.given) bail("missing scale matrix layout");
+    if (!layout_fits(r.scale_layout, r.data.size())) bail("matrix view outside initialized storage");
+    const Request::Layout &xl = r.x_layout, &sl = r.scale_layout;
+    if (xl.shape[0] != sl.shape[0] || xl.shape[1] != sl.shape[1])
+      bail("invalid H128 view shape or scale dtype");
+    const uint64_t rows = xl.shape[0], cols = xl.shape[1], n = rows * cols;
+    if (n > UINT32_MAX) bail("H128 view size overflow");
+    if (cols == 0 || cols % 128) bail("H128 view width must be positive and 128-aligned");
+    if (n == 0) return "[]";
+    // gather both views into rows x cols (x as f16: astype rounds to nearest even)
+    std::vector<uint16_t> xs(n), ss(n);
+    for (uint64_t i = 0; i < rows; ++i)
+      for (uint64_t j = 0; j < cols; ++j) {
+        const int64_t xi = xl.offset + (int64_t)i * xl.strides[0] + (int64_t)j * xl.strides[1];
+        const int64_t si = sl.offset + (int64_t)i * sl.strides[0] + (int64_t)j * sl.strides[1];
+        xs[i * cols + j] = r.has_x_f32 ? __builtin_bit_cast(uint16_t, (_Float16)r.x_f32[xi])
+                                       : r.x[xi];
+        ss[i * cols + j] = r.data[si];
+      }
+    DeviceBuffer x(xs), sc(ss), o(n * 2);
+    lib_check(exl3_prepare128(x.as<uint16_t>(), (int64_t)n, (int)cols, sc.as<uint16_t>(),
+                              (int64_t)n, o.as<uint16_t>(), nullptr));
+    return json_list(o.read<uint16_t>(n));
   }
   if (r.op == "metal-prepare128") {  // main.rs:1338-1342, gpu.rs:1537-1558
     // extents checked before any upload, as prepare128_blocks (contracts.rs:2146-2159)

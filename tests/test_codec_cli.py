@@ -127,3 +127,29 @@ def test_malformed_lines_and_defaults():
     assert rows[2] == {"data": []}  # default k = 4 is valid, nothing to pack
     bad = subprocess.run([str(CODEC), "serve"], capture_output=True, text=True, timeout=60)
     assert bad.returncode == 2
+
+
+def test_prepare_view_rejections_of_the_reference_harness():
+    """The rejected metal-prepare-view requests of the reference's
+    tests/physical_prepare128.py, answered before any GPU work, and its empty
+    view starting one element past the storage."""
+    view = {"shape": [1, 128], "strides": [0, 0], "offset": 0}
+    zero = {"op": "metal-prepare-view", "x": [0], "data": [0], "x_layout": view,
+            "scale_layout": view}
+    cases = [({"x_layout": {**view, "strides": [0, -1]}}, "outside initialized storage"),
+             ({"scale_layout": {**view, "strides": [0, 2 ** 63 - 1]}}, "outside initialized storage"),
+             ({"x_layout": {**view, "offset": -1}}, "outside initialized storage"),
+             ({"x_layout": {**view, "shape": [2, 128]}}, "invalid H128 view shape"),
+             ({"x_f32": [0]}, "conflicting input buffer dtypes"),
+             ({"x_layout": None}, "missing input matrix layout"),
+             ({"scale_layout": None}, "missing scale matrix layout"),
+             ({"x_layout": {**view, "shape": [1, 127]}, "scale_layout": {**view, "shape": [1, 127]}},
+              "128-aligned"),
+             ({"x_layout": {**view, "shape": [2 ** 31, 128]},
+               "scale_layout": {**view, "shape": [2 ** 31, 128]}}, "size overflow")]
+    one_past = {**view, "shape": [0, 128], "offset": 1}
+    rows = run([{**zero, **f} for f, _ in cases] + [{**zero, "x_layout": one_past,
+                                                     "scale_layout": one_past}])
+    for (_, msg), row in zip(cases, rows):
+        assert msg in row.get("error", ""), (msg, row)
+    assert rows[-1] == {"data": []}

@@ -168,3 +168,44 @@ def test_prepare128_codec_and_abi_match_the_oracle():
     # basis rows: xhat is the normalised Sylvester row (exact in f16)
     basis = np.asarray(prepare128_oracle(*cases[0][1:])).astype(np.float64)
     assert np.all(np.abs(np.abs(basis) - 2 ** -3.5) < 2 ** -14)
+
+
+def test_prepare_view_strided_views_match_the_oracle():
+    """The view cases of the reference's physical_prepare128.py: transposed,
+    reversed, negative-stride and broadcast views of f16 and f32 storage with
+    guard words around each backing array, against the oracle on the gathered
+    rows (element scales)."""
+    rng = np.random.default_rng(75)
+    reqs, wants, names = [], [], []
+    for width in (128, 640, 2560):
+        rows = 3
+        for dtype in (np.float16, np.float32):
+            base = rng.normal(0, 0.5, (2 * width + 2, rows + 2)).astype(dtype)
+            scales = rng.normal(0, 0.75, (rows + 2, width + 2)).astype(np.float16)
+            for name, x, sv in (
+                ("transpose-reverse", base[1:-1:2, -2:0:-1].T, scales[1:-1, -2:0:-1]),
+                ("negative-row-col", base[-2:0:-2, -2:0:-1].T, scales[-2:0:-1, 1:-1]),
+                ("row-broadcast", np.broadcast_to(base[1:-1:2, 1], (rows, width)), scales[1:-1, 1:-1]),
+                ("column-broadcast", np.broadcast_to(base[1, 1:-1, None], (rows, width)),
+                 np.broadcast_to(scales[1, 1:-1], (rows, width))),
+            ):
+                def layout(view, backing):
+                    return {"shape": list(view.shape),
+                            "strides": [v // view.itemsize for v in view.strides],
+                            "offset": (view.ctypes.data - backing.ctypes.data) // view.itemsize}
+
+                field = "x" if dtype == np.float16 else "x_f32"
+                raw = base.view(np.uint16) if dtype == np.float16 else base
+                reqs.append({"op": "metal-prepare-view", field: raw.ravel().tolist(),
+                             "x_layout": layout(x, base), "scale_layout": layout(sv, scales),
+                             "data": scales.view(np.uint16).ravel().tolist()})
+                xs = np.ascontiguousarray(x).astype(np.float16)
+                ss = np.ascontiguousarray(sv)
+                wants.append(np.concatenate([oracle.prologue(xs[r:r + 1], ss[r]) for r in range(rows)]))
+                names.append(f"{name}-{width}-{dtype.__name__}")
+    rows_out = run(reqs)
+    for name, want, row in zip(names, wants, rows_out):
+        got = np.array(row["data"], np.uint16)
+        bad = int((got != want.view(np.uint16).ravel()).sum())
+        print(f"prepare-view {name}: {bad} of {got.size} differ", flush=True)
+        assert bad == 0, name

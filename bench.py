@@ -186,8 +186,8 @@ def moe_leg(steps, warmup):
     stream = torch.cuda.current_stream()
 
     def call(m):  # on the current stream (the capture stream inside torch.cuda.graph)
-        rc = lib.exl3_moe_forward(m._handle, x.data_ptr(), rows, sel.data_ptr(), sc.data_ptr(),
-                                  y.data_ptr(), ws.data_ptr(), ws.numel(),
+        rc = lib.exl3_moe_forward(m._handle, x.data_ptr(), 9, rows, sel.data_ptr(), sc.data_ptr(),
+                                  9, y.data_ptr(), ws.data_ptr(), ws.numel(),
                                   ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
         if rc:
             raise RuntimeError(lib.exl3_last_error().decode())

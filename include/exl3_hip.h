@@ -86,17 +86,27 @@ size_t exl3_linear_workspace_bytes(const exl3_linear* handle, int64_t rows);
  * be recorded into a graph). */
 int exl3_workspace_init(void* workspace, size_t bytes, void* stream);
 
+/* Output dtype of a projection for activations of x_type (linear.rs:992-995:
+ * y.astype(x.dtype) + bias with the f16 bias under MLX's type promotion):
+ * x_type without a bias; with a bias f16 -> f16, f32 -> f32 and bf16 -> f32
+ * (MLX promotes bfloat16 + float16 to float32).  -1 for a null handle or an
+ * unknown dtype. */
+int32_t exl3_linear_output_dtype(const exl3_linear* handle, int32_t x_type);
+
 /* Exl3Linear::forward, linear.rs:731-998: y[rows][out] = EXL3 linear of
- * x[rows][in].  x_type / y_type: exl3_dtype (the reference returns x's dtype;
- * other output types are a superset).  rows >= 1.  rows <= 16 runs the fused
- * multi-row QMV (one launch); larger rows run the prologue and the QMM. */
+ * x[rows][in].  x_type: exl3_dtype; y_type must equal
+ * exl3_linear_output_dtype(handle, x_type) (EXL3_EINVAL otherwise): the f16
+ * result is cast to x's dtype, then the bias is added in the promoted dtype.
+ * rows >= 1.  rows <= 16 runs the fused multi-row QMV (one launch); larger
+ * rows run the prologue and the QMM. */
 int exl3_linear_forward(const exl3_linear* handle, const void* x, int32_t x_type, int64_t rows,
                         void* y, int32_t y_type, void* workspace, size_t workspace_bytes,
                         void* stream);
 
 /* Exl3Group::new/forward, linear.rs:2285-2382: up to 8 projections with the
  * same input width, K and codebook applied to one x (q/k/v, gate/up); ys[i]
- * receives parts[i]'s output (dtype of x).  One launch covers every member's
+ * receives parts[i]'s output in exl3_linear_output_dtype(parts[i], x_type)
+ * (x's dtype; f32 for a biased member under bf16 activations).  One launch covers every member's
  * column blocks (rows <= 16), or one prologue launch and one QMM launch (rows
  * > 16); each member's output is bit-identical to its own exl3_linear_forward.
  * Workspace: exl3_group_workspace_bytes. */
@@ -153,13 +163,24 @@ int exl3_moe_create_gelu(const uint16_t* gu_trellis, const uint16_t* gu_suh,
                          int32_t hidden, int32_t experts, int32_t top_k, int32_t k, int32_t cb,
                          int32_t logical_hidden, exl3_moe** out_handle);
 void exl3_moe_destroy(exl3_moe* handle);
+/* Input width and per-expert hidden width of a SwitchGLU handle (the
+ * reference's Exl3SwitchGlu input / hidden fields, moe.rs:886-896); 0 for a
+ * null handle. */
+int32_t exl3_moe_in_features(const exl3_moe* handle);
+int32_t exl3_moe_hidden_features(const exl3_moe* handle);
 size_t exl3_moe_workspace_bytes(const exl3_moe* handle, int64_t rows);
 
-/* Exl3SwitchGlu::forward, moe.rs:905-975: x f16[rows][in], selected
- * u32[rows][top_k] (< experts), scores f16[rows][top_k]; y f16[rows][in].
- * The routing plan (moe.rs:66-182) is built on the device. */
-int exl3_moe_forward(const exl3_moe* handle, const uint16_t* x, int64_t rows,
-                     const uint32_t* selected, const uint16_t* scores, uint16_t* y,
+/* Exl3SwitchGlu::forward, moe.rs:905-975: x [rows][in] of x_type (f16, bf16
+ * or f32; cast to f16 before the input scales, as routed_inputs reads
+ * half(x), moe.rs:205-206), selected u32[rows][top_k] (< experts), scores
+ * [rows][top_k] of scores_type.  y [rows][in] in the dtype of the reference's
+ * weighted sum (finish_and_reduce, moe.rs:602-608: f16 expert outputs times
+ * the scores, summed over top_k): f16 for f16 scores (f16 products, f32 sum
+ * rounded to f16); f32 for f32 or bf16 scores (MLX promotes f16 * f32 and
+ * f16 * bf16 to f32: f32 products and sum).  The routing plan (moe.rs:66-182)
+ * is built on the device. */
+int exl3_moe_forward(const exl3_moe* handle, const void* x, int32_t x_type, int64_t rows,
+                     const uint32_t* selected, const void* scores, int32_t scores_type, void* y,
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* The input prologue of every EXL3 projection as an op of its own,
@@ -181,14 +202,15 @@ int exl3_prepare128(const uint16_t* x, int64_t elements, int32_t width, const ui
  * [experts][2][hidden], down_suh f16 [experts][hidden], selected u32 [slots]
  * -> xhat f16 [slots][hidden], the down projection's input (slots routed to
  * ids >= experts get zeros).  finish_and_reduce (moe.rs:586-609): raw f32
- * [rows*top_k][width], svh f16 [rows*top_k][width], scores f16 [rows][top_k]
- * -> y f16 [rows][width]. */
+ * [rows*top_k][width], svh f16 [rows*top_k][width], scores [rows][top_k] of
+ * scores_type -> y [rows][width], f16 for f16 scores and f32 for f32 or bf16
+ * scores (the promotion of exl3_moe_forward). */
 int exl3_swiglu_down_input(const float* gate_up, const uint16_t* gu_svh, const uint16_t* down_suh,
                            const uint32_t* selected, int64_t slots, int32_t hidden,
                            int32_t experts, uint16_t* xhat, void* stream);
-int exl3_finish_and_reduce(const float* raw, const uint16_t* svh, const uint16_t* scores,
-                           int64_t rows, int32_t top_k, int32_t width, uint16_t* y,
-                           void* stream);
+int exl3_finish_and_reduce(const float* raw, const uint16_t* svh, const void* scores,
+                           int32_t scores_type, int64_t rows, int32_t top_k, int32_t width,
+                           void* y, void* stream);
 
 /* Decode hook, the reference's `metal-decode` codec op (exl3.metal:102-109,
  * main.rs:945-967): for every tile, states[t*256 + i] (nullable) and the f16

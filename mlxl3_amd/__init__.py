@@ -78,6 +78,7 @@ _SIGNATURES = {
     "exl3_linear_out_features": (_i32, [_vp]),
     "exl3_linear_workspace_bytes": (_sz, [_vp, _i64]),
     "exl3_workspace_init": (_i32, [_vp, _sz, _vp]),
+    "exl3_linear_output_dtype": (_i32, [_vp, _i32]),
     "exl3_linear_forward": (_i32, [_vp, _vp, _i32, _i64, _vp, _i32, _vp, _sz, _vp]),
     "exl3_group_workspace_bytes": (_sz, [_vp, _i32, _i64]),
     "exl3_group_forward": (_i32, [_vp, _i32, _vp, _i32, _i64, _vp, _vp, _sz, _vp]),
@@ -95,10 +96,12 @@ _SIGNATURES = {
          ctypes.POINTER(_vp)],
     ),
     "exl3_moe_destroy": (None, [_vp]),
+    "exl3_moe_in_features": (_i32, [_vp]),
+    "exl3_moe_hidden_features": (_i32, [_vp]),
     "exl3_moe_workspace_bytes": (_sz, [_vp, _i64]),
-    "exl3_moe_forward": (_i32, [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "exl3_moe_forward": (_i32, [_vp, _vp, _i32, _i64, _vp, _vp, _i32, _vp, _vp, _sz, _vp]),
     "exl3_swiglu_down_input": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp]),
-    "exl3_finish_and_reduce": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp]),
+    "exl3_finish_and_reduce": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp]),
     "exl3_prepare128": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _vp]),
     "exl3_decode_tiles": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _vp]),
     "exl3_codewords": (_i32, [_vp, _i64, _i32, _vp, _vp]),
@@ -174,6 +177,30 @@ def _dtype_code(dtype) -> int:
         raise Exl3Error(-1, f"unsupported activation dtype {dtype}") from None
 
 
+def _code_dtype(code: int):
+    _dtype_code(_torch().float16)  # fills the table
+    for dtype, c in _DTYPE_CODES.items():
+        if c == code:
+            return dtype
+    raise Exl3Error(-1, f"unsupported dtype code {code}")
+
+
+def result_dtype(x_dtype, has_bias: bool):
+    """Output dtype of a projection (linear.rs:992-995): y.astype(x.dtype) + an
+    f16 bias under MLX's promotion -- x's dtype without a bias; with one,
+    float16 stays float16 and bfloat16 or float32 give float32."""
+    torch = _torch()
+    return torch.float32 if has_bias and x_dtype == torch.bfloat16 else x_dtype
+
+
+def scores_result_dtype(scores_dtype):
+    """Output dtype of the SwitchGLU's weighted top-k sum (finish_and_reduce,
+    moe.rs:602-608): f16 expert outputs times the scores -- float16 for
+    float16 scores, float32 for float32 or bfloat16 ones (MLX promotes)."""
+    torch = _torch()
+    return torch.float16 if scores_dtype == torch.float16 else torch.float32
+
+
 def _stream_ptr(device) -> int:
     torch = _torch()
     return torch.cuda.current_stream(device).cuda_stream
@@ -195,7 +222,12 @@ def _require_device(t, name: str, dtypes=None):
 
 
 class _Workspace:
-    """Per-device zero-initialised workspace, grown on demand."""
+    """Per-device zero-initialised workspace, grown on demand.
+
+    A workspace handed to a forward call by its caller must likewise have been
+    zero-filled once (``torch.zeros``, or ``exl3_workspace_init``): the split-K
+    kernels count arrivals in its first 64 KiB, which every call leaves at zero
+    again.  Calls sharing one workspace must not run concurrently (one stream)."""
 
     def __init__(self):
         self.buf = None
@@ -403,8 +435,20 @@ class Exl3Linear:
     def workspace_bytes(self, rows: int) -> int:
         return int(load_library().exl3_linear_workspace_bytes(self._handle, int(rows)))
 
-    def forward(self, x, out_dtype=None, workspace=None):
-        """y = linear(x) for x [..., in]; output dtype = x.dtype unless given."""
+    @property
+    def has_bias(self) -> bool:
+        lib = load_library()
+        return lib.exl3_linear_output_dtype(self._handle, 12) == 10  # bf16 -> f32 iff a bias
+
+    def output_dtype(self, x_dtype):
+        """The dtype forward returns for x_dtype activations (result_dtype)."""
+        code = load_library().exl3_linear_output_dtype(self._handle, _dtype_code(x_dtype))
+        return _code_dtype(code)
+
+    def forward(self, x, workspace=None):
+        """y = linear(x) for x [..., in] (f16, bf16 or f32); y has x's dtype, or
+        float32 for bfloat16 activations with a bias (result_dtype).  A given
+        workspace must have been zero-filled once (see _Workspace)."""
         torch = _torch()
         x = _require_device(x, "x", (torch.float16, torch.bfloat16, torch.float32))
         if x.shape[-1] != self.in_features or x.numel() % self.in_features:
@@ -412,7 +456,7 @@ class Exl3Linear:
         rows = x.numel() // self.in_features
         if rows == 0:
             raise Exl3Error(-1, "EXL3 linear input cannot be empty")
-        out_dtype = x.dtype if out_dtype is None else out_dtype
+        out_dtype = self.output_dtype(x.dtype)
         y = torch.empty(*x.shape[:-1], self.out_features, dtype=out_dtype, device=x.device)
         need = self.workspace_bytes(rows)
         ws = workspace if workspace is not None else self._ws.get(need, x.device)
@@ -455,7 +499,8 @@ class Exl3Group:
         rows = x.numel() // n_in
         if rows == 0:
             raise Exl3Error(-1, "grouped EXL3 input cannot be empty")
-        ys = [torch.empty(*x.shape[:-1], l.out_features, dtype=x.dtype, device=x.device) for l in self.linears]
+        ys = [torch.empty(*x.shape[:-1], l.out_features, dtype=l.output_dtype(x.dtype), device=x.device)
+              for l in self.linears]
         ws = self._ws.get(self.workspace_bytes(rows), x.device)
         outs = (_vp * len(ys))(*[y.data_ptr() for y in ys])
         _check(
@@ -505,19 +550,20 @@ def swiglu_down_input(gate_up, gu_svh, down_suh, selected):
 
 def finish_and_reduce(raw, svh, scores):
     """finish_and_reduce (moe.rs:586-609) on device tensors: f32 raw
-    [rows*top_k, width], f16 svh of the same shape, f16 scores [rows, top_k]
-    -> f16 [rows, width]."""
+    [rows*top_k, width], f16 svh of the same shape, scores [rows, top_k]
+    (float16, bfloat16 or float32) -> [rows, width] in scores_result_dtype."""
     torch = _torch()
     raw = _require_device(raw, "raw", (torch.float32,))
     svh = _require_device(svh, "svh", (torch.float16,))
-    scores = _require_device(scores, "scores", (torch.float16,))
+    scores = _require_device(scores, "scores", (torch.float16, torch.bfloat16, torch.float32))
     rows, top_k = scores.shape
     width = raw.shape[-1]
     if raw.numel() != rows * top_k * width or svh.shape != raw.shape:
         raise Exl3Error(-1, "invalid expert reduction dimensions")
-    y = torch.empty(rows, width, dtype=torch.float16, device=raw.device)
-    _check(load_library().exl3_finish_and_reduce(_ptr(raw), _ptr(svh), _ptr(scores), rows, top_k,
-                                                 width, _ptr(y), _stream_ptr(raw.device)))
+    y = torch.empty(rows, width, dtype=scores_result_dtype(scores.dtype), device=raw.device)
+    _check(load_library().exl3_finish_and_reduce(_ptr(raw), _ptr(svh), _ptr(scores),
+                                                 _dtype_code(scores.dtype), rows, top_k, width,
+                                                 _ptr(y), _stream_ptr(raw.device)))
     return y
 
 
@@ -595,11 +641,30 @@ class Exl3SwitchGlu:
                  logical_hidden: Optional[int] = None):
         torch = _torch()
         lib = load_library()
-        in_tiles, gu_cols, k16 = gu_trellis.shape
-        experts = gu_suh.shape[0]
-        hidden = gu_svh.shape[-1]
-        self.input, self.hidden, self.experts, self.top_k = in_tiles * 16, hidden, experts, int(top_k)
-        self.k, self.cb = int(k), int(cb)
+        # Exl3SwitchGlu::new_with_activation's checks and messages (moe.rs:851-879),
+        # before anything reaches the device
+        if len(gu_suh.shape) != 3:
+            raise Exl3Error(-1, "gate/up input scales must have rank 3")
+        if len(gu_svh.shape) != 3:
+            raise Exl3Error(-1, "gate/up output scales must have rank 3")
+        experts, projections, n_in = (int(d) for d in gu_suh.shape)
+        scale_experts, scale_projections, hidden = (int(d) for d in gu_svh.shape)
+        top_k, k = int(top_k), int(k)
+        if (experts <= 0 or top_k <= 0 or top_k > experts or n_in <= 0 or hidden <= 0
+                or n_in % 128 or hidden % 128 or not 1 <= k <= 8 or k == 7
+                or experts * hidden > 2**31 - 1 or experts * n_in > 2**31 - 1):
+            raise Exl3Error(-1, "invalid or overflowing SwitchGLU dimensions")
+        if projections != 2 or scale_experts != experts or scale_projections != 2:
+            raise Exl3Error(-1, "invalid SwitchGLU dimensions")
+        gu_tiles, down_tiles, packed = experts * hidden // 8, experts * n_in // 16, 16 * k
+        if (tuple(down_suh.shape) != (experts, hidden) or tuple(down_svh.shape) != (experts, n_in)
+                or tuple(gu_trellis.shape) != (n_in // 16, gu_tiles, packed)
+                or tuple(down_trellis.shape) != (hidden // 16, down_tiles, packed)):
+            raise Exl3Error(-1, "SwitchGLU trellis/scales disagree")
+        if any(t.dtype not in (torch.int16, torch.uint16) for t in (gu_trellis, down_trellis)):
+            raise Exl3Error(-1, "expert trellis must contain 16-bit integers")
+        self.input, self.hidden, self.experts, self.top_k = n_in, hidden, experts, top_k
+        self.k, self.cb = k, int(cb)
         if activation not in ("silu", "gelu"):
             raise Exl3Error(-1, f"unknown GLU activation {activation!r}")
         self.activation = activation
@@ -689,21 +754,26 @@ class Exl3SwitchGlu:
             self._handle = None
 
     def forward(self, x, selected, scores):
+        """Exl3SwitchGlu::forward (moe.rs:905-975): x [rows, in] (float16,
+        bfloat16 or float32; cast to f16 as routed_inputs reads it), selected
+        [rows, top_k] expert ids, scores [rows, top_k] (float16, bfloat16 or
+        float32, kept in their dtype) -> [rows, in] in scores_result_dtype."""
         torch = _torch()
-        x = _require_device(x, "x", (torch.float16,))
+        floats = (torch.float16, torch.bfloat16, torch.float32)
+        x = _require_device(x, "x", floats)
         rows = x.shape[0]
         if x.dim() != 2 or x.shape[1] != self.input or tuple(selected.shape) != (rows, self.top_k) \
                 or tuple(scores.shape) != (rows, self.top_k):
             raise Exl3Error(-1, "invalid SwitchGLU input/routes")
         selected = _require_device(selected, "selected").to(torch.int32).contiguous()
-        scores = _require_device(scores, "scores").to(torch.float16).contiguous()
-        y = torch.empty_like(x)
+        scores = _require_device(scores, "scores", floats)
+        y = torch.empty(rows, self.input, dtype=scores_result_dtype(scores.dtype), device=x.device)
         need = int(load_library().exl3_moe_workspace_bytes(self._handle, rows))
         ws = self._ws.get(need, x.device)
         _check(
             load_library().exl3_moe_forward(
-                self._handle, _ptr(x), rows, _ptr(selected), _ptr(scores), _ptr(y), _ptr(ws),
-                ws.numel(), _stream_ptr(x.device),
+                self._handle, _ptr(x), _dtype_code(x.dtype), rows, _ptr(selected), _ptr(scores),
+                _dtype_code(scores.dtype), _ptr(y), _ptr(ws), ws.numel(), _stream_ptr(x.device),
             )
         )
         return y

@@ -36,6 +36,13 @@ int exl3::check_launch(const char* what) {
 
 static bool valid_dtype(int dt) { return dt == EXL3_F16 || dt == EXL3_F32 || dt == EXL3_BF16; }
 
+// Output dtype of a projection (linear.rs:992-995): y.astype(x.dtype) + bias
+// with the f16 bias, under MLX's promotion -- bf16 + f16 is f32, f16 + f16
+// f16, f32 + f16 f32; without a bias the activation dtype.
+static int result_dtype(int x_type, bool has_bias) {
+  return has_bias && x_type == EXL3_BF16 ? EXL3_F32 : x_type;
+}
+
 // ---------------------------------------------------------------------------
 // handles
 // ---------------------------------------------------------------------------
@@ -214,7 +221,7 @@ static int check_rows(const Group& g, int64_t rows) {
   return EXL3_OK;
 }
 
-static Member member_of(const exl3_linear* h, void* y, int cblk0) {
+static Member member_of(const exl3_linear* h, void* y, int cblk0, int x_type) {
   Member m;
   m.trellis = (const uint32_t*)h->trellis;
   m.suh = h->suh;
@@ -224,17 +231,18 @@ static Member member_of(const exl3_linear* h, void* y, int cblk0) {
   m.y = y;
   m.out = h->out;
   m.cblk0 = cblk0;
+  m.y_dtype = result_dtype(x_type, h->bias != nullptr);
   return m;
 }
 
 // One QMV launch (rows <= 16) over the group; `glu` for a (gate, up) pair.
 static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows,
-                         void* const* ys, int y_type, uint32_t* counters, char* scratch,
-                         const Glu& glu, hipStream_t stream) {
+                         void* const* ys, uint32_t* counters, char* scratch, const Glu& glu,
+                         hipStream_t stream) {
   QmvParams p{};
   int cblk0 = 0;
   for (int i = 0; i < g.count; ++i) {
-    p.mem[i] = member_of(g.parts[i], ys[i], cblk0);
+    p.mem[i] = member_of(g.parts[i], ys[i], cblk0, x_type);
     cblk0 += g.parts[i]->out / 128;
   }
   int kw;
@@ -263,7 +271,6 @@ static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows
   p.total_out = g.total_out;
   p.M = (int)rows;
   p.x_dtype = x_type;
-  p.y_dtype = y_type;
   p.glu = glu;
   const int nb = g.in / 128;
   int max_blocks = 0;
@@ -280,7 +287,7 @@ static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows
 // Prologue (one launch for all members) and one QMM launch over the group.
 // xhats: per member, null to run the prologue into the scratch.
 static int run_group_qmm(const Group& g, const void* x, int x_type, int64_t rows,
-                         void* const* ys, int y_type, uint32_t* counters, char* scratch,
+                         void* const* ys, uint32_t* counters, char* scratch,
                          const uint16_t* given_xhat, hipStream_t stream) {
   const size_t xbytes = align_up(sizeof(uint16_t) * (size_t)rows * g.in);
   QmmParams q{};
@@ -299,7 +306,7 @@ static int run_group_qmm(const Group& g, const void* x, int x_type, int64_t rows
   }
   int cblk0 = 0;
   for (int i = 0; i < g.count; ++i) {
-    q.mem[i] = member_of(g.parts[i], ys[i], cblk0);
+    q.mem[i] = member_of(g.parts[i], ys[i], cblk0, x_type);
     q.mem[i].xhat = given_xhat ? given_xhat : (const uint16_t*)(scratch + i * xbytes);
     cblk0 += g.parts[i]->out / 128;
   }
@@ -310,7 +317,7 @@ static int run_group_qmm(const Group& g, const void* x, int x_type, int64_t rows
   q.in = g.in;
   q.total_out = g.total_out;
   q.M = (int)rows;
-  q.y_dtype = y_type;
+  q.x_dtype = x_type;
   q.col_blocks = g.total_out / 128;
   q.mtiles = sh.mtiles;
   q.splits = sh.splits;
@@ -322,13 +329,11 @@ static int run_group_qmm(const Group& g, const void* x, int x_type, int64_t rows
 }
 
 static int group_forward(const Group& g, const void* x, int x_type, int64_t rows,
-                         void* const* ys, int y_type, void* ws, size_t ws_bytes,
-                         hipStream_t stream) {
+                         void* const* ys, void* ws, size_t ws_bytes, hipStream_t stream) {
   if (!x) return fail(EXL3_EINVAL, "null activation pointer");
   for (int i = 0; i < g.count; ++i)
     if (!ys[i]) return fail(EXL3_EINVAL, "null activation pointer");
-  if (!valid_dtype(x_type) || !valid_dtype(y_type))
-    return fail(EXL3_EINVAL, "unsupported dtype codes %d -> %d", x_type, y_type);
+  if (!valid_dtype(x_type)) return fail(EXL3_EINVAL, "unsupported activation dtype code %d", x_type);
   if (int rc = check_rows(g, rows)) return rc;
   const size_t need = kWorkspaceCounterBytes + group_scratch_bytes(g, rows);
   if (!ws || ws_bytes < need)
@@ -336,9 +341,8 @@ static int group_forward(const Group& g, const void* x, int x_type, int64_t rows
   uint32_t* counters = (uint32_t*)ws;
   char* scratch = (char*)ws + kWorkspaceCounterBytes;
   const Glu none{};
-  if (rows <= kQmvMaxRows)
-    return run_group_qmv(g, x, x_type, rows, ys, y_type, counters, scratch, none, stream);
-  return run_group_qmm(g, x, x_type, rows, ys, y_type, counters, scratch, nullptr, stream);
+  if (rows <= kQmvMaxRows) return run_group_qmv(g, x, x_type, rows, ys, counters, scratch, none, stream);
+  return run_group_qmm(g, x, x_type, rows, ys, counters, scratch, nullptr, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -408,21 +412,18 @@ static int mlp_forward(const exl3_linear* gate, const exl3_linear* up, const exl
     glu.on = 1;
     glu.out = act;
     void* gu_y[2] = {nullptr, nullptr};  // not written: the edge consumes the partials
-    if (int rc = run_group_qmv(g, x, EXL3_F16, rows, gu_y, EXL3_F16, counters, base + act_bytes,
-                               glu, stream))
+    if (int rc = run_group_qmv(g, x, EXL3_F16, rows, gu_y, counters, base + act_bytes, glu, stream))
       return rc;
-    return run_group_qmv(d, act, EXL3_F16, rows, dy, EXL3_F16, counters, base + act_bytes, Glu{},
-                         stream);
+    return run_group_qmv(d, act, EXL3_F16, rows, dy, counters, base + act_bytes, Glu{}, stream);
   }
   void* gu_y[2] = {base + act_bytes, base + 2 * act_bytes};
   char* scratch = base + 3 * act_bytes;
-  if (int rc = run_group_qmm(g, x, EXL3_F16, rows, gu_y, EXL3_F16, counters, scratch, nullptr,
-                             stream))
+  if (int rc = run_group_qmm(g, x, EXL3_F16, rows, gu_y, counters, scratch, nullptr, stream))
     return rc;
   launch_swiglu_prepare((const uint16_t*)gu_y[0], (const uint16_t*)gu_y[1], down->suh, gate->out,
                         (int)rows, act, stream);
   if (int rc = check_launch("SwiGLU prepare launch")) return rc;
-  return run_group_qmm(d, nullptr, EXL3_F16, rows, dy, EXL3_F16, counters, scratch, act, stream);
+  return run_group_qmm(d, nullptr, EXL3_F16, rows, dy, counters, scratch, act, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -495,13 +496,24 @@ int exl3_workspace_init(void* workspace, size_t bytes, void* stream) {
   return check_launch("workspace init");
 }
 
+int32_t exl3_linear_output_dtype(const exl3_linear* h, int32_t x_type) {
+  if (!h || !valid_dtype(x_type)) return -1;
+  return result_dtype(x_type, h->bias != nullptr);
+}
+
 int exl3_linear_forward(const exl3_linear* h, const void* x, int32_t x_type, int64_t rows, void* y,
                         int32_t y_type, void* workspace, size_t workspace_bytes, void* stream) {
   if (!h) return fail(EXL3_EINVAL, "null EXL3 linear handle");
+  if (!valid_dtype(x_type)) return fail(EXL3_EINVAL, "unsupported activation dtype code %d", x_type);
+  const int want = result_dtype(x_type, h->bias != nullptr);
+  if (y_type != want)
+    return fail(EXL3_EINVAL,
+                "EXL3 output dtype %d differs from the projection's result dtype %d (the input "
+                "dtype, promoted with the f16 bias)",
+                y_type, want);
   Group g;
   if (int rc = make_group(&h, 1, g)) return rc;
-  return group_forward(g, x, x_type, rows, &y, y_type, workspace, workspace_bytes,
-                       (hipStream_t)stream);
+  return group_forward(g, x, x_type, rows, &y, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 int exl3_group_forward(const exl3_linear* const* parts, int32_t count, const void* x,
@@ -510,8 +522,7 @@ int exl3_group_forward(const exl3_linear* const* parts, int32_t count, const voi
   if (!ys) return fail(EXL3_EINVAL, "empty EXL3 group");
   Group g;
   if (int rc = make_group(parts, count, g)) return rc;
-  return group_forward(g, x, x_type, rows, ys, x_type, workspace, workspace_bytes,
-                       (hipStream_t)stream);
+  return group_forward(g, x, x_type, rows, ys, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 int exl3_mlp_forward(const exl3_linear* gate, const exl3_linear* up, const exl3_linear* down,

@@ -354,8 +354,8 @@ std::vector<uint16_t> moe_run(exl3_moe* h, const std::vector<uint16_t>& xv,
   const size_t wb = exl3_moe_workspace_bytes(h, rows);
   if (wb == 0) bail("MoE slot overflow");
   DeviceBuffer ws(wb);
-  lib_check(exl3_moe_forward(h, x.as<uint16_t>(), rows, s.as<uint32_t>(), b.as<uint16_t>(),
-                             y.as<uint16_t>(), ws.p, wb, nullptr));
+  lib_check(exl3_moe_forward(h, x.p, EXL3_F16, rows, s.as<uint32_t>(), b.p, EXL3_F16, y.p, ws.p,
+                             wb, nullptr));
   return y.read<uint16_t>(xv.size());
 }
 
@@ -601,8 +601,8 @@ std::string run(const Request& r) {
     expect_len(r.svh.size(), slots * width);
     if (slots == 0) return json_list(std::vector<uint16_t>(width, 0));  // an empty sum
     DeviceBuffer raw(r.state), sv(r.svh), sc(r.beta), y(width * 2);
-    lib_check(exl3_finish_and_reduce(raw.as<float>(), sv.as<uint16_t>(), sc.as<uint16_t>(), 1,
-                                     (int)slots, (int)width, y.as<uint16_t>(), nullptr));
+    lib_check(exl3_finish_and_reduce(raw.as<float>(), sv.as<uint16_t>(), sc.p, EXL3_F16, 1,
+                                     (int)slots, (int)width, y.p, nullptr));
     return json_list(y.read<uint16_t>(width));
   }
   if (r.op == "mlx-checkpoint-switch") {  // validate_moe_codec main.rs:230-238, run :701-725
@@ -613,10 +613,19 @@ std::string run(const Request& r) {
     CheckpointGuard c;
     lib_check(exl3_checkpoint_open(r.path.c_str(), &c.c));
     const bool lfm = std::strcmp(exl3_checkpoint_model_type(c.c), "lfm2_moe") == 0;
+    // Exl3SwitchGlu::forward's shape check (moe.rs:911-918) on the [1, len]
+    // row, against the bank's input width (first gate trellis: [in/16, ...]),
+    // before the bank is uploaded
+    exl3_tensor_info gate0;
+    const std::string gate_name = r.prefix + ".0." + (lfm ? "w1" : "gate_proj") + ".trellis";
+    if (exl3_checkpoint_tensor(c.c, gate_name.c_str(), &gate0) == EXL3_OK && gate0.ndim == 3 &&
+        r.x.size() != (uint64_t)gate0.shape[0] * 16)
+      bail("invalid SwitchGLU input/routes");
     MoeGuard g;
     lib_check(exl3_moe_load(c.c, r.prefix.c_str(), (int)r.key_heads, (int)r.selected.size(),
                             lfm ? "w1" : nullptr, lfm ? "w3" : nullptr, lfm ? "w2" : nullptr,
                             &g.h));
+    if (r.x.size() != (size_t)exl3_moe_in_features(g.h)) bail("invalid SwitchGLU input/routes");
     return json_list(moe_run(g.h, r.x, r.selected, r.beta, 1));
   }
   if (r.op == "mlx-checkpoint-group") {  // main.rs:677-700
@@ -630,26 +639,43 @@ std::string run(const Request& r) {
         for (auto* h : parts) exl3_linear_destroy(h);
       }
     } cleanup{parts};
-    // K and codebook of each projection, as Exl3Linear::from_checkpoint reads them
+    // K, codebook and input width of each projection, as
+    // Exl3Linear::from_checkpoint reads them (trellis [in/16][out/16][16k]),
+    // before anything is uploaded; a projection whose trellis is missing or
+    // malformed is left to exl3_linear_load's error
     std::vector<std::pair<int64_t, int>> kinds;
+    std::vector<int64_t> widths;
+    bool described = true;
+    for (const std::string& p : r.prefixes) {
+      exl3_tensor_info info;
+      if (exl3_checkpoint_tensor(c.c, (p + ".trellis").c_str(), &info) != EXL3_OK ||
+          info.ndim != 3) {
+        described = false;
+        break;
+      }
+      widths.push_back(info.shape[0] * 16);
+      const int64_t k16 = info.shape[2];
+      const int kcb = exl3_checkpoint_tensor(c.c, (p + ".mul1").c_str(), &info) == EXL3_OK ? 2
+                      : exl3_checkpoint_tensor(c.c, (p + ".mcg").c_str(), &info) == EXL3_OK ? 1
+                                                                                             : 0;
+      kinds.emplace_back(k16 / 16, kcb);
+    }
+    // Exl3Group::compatible (linear.rs:2303-2311)
+    bool grouped = described && r.prefixes.size() >= 2 && kinds[0].first != 7;
+    for (size_t i = 0; grouped && i < kinds.size(); ++i)
+      grouped = widths[i] == widths[0] && kinds[i] == kinds[0];
+    // the input row against every projection's width: Exl3Group::forward
+    // (linear.rs:2388-2391) or each Exl3Linear::forward (linear.rs:739-743)
+    if (described)
+      for (int64_t w : widths)
+        if ((uint64_t)w != r.x.size())
+          bail(grouped ? std::string("invalid grouped EXL3 input")
+                       : "invalid EXL3 linear input for " + std::to_string(w) + " inputs");
     for (const std::string& p : r.prefixes) {
       exl3_linear* h = nullptr;
       lib_check(exl3_linear_load(c.c, p.c_str(), &h));
       parts.push_back(h);
-      exl3_tensor_info info;
-      lib_check(exl3_checkpoint_tensor(c.c, (p + ".trellis").c_str(), &info));
-      const int kcb = exl3_checkpoint_tensor(c.c, (p + ".mul1").c_str(), &info) == EXL3_OK ? 2
-                      : exl3_checkpoint_tensor(c.c, (p + ".mcg").c_str(), &info) == EXL3_OK ? 1
-                                                                                             : 0;
-      exl3_checkpoint_tensor(c.c, (p + ".trellis").c_str(), &info);
-      kinds.emplace_back(info.shape[info.ndim - 1] / 16, kcb);
     }
-    const int32_t in = exl3_linear_in_features(parts[0]);
-    if ((uint64_t)in != r.x.size()) bail("invalid linear input rows");
-    // Exl3Group::compatible (linear.rs:2303-2311)
-    bool grouped = parts.size() >= 2 && kinds[0].first != 7;
-    for (size_t i = 0; i < parts.size(); ++i)
-      grouped = grouped && exl3_linear_in_features(parts[i]) == in && kinds[i] == kinds[0];
     DeviceBuffer x(r.x);
     std::vector<DeviceBuffer*> ys;
     struct YCleanup {

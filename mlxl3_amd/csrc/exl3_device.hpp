@@ -57,20 +57,25 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 
 enum : int { DT_F16 = 9, DT_F32 = 10, DT_BF16 = 12 };
 
-// Output conversion of the linear epilogue (linear.rs:992-997): the f16 value
-// is cast to the activation dtype, then the f16 bias is added in that dtype.
-__device__ __forceinline__ void store_out(void* p, int dt, size_t i, float v16, const uint16_t* bias,
-                                          int col) {
-  if (dt == DT_F16) {
-    float v = bias ? round_f16(v16 + h2f(bias[col])) : v16;
+// Output conversion of the linear epilogue (linear.rs:992-995): the f16 value
+// is cast to the activation dtype x_dt, then the f16 bias is added with MLX's
+// type promotion -- f16 + f16 in f16, f32 + f16 in f32, and bf16 + f16 in f32
+// (MLX promotes the pair to float32).  y_dt is that result dtype: x_dt without
+// a bias, f32 for bf16 activations with a bias (the host checks it).
+__device__ __forceinline__ float out_value(int x_dt, float v16, const uint16_t* bias, int col) {
+  float v = x_dt == DT_BF16 ? bf2f(f2bf(v16)) : v16;
+  if (bias) v = x_dt == DT_F16 ? round_f16(v + h2f(bias[col])) : v + h2f(bias[col]);
+  return v;
+}
+__device__ __forceinline__ void store_out(void* p, int y_dt, int x_dt, size_t i, float v16,
+                                          const uint16_t* bias, int col) {
+  const float v = out_value(x_dt, v16, bias, col);
+  if (y_dt == DT_F16)
     ((uint16_t*)p)[i] = f2h(v);
-  } else if (dt == DT_BF16) {
-    float v = bf2f(f2bf(v16));
-    if (bias) v = v + h2f(bias[col]);
+  else if (y_dt == DT_BF16)
     ((uint16_t*)p)[i] = f2bf(v);
-  } else {
-    ((float*)p)[i] = bias ? v16 + h2f(bias[col]) : v16;
-  }
+  else
+    ((float*)p)[i] = v;
 }
 
 // ---------------------------------------------------------------------------

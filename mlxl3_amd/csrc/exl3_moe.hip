@@ -90,8 +90,11 @@ bool moe_layout(const exl3_moe* h, int64_t rows, MoeLayout& L) {
     if (v == 16 || v == 64) L.block_rows = v;
   }
   // each expert's last block may be partial: sum ceil(c_e/b) <= slots/b + E
-  L.max_blocks = (int)(slots / L.block_rows + h->experts + 1);
-  L.ncounters = L.max_blocks * std::max(h->hidden, h->in) / 128;
+  const int64_t max_blocks = slots / L.block_rows + h->experts + 1;
+  const int64_t ncounters = max_blocks * (std::max(h->hidden, h->in) / 128);
+  if (ncounters > INT32_MAX) return false;
+  L.max_blocks = (int)max_blocks;
+  L.ncounters = (int)ncounters;
   L.splits_gu = moe_splits(h, slots, L.block_rows, h->in, h->hidden / 128);
   L.splits_down = moe_splits(h, slots, L.block_rows, h->hidden, h->in / 128);
   size_t off = kWorkspaceCounterBytes;  // the shared counter region stays untouched
@@ -108,7 +111,7 @@ bool moe_layout(const exl3_moe* h, int64_t rows, MoeLayout& L) {
   L.counters = take((size_t)L.ncounters * sizeof(uint32_t));
   L.xgu = take((size_t)2 * slots * h->in * sizeof(uint16_t));
   L.xd = take((size_t)slots * h->hidden * sizeof(uint16_t));
-  L.z = take((size_t)slots * h->in * sizeof(uint16_t));
+  L.z = take((size_t)slots * h->in * sizeof(float));  // f32 for f32 / bf16 scores
   const size_t pgu = L.splits_gu > 1 ? (size_t)L.splits_gu * 2 * slots * h->hidden : 0;
   const size_t pdn = L.splits_down > 1 ? (size_t)L.splits_down * slots * h->in : 0;
   L.partials = take(std::max(pgu, pdn) * sizeof(float));
@@ -163,6 +166,9 @@ int exl3_moe_create_gelu(const uint16_t* gu_trellis, const uint16_t* gu_suh,
   return EXL3_OK;
 }
 
+int32_t exl3_moe_in_features(const exl3_moe* h) { return h ? h->in : 0; }
+int32_t exl3_moe_hidden_features(const exl3_moe* h) { return h ? h->hidden : 0; }
+
 void exl3_moe_destroy(exl3_moe* h) {
   if (h && h->owned) (void)hipFree(h->owned);
   delete h;
@@ -196,9 +202,9 @@ int exl3_swiglu_down_input(const float* gate_up, const uint16_t* gu_svh, const u
   return check_launch("swiglu_down_input launch");
 }
 
-int exl3_finish_and_reduce(const float* raw, const uint16_t* svh, const uint16_t* scores,
-                           int64_t rows, int32_t top_k, int32_t width, uint16_t* y,
-                           void* stream) {
+int exl3_finish_and_reduce(const float* raw, const uint16_t* svh, const void* scores,
+                           int32_t scores_type, int64_t rows, int32_t top_k, int32_t width,
+                           void* y, void* stream) {
   // finish_and_reduce's checks (moe.rs:596-602)
   if (rows <= 0 || rows > INT32_MAX || top_k <= 0 || width <= 0 || width % 128)
     return fail(EXL3_EINVAL, "invalid expert reduction dimensions");
@@ -207,17 +213,23 @@ int exl3_finish_and_reduce(const float* raw, const uint16_t* svh, const uint16_t
   if (rows * (int64_t)top_k > INT32_MAX)
     return fail(EXL3_EINVAL, "invalid expert reduction dimensions");
   if (!raw || !svh || !scores || !y) return fail(EXL3_EINVAL, "null expert reduction buffer");
+  if (scores_type != EXL3_F16 && scores_type != EXL3_F32 && scores_type != EXL3_BF16)
+    return fail(EXL3_EINVAL, "unsupported score dtype code %d", scores_type);
   finish_and_reduce_kernel<<<dim3((unsigned)rows, width / 128), 64, 0, (hipStream_t)stream>>>(
-      raw, svh, scores, top_k, width, y);
+      raw, svh, scores, scores_type, top_k, width, y);
   return check_launch("finish_and_reduce launch");
 }
 
-int exl3_moe_forward(const exl3_moe* h, const uint16_t* x, int64_t rows,
-                     const uint32_t* selected, const uint16_t* scores, uint16_t* y,
+static bool valid_dtype(int dt) { return dt == EXL3_F16 || dt == EXL3_F32 || dt == EXL3_BF16; }
+
+int exl3_moe_forward(const exl3_moe* h, const void* x, int32_t x_type, int64_t rows,
+                     const uint32_t* selected, const void* scores, int32_t scores_type, void* y,
                      void* workspace, size_t workspace_bytes, void* stream) {
   if (!h) return fail(EXL3_EINVAL, "handle is null");
   if (rows < 1 || !x || !selected || !scores || !y)
     return fail(EXL3_EINVAL, "invalid SwitchGLU input/routes");
+  if (!valid_dtype(x_type) || !valid_dtype(scores_type))
+    return fail(EXL3_EINVAL, "unsupported dtype codes %d (x), %d (scores)", x_type, scores_type);
   MoeLayout L;
   if (!moe_layout(h, rows, L)) return fail(EXL3_EINVAL, "MoE slot overflow");
   if (!workspace || workspace_bytes < L.total)
@@ -251,7 +263,7 @@ int exl3_moe_forward(const exl3_moe* h, const uint16_t* x, int64_t rows,
 
   uint16_t* xgu = (uint16_t*)(ws + L.xgu);
   moe_gather_kernel<<<(unsigned)((2 * (int64_t)slots + 3) / 4), 256, 0, s>>>(
-      x, h->in, h->top_k, selected, pp.sorted_slot, pp.counts + 1, slots, h->gu_suh, xgu);
+      x, x_type, h->in, h->top_k, selected, pp.sorted_slot, pp.counts + 1, slots, h->gu_suh, xgu);
   if (int rc = check_launch("moe gather")) return rc;
 
   MoeMmParams q{};
@@ -288,12 +300,13 @@ int exl3_moe_forward(const exl3_moe* h, const uint16_t* x, int64_t rows,
   q.xa = q.xd;
   q.down_svh = h->down_svh;
   q.scores = scores;
-  q.z = (uint16_t*)(ws + L.z);
+  q.scores_dtype = scores_type;
+  q.z = ws + L.z;
   down<<<L.max_blocks * q.col_blocks * q.splits, 256, 0, s>>>(q);
   if (int rc = check_launch("moe down")) return rc;
 
   moe_reduce_kernel<<<dim3((unsigned)rows, (h->in + 255) / 256), 256, 0, s>>>(
-      q.z, selected, h->experts, h->top_k, h->in, y);
+      q.z, scores_type, selected, h->experts, h->top_k, h->in, y);
   return check_launch("moe reduce");
 }
 

@@ -18,8 +18,10 @@
 //               forward_gelu: staged Hadamards and GEGLU instead);
 //   4. down:    the same kernel with 4 waves over the down bank; the epilogue is
 //               finish_and_reduce's per-slot part (moe.rs:586-609): f16, staged
-//               Hadamard, *svh, *score, stored per slot;
-//   5. reduce:  y[row] = f16(sum over top_k in slot order, f32).
+//               Hadamard, *svh, *score (f16 scores: an f16 product; f32 or bf16
+//               scores: an f32 product, MLX's promotion), stored per slot;
+//   5. reduce:  y[row] = sum over top_k in slot order in f32, then f16 (f16
+//               scores) or kept f32 (f32 or bf16 scores).
 // Small inputs (decode: a handful of slots) split K over several workgroups
 // whose f32 partials meet in the last arriving one (agent-scope relaxed
 // atomics, as in the QMV), which adds them in split order.  Each row's
@@ -120,8 +122,9 @@ __global__ __launch_bounds__(1024) void moe_plan_kernel(MoePlanParams p) {
 // projection): the slot and expert lookups once, then the row's blocks with
 // eight blocks' loads in flight.  grid ceil(2 * slots / 4), 256 threads;
 // positions past the routed count idle.
-__global__ __launch_bounds__(256) void moe_gather_kernel(const uint16_t* __restrict__ x, int in,
-                                                         int top_k, const uint32_t* selected,
+__global__ __launch_bounds__(256) void moe_gather_kernel(const void* __restrict__ x, int x_dtype,
+                                                         int in, int top_k,
+                                                         const uint32_t* selected,
                                                          const int* sorted_slot,
                                                          const int* routed, int slots_pad,
                                                          const uint16_t* __restrict__ gu_suh,
@@ -131,7 +134,7 @@ __global__ __launch_bounds__(256) void moe_gather_kernel(const uint16_t* __restr
   if (pos >= *routed) return;  // uniform per wave
   const int slot = sorted_slot[pos];
   const uint16_t* suh = gu_suh + ((size_t)selected[slot] * 2 + proj) * in;
-  pair_prologue_row(x, DT_F16, (size_t)(slot / top_k) * in, suh, 0, in >> 7, threadIdx.x & 63,
+  pair_prologue_row(x, x_dtype, (size_t)(slot / top_k) * in, suh, 0, in >> 7, threadIdx.x & 63,
                     xgu + ((size_t)proj * slots_pad + pos) * in);
 }
 
@@ -158,9 +161,24 @@ struct MoeMmParams {
   int logical_hidden;       // GELU: outputs of columns >= logical_hidden are zero
   // down epilogue
   const uint16_t* down_svh; // [E][width]
-  const uint16_t* scores;   // [slots]
-  uint16_t* z;              // [slots][width]
+  const void* scores;       // [slots] of scores_dtype
+  int scores_dtype;         // f16: f16 products; f32 / bf16: f32 products
+  void* z;                  // [slots][width], f16 (f16 scores) or f32
 };
+
+// A routing score as f32 (f16, bf16 or f32 storage).
+__device__ __forceinline__ float load_score(const void* scores, int dt, size_t i) {
+  if (dt == DT_F32) return ((const float*)scores)[i];
+  const uint16_t b = ((const uint16_t*)scores)[i];
+  return dt == DT_BF16 ? bf2f(b) : h2f(b);
+}
+
+// One slot's weighted output value (finish_and_reduce, moe.rs:604-607): the
+// f16 value times its score -- rounded to f16 when the score is f16, an f32
+// product otherwise (MLX promotes f16 * f32 and f16 * bf16 to f32).
+__device__ __forceinline__ float weighted(float v16, float score, int scores_dtype) {
+  return scores_dtype == DT_F16 ? round_f16(v16 * score) : v16 * score;
+}
 
 // Epilogue of one routed row of a 128-column block: (g0, g1) and (u0, u1) are
 // the f32 sums of columns (lane, lane+64) of the first and last projection.
@@ -218,12 +236,17 @@ __device__ __forceinline__ void moe_finish_row(const MoeMmParams& p, int e, int 
     v0 = round_f16(v0 * kHadScale);
     v1 = round_f16(v1 * kHadScale);
     const uint16_t* sv = p.down_svh + (size_t)e * p.width + col0;
-    const float sc = h2f(p.scores[slot]);
-    v0 = round_f16(round_f16(v0 * h2f(sv[lane])) * sc);
-    v1 = round_f16(round_f16(v1 * h2f(sv[lane + 64])) * sc);
-    uint16_t* dst = p.z + (size_t)slot * p.width + col0;
-    dst[lane] = f2h(v0);
-    dst[lane + 64] = f2h(v1);
+    const float sc = load_score(p.scores, p.scores_dtype, slot);
+    v0 = weighted(round_f16(v0 * h2f(sv[lane])), sc, p.scores_dtype);
+    v1 = weighted(round_f16(v1 * h2f(sv[lane + 64])), sc, p.scores_dtype);
+    const size_t at = (size_t)slot * p.width + col0 + lane;
+    if (p.scores_dtype == DT_F16) {
+      ((uint16_t*)p.z)[at] = f2h(v0);
+      ((uint16_t*)p.z)[at + 64] = f2h(v1);
+    } else {
+      ((float*)p.z)[at] = v0;
+      ((float*)p.z)[at + 64] = v1;
+    }
   }
 }
 
@@ -458,43 +481,60 @@ __global__ __launch_bounds__(64) void swiglu_down_input_kernel(MoeMmParams p,
                        gate_up[off + p.width + lane], gate_up[off + p.width + lane + 64], lane);
 }
 
-// finish_and_reduce (moe.rs:586-609) as an op: y[row] = f16(sum_t f32(
-// f16(f16(H(f16(raw)) * svh) * score))) over slots row*top_k + t in t order,
-// H the staged Hadamard with f16(v * scale), svh one row per slot.  One wave
-// per (row, 128-column block); grid (rows, width / 128).
+// Stores one reduced output value: f16 for f16 scores, f32 otherwise (the
+// dtype MLX's promotion gives the weighted sum).
+__device__ __forceinline__ void store_reduced(void* y, int scores_dtype, size_t i, float v) {
+  if (scores_dtype == DT_F16)
+    ((uint16_t*)y)[i] = f2h(v);
+  else
+    ((float*)y)[i] = v;
+}
+
+// finish_and_reduce (moe.rs:586-609) as an op: y[row] = sum_t of
+// weighted(f16(H(f16(raw)) * svh), score) over slots row*top_k + t in t order
+// (f32 adds), rounded to f16 for f16 scores; H the staged Hadamard with
+// f16(v * scale), svh one row per slot.  One wave per (row, 128-column block);
+// grid (rows, width / 128).
 __global__ __launch_bounds__(64) void finish_and_reduce_kernel(const float* __restrict__ raw,
                                                                const uint16_t* __restrict__ svh,
-                                                               const uint16_t* __restrict__ scores,
-                                                               int top_k, int width,
-                                                               uint16_t* __restrict__ y) {
+                                                               const void* __restrict__ scores,
+                                                               int scores_dtype, int top_k,
+                                                               int width, void* __restrict__ y) {
   const int row = blockIdx.x, col = blockIdx.y * 128 + threadIdx.x, lane = threadIdx.x;
   float a0 = 0.f, a1 = 0.f;
   for (int t = 0; t < top_k; ++t) {
     const size_t slot = (size_t)row * top_k + t;
     float v0 = round_f16(raw[slot * width + col]), v1 = round_f16(raw[slot * width + col + 64]);
     h128_wave<true>(v0, v1, lane);
-    const float sc = h2f(scores[slot]);
-    a0 += round_f16(round_f16(round_f16(v0 * kHadScale) * h2f(svh[slot * width + col])) * sc);
-    a1 += round_f16(round_f16(round_f16(v1 * kHadScale) * h2f(svh[slot * width + col + 64])) * sc);
+    const float sc = load_score(scores, scores_dtype, slot);
+    a0 += weighted(round_f16(round_f16(v0 * kHadScale) * h2f(svh[slot * width + col])), sc,
+                   scores_dtype);
+    a1 += weighted(round_f16(round_f16(v1 * kHadScale) * h2f(svh[slot * width + col + 64])), sc,
+                   scores_dtype);
   }
-  y[(size_t)row * width + col] = f2h(a0);
-  y[(size_t)row * width + col + 64] = f2h(a1);
+  store_reduced(y, scores_dtype, (size_t)row * width + col, a0);
+  store_reduced(y, scores_dtype, (size_t)row * width + col + 64, a1);
 }
 
-// y[row][i] = f16(sum_t f32(z[row*top_k + t][i])) in t order; slots routed to
-// no valid expert contribute zero.  grid (rows, ceil(width/256)).
-__global__ __launch_bounds__(256) void moe_reduce_kernel(const uint16_t* __restrict__ z,
+// y[row][i] = sum_t z[row*top_k + t][i] in t order with f32 adds (z f16 for
+// f16 scores, f32 otherwise), stored as f16 or f32 the same way; slots routed
+// to no valid expert contribute zero.  grid (rows, ceil(width/256)).
+__global__ __launch_bounds__(256) void moe_reduce_kernel(const void* __restrict__ z,
+                                                         int scores_dtype,
                                                          const uint32_t* __restrict__ selected,
                                                          int experts, int top_k, int width,
-                                                         uint16_t* __restrict__ y) {
+                                                         void* __restrict__ y) {
   const int i = blockIdx.y * 256 + threadIdx.x, row = blockIdx.x;
   if (i >= width) return;
   float acc = 0.f;
   for (int t = 0; t < top_k; ++t) {
     const int slot = row * top_k + t;
-    if (selected[slot] < (uint32_t)experts) acc += h2f(z[(size_t)slot * width + i]);
+    if (selected[slot] < (uint32_t)experts) {
+      const size_t at = (size_t)slot * width + i;
+      acc += scores_dtype == DT_F16 ? h2f(((const uint16_t*)z)[at]) : ((const float*)z)[at];
+    }
   }
-  y[(size_t)row * width + i] = f2h(acc);
+  store_reduced(y, scores_dtype, (size_t)row * width + i, acc);
 }
 
 }  // namespace exl3

@@ -19,6 +19,7 @@ struct Member {
   void* y;                  // [M][out] of y_dtype
   int out;                  // columns
   int cblk0;                // first global column block
+  int y_dtype;              // x_dtype, or f32 for bf16 activations with a bias
 };
 
 // SwiGLU edge of a (gate, up) QMV group: members 0 and 1 have equal widths;
@@ -39,7 +40,7 @@ struct QmvParams {
   float* partials;     // [splits][M][total_out]
   uint32_t* counters;  // [total_out/128] (GLU: [out/128]), zero between calls
   int in, total_out, M, splits;
-  int x_dtype, y_dtype;
+  int x_dtype;
   Glu glu;
 };
 
@@ -48,7 +49,8 @@ struct QmmParams {
   int members;
   float* partials;     // [splits][M][total_out] f32 (splits > 1)
   uint32_t* counters;  // [mtiles * col_blocks], zero between calls (splits > 1)
-  int in, total_out, M, y_dtype;
+  int in, total_out, M;
+  int x_dtype;         // the activation dtype (the output's intermediate cast)
   int col_blocks;      // total_out / 128
   int mtiles;          // ceil(M / rows per workgroup)
   int splits;          // K-ranges per output tile (global split-K)

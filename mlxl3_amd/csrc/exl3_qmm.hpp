@@ -123,13 +123,17 @@ __device__ __forceinline__ void qmm_stage_row(const float (&v)[8], int lane, uin
   }
 }
 
-// 16-bit output bits of the linear epilogue's final cast (+ bias), as
-// store_out computes them.
-__device__ __forceinline__ uint32_t out16(float v16, float b, bool has_bias, int dt) {
-  if (dt == DT_F16) return f2h(has_bias ? round_f16(v16 + b) : v16);
-  float v = bf2f(f2bf(v16));
-  if (has_bias) v = v + b;
-  return f2bf(v);
+// Value of the linear epilogue's final cast (+ bias), as out_value computes
+// it: the cast to the activation dtype x_dt, then the bias added with MLX's
+// promotion (f16 + f16 in f16, f32 or bf16 + f16 in f32).
+__device__ __forceinline__ float out_cast(float v16, float b, bool has_bias, int x_dt) {
+  float v = x_dt == DT_BF16 ? bf2f(f2bf(v16)) : v16;
+  if (has_bias) v = x_dt == DT_F16 ? round_f16(v + b) : v + b;
+  return v;
+}
+// 16-bit output bits (f16 or bf16 result dtype).
+__device__ __forceinline__ uint32_t out16(float v, int y_dt) {
+  return y_dt == DT_F16 ? f2h(v) : f2bf(v);
 }
 
 // Finishing side: each lane holds 8 consecutive columns 8*(lane&15)+j of one
@@ -139,7 +143,7 @@ __device__ __forceinline__ uint32_t out16(float v16, float b, bool has_bias, int
 // one 16-byte store (two for f32).  sv/bv: svh and bias of the lane's columns.
 __device__ __forceinline__ void qmm_finish_chunk(const u32x4 raw, const float (&sv)[8],
                                                  const float (&bv)[8], int lane, bool live,
-                                                 const Member& mm, int y_dtype, size_t yoff) {
+                                                 const Member& mm, int x_dtype, size_t yoff) {
   float v[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -168,12 +172,14 @@ __device__ __forceinline__ void qmm_finish_chunk(const u32x4 raw, const float (&
   for (int j = 0; j < 8; ++j) v[j] = round_f16(round_f16(v[j] * kHadScale) * sv[j]);
   if (!live) return;
   const bool has_bias = mm.bias != nullptr;
-  if (y_dtype == DT_F32) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = out_cast(v[j], bv[j], has_bias, x_dtype);
+  if (mm.y_dtype == DT_F32) {
     float4v o0, o1;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      o0[j] = has_bias ? v[j] + bv[j] : v[j];
-      o1[j] = has_bias ? v[j + 4] + bv[j + 4] : v[j + 4];
+      o0[j] = v[j];
+      o1[j] = v[j + 4];
     }
     float4v* yp = (float4v*)((float*)mm.y + yoff);
     yp[0] = o0;
@@ -183,8 +189,7 @@ __device__ __forceinline__ void qmm_finish_chunk(const u32x4 raw, const float (&
   u32x4 o;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    o[i] = out16(v[2 * i], bv[2 * i], has_bias, y_dtype) |
-           (out16(v[2 * i + 1], bv[2 * i + 1], has_bias, y_dtype) << 16);
+    o[i] = out16(v[2 * i], mm.y_dtype) | (out16(v[2 * i + 1], mm.y_dtype) << 16);
   *(u32x4*)((uint16_t*)mm.y + yoff) = o;
 }
 
@@ -487,7 +492,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
       const int rl = wave * 8 * MB + 4 * i + (lane >> 4);
       const int row = mtile * 64 * MB + rl;
       const u32x4 raw = *(const u32x4*)(ys + rl * kYStride + 8 * chunk);
-      qmm_finish_chunk(raw, sv, bv, lane, row < p.M, mm, p.y_dtype,
+      qmm_finish_chunk(raw, sv, bv, lane, row < p.M, mm, p.x_dtype,
                        (size_t)row * mm.out + colb + 8 * chunk);
     }
   }

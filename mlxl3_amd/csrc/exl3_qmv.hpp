@@ -119,11 +119,11 @@ __device__ __forceinline__ void finish_vals128(float& v0, float& v1, int lane, i
 __device__ __forceinline__ void finish_row128(float v0, float v1, int lane, int col0,
                                               const uint16_t* __restrict__ svh,
                                               const uint16_t* __restrict__ bias, void* y,
-                                              int y_dtype, size_t row_off) {
+                                              int y_dtype, int x_dtype, size_t row_off) {
   finish_vals128(v0, v1, lane, col0, svh);
   int c0 = col0 + lane, c1 = col0 + lane + 64;
-  store_out(y, y_dtype, row_off + c0, v0, bias, c0);
-  store_out(y, y_dtype, row_off + c1, v1, bias, c1);
+  store_out(y, y_dtype, x_dtype, row_off + c0, v0, bias, c0);
+  store_out(y, y_dtype, x_dtype, row_off + c1, v1, bias, c1);
 }
 // f16 output value with the optional bias added in f16 (y + bias).
 __device__ __forceinline__ float with_bias_f16(float v16, const uint16_t* __restrict__ bias,
@@ -545,7 +545,8 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
     for (int m = wave; m < M; m += 4 * KW) {
       float v0, v1;
       sum_row(m, cblk * 128, v0, v1);
-      finish_row128(v0, v1, lane, colb_l, mm.svh, mm.bias, mm.y, p.y_dtype, (size_t)m * mm.out);
+      finish_row128(v0, v1, lane, colb_l, mm.svh, mm.bias, mm.y, mm.y_dtype, p.x_dtype,
+                    (size_t)m * mm.out);
     }
     return;
   }
@@ -584,8 +585,8 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
       for (int t = 0; t < kRows; ++t) {
         const int m = m0 + t * 4 * KW;
         if (m < M)
-          finish_row128(v0[t], v1[t], lane, colb_l, mm.svh, mm.bias, mm.y, p.y_dtype,
-                        (size_t)m * mm.out);
+          finish_row128(v0[t], v1[t], lane, colb_l, mm.svh, mm.bias, mm.y, mm.y_dtype,
+                        p.x_dtype, (size_t)m * mm.out);
       }
     }
     return;

@@ -111,11 +111,12 @@ def moe_layer(seed: int, base_id: int, in_features: int, hidden: int, experts: i
     return gu, gu_suh, gu_svh, down, down_suh, down_svh
 
 
-def moe_routes(seed: int, tensor_id: int, rows: int, experts: int, top_k: int):
+def moe_routes(seed: int, tensor_id: int, rows: int, experts: int, top_k: int,
+               dtype=np.float16):
     """Top-k routing from softmax(N(0,1) logits), probabilities renormalised over the top k.
 
     Returns (selected uint32 [rows, top_k] in descending-probability order,
-    scores float16 [rows, top_k]).
+    scores [rows, top_k] of `dtype`, float16 by default).
     """
     logits = normal(seed, tensor_id, rows * experts).reshape(rows, experts).astype(np.float32)
     p = np.exp(logits - logits.max(axis=1, keepdims=True))
@@ -123,7 +124,7 @@ def moe_routes(seed: int, tensor_id: int, rows: int, experts: int, top_k: int):
     order = np.argsort(-p, axis=1, kind="stable")[:, :top_k]
     top = np.take_along_axis(p, order, axis=1)
     top /= top.sum(axis=1, keepdims=True)
-    return order.astype(np.uint32), top.astype(np.float16)
+    return order.astype(np.uint32), top.astype(dtype)
 
 
 # ---------------------------------------------------------------------------

@@ -55,8 +55,10 @@ def lib():
         L.exl3o_swiglu_down_input.argtypes = [_f32p, _u16p, _u16p, _u32p, ctypes.c_int64,
                                               ctypes.c_int, ctypes.c_int, _u16p]
         L.exl3o_finish_and_reduce.restype = ctypes.c_int
-        L.exl3o_finish_and_reduce.argtypes = [_f32p, _u16p, _u16p, ctypes.c_int64, ctypes.c_int,
-                                              ctypes.c_int, _u16p]
+        L.exl3o_finish_and_reduce.argtypes = [_f32p, _u16p, _vp, ctypes.c_int, ctypes.c_int64,
+                                              ctypes.c_int, ctypes.c_int, _vp]
+        L.exl3o_result_dtype.restype = ctypes.c_int
+        L.exl3o_result_dtype.argtypes = [ctypes.c_int, ctypes.c_int]
         L.exl3o_geglu.restype = None
         L.exl3o_geglu.argtypes = [_u16p, _u16p, _u16p, ctypes.c_int64]
         L.exl3o_codeword.restype = ctypes.c_uint16
@@ -83,10 +85,11 @@ def lib():
         L.exl3o_prologue.restype = ctypes.c_int
         L.exl3o_prologue.argtypes = [_vp, ctypes.c_int, ctypes.c_int64, ctypes.c_int, _u16p, _u16p]
         L.exl3o_moe_forward.restype = ctypes.c_int
-        L.exl3o_moe_forward.argtypes = [_u16p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+        L.exl3o_moe_forward.argtypes = [_vp, ctypes.c_int, ctypes.c_int64, ctypes.c_int,
                                         ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                        _u16p, _u16p, _u16p, _u16p, _u16p, _u16p, _u32p, _u16p,
-                                        _u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+                                        ctypes.c_int, _u16p, _u16p, _u16p, _u16p, _u16p, _u16p,
+                                        _u32p, _vp, ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int]
         _lib = L
     return _lib
 
@@ -100,12 +103,26 @@ def _u16(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.uint16)
 
 
-def _dtype_code(a: np.ndarray) -> int:
+def _dtype_code(a: np.ndarray, dtype=None) -> int:
+    """Dtype code of an activation array: float16, float32, or (dtype="bf16")
+    bfloat16 bits held in a uint16 array (numpy has no bfloat16)."""
+    if dtype == "bf16":
+        if a.dtype != np.uint16:
+            raise ValueError("bf16 arrays are passed as their uint16 bits")
+        return DT_BF16
     if a.dtype == np.float16:
         return DT_F16
     if a.dtype == np.float32:
         return DT_F32
-    raise ValueError(f"oracle activations are float16 or float32, got {a.dtype}")
+    raise ValueError(f"oracle activations are float16, float32 or bf16 bits, got {a.dtype}")
+
+
+_NP_OF_CODE = {DT_F16: np.float16, DT_F32: np.float32, DT_BF16: np.uint16}
+
+
+def result_dtype(x_code: int, has_bias: bool) -> int:
+    """exl3o_result_dtype: the projection's output dtype code."""
+    return int(lib().exl3o_result_dtype(int(x_code), int(bool(has_bias))))
 
 
 def codeword(state: int, cb: int) -> int:
@@ -178,17 +195,21 @@ def prologue(x, suh) -> np.ndarray:
 
 
 def forward(x, trellis, suh, svh, k: int, cb: int, bias=None, mode: int = 1, threads: int = 0,
-            return_yhat: bool = False):
-    """EXL3 linear on the CPU.  mode 1: engine glue semantics; mode 0: ref/forward.py."""
+            return_yhat: bool = False, x_dtype=None):
+    """EXL3 linear on the CPU.  mode 1: engine glue semantics; mode 0: ref/forward.py.
+    x: float16, float32, or bf16 bits (uint16) with x_dtype="bf16".  The result
+    has the projection's output dtype (result_dtype): x's dtype, or float32 for
+    bf16 activations with a bias; bf16 results are returned as uint16 bits."""
     x = np.ascontiguousarray(x)
+    code = _dtype_code(x, x_dtype)
     n_in = int(x.shape[-1])
     rows = x.size // n_in
     tr = _u16(trellis)
     n_out = int(tr.shape[1]) * 16 if tr.ndim == 3 else int(len(svh))
-    y = np.empty((rows, n_out), x.dtype)
+    y = np.empty((rows, n_out), _NP_OF_CODE[result_dtype(code, bias is not None)])
     yhat = np.empty((rows, n_out), np.float32) if return_yhat else None
     b = None if bias is None else _u16(bias)
-    rc = lib().exl3o_forward(mode, x.ctypes.data, _dtype_code(x), rows, tr.ravel(), n_in, n_out,
+    rc = lib().exl3o_forward(mode, x.ctypes.data, code, rows, tr.ravel(), n_in, n_out,
                              k, cb, _u16(suh), _u16(svh), None if b is None else b.ctypes.data,
                              y.ctypes.data, None if yhat is None else yhat.ctypes.data, threads)
     if rc:
@@ -199,11 +220,16 @@ def forward(x, trellis, suh, svh, k: int, cb: int, bias=None, mode: int = 1, thr
 
 def moe_forward(x, selected, scores, gu_trellis, gu_suh, gu_svh, down_trellis, down_suh,
                 down_svh, k: int, cb: int, threads: int = 0, activation: str = "silu",
-                logical_hidden=None) -> np.ndarray:
+                logical_hidden=None, x_dtype=None, scores_dtype=None) -> np.ndarray:
     """Exl3SwitchGlu::forward (moe.rs:905-975) for activation "silu", and
     forward_gelu (moe.rs:1087-1153) for "gelu" with GEGLU outputs from column
-    logical_hidden on set to zero (None: the whole hidden width)."""
-    x = _u16(x)
+    logical_hidden on set to zero (None: the whole hidden width).  x and
+    scores: float16, float32, or bf16 bits (uint16) with x_dtype / scores_dtype
+    "bf16".  Returns float16 for f16 scores, float32 otherwise."""
+    x = np.ascontiguousarray(x)
+    xcode = _dtype_code(x, x_dtype)
+    sc = np.ascontiguousarray(scores)
+    scode = _dtype_code(sc, scores_dtype)
     rows, n_in = x.shape
     experts, hidden = gu_svh.shape[0], gu_svh.shape[-1]
     top_k = selected.shape[1]
@@ -211,16 +237,16 @@ def moe_forward(x, selected, scores, gu_trellis, gu_suh, gu_svh, down_trellis, d
         raise ValueError(f"unknown GLU activation {activation!r}")
     gelu = activation == "gelu"
     logical = hidden if logical_hidden is None else int(logical_hidden)
-    y = np.empty((rows, n_in), np.uint16)
-    rc = lib().exl3o_moe_forward(x.ravel(), rows, n_in, hidden, experts, top_k, k, cb,
+    y = np.empty((rows, n_in), np.float16 if scode == DT_F16 else np.float32)
+    rc = lib().exl3o_moe_forward(x.ctypes.data, xcode, rows, n_in, hidden, experts, top_k, k, cb,
                                  _u16(gu_trellis).ravel(), _u16(gu_suh).ravel(),
                                  _u16(gu_svh).ravel(), _u16(down_trellis).ravel(),
                                  _u16(down_suh).ravel(), _u16(down_svh).ravel(),
                                  np.ascontiguousarray(selected, np.uint32).ravel(),
-                                 _u16(scores).ravel(), y.ravel(), int(gelu), logical, threads)
+                                 sc.ctypes.data, scode, y.ctypes.data, int(gelu), logical, threads)
     if rc:
         raise ValueError(f"oracle MoE forward failed ({rc})")
-    return y.view(np.float16)
+    return y
 
 
 def swiglu(gate, up) -> np.ndarray:
@@ -247,19 +273,22 @@ def swiglu_down_input(gate_up, gu_svh, down_suh, selected) -> np.ndarray:
     return out.view(np.float16)
 
 
-def finish_and_reduce(raw, svh, scores) -> np.ndarray:
+def finish_and_reduce(raw, svh, scores, scores_dtype=None) -> np.ndarray:
     """finish_and_reduce (moe.rs:586-609): raw f32 [rows*top_k, width], svh f16
-    of the same shape, scores f16 [rows, top_k] -> f16 [rows, width]."""
+    of the same shape, scores [rows, top_k] (float16, float32, or bf16 bits with
+    scores_dtype="bf16") -> [rows, width], float16 for f16 scores, float32
+    otherwise."""
     raw = np.ascontiguousarray(raw, np.float32)
-    sc = np.asarray(scores)
+    sc = np.ascontiguousarray(scores)
+    code = _dtype_code(sc, scores_dtype)
     rows, top_k = sc.shape
     width = raw.shape[-1]
-    y = np.empty((rows, width), np.uint16)
-    rc = lib().exl3o_finish_and_reduce(raw.ravel(), _u16(svh).ravel(), _u16(sc).ravel(), rows,
-                                       top_k, width, y.ravel())
+    y = np.empty((rows, width), np.float16 if code == DT_F16 else np.float32)
+    rc = lib().exl3o_finish_and_reduce(raw.ravel(), _u16(svh).ravel(), sc.ctypes.data, code, rows,
+                                       top_k, width, y.ctypes.data)
     if rc:
         raise ValueError(f"oracle finish_and_reduce failed ({rc})")
-    return y.view(np.float16)
+    return y
 
 
 def geglu(gate, up) -> np.ndarray:

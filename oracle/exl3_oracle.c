@@ -269,6 +269,27 @@ static void store_y(void* y, int dt, int64_t i, float v) {
 
 static int valid_dtype(int dt) { return dt == DT_F16 || dt == DT_F32 || dt == DT_BF16; }
 
+int exl3o_result_dtype(int x_dtype, int has_bias) {
+    return has_bias && x_dtype == DT_BF16 ? DT_F32 : x_dtype;
+}
+
+/* finish_and_reduce's weighted value (moe.rs:604-607): f16 * f16 rounds to
+ * f16; f16 * f32 and f16 * bf16 are f32 products (MLX promotes to f32). */
+static float load_score(const void* scores, int dt, int64_t i) {
+    if (dt == DT_F32) return ((const float*)scores)[i];
+    if (dt == DT_BF16) return exl3o_bf16_to_f32(((const uint16_t*)scores)[i]);
+    return h2f(((const uint16_t*)scores)[i]);
+}
+static float weighted(float v16, float score, int scores_dtype) {
+    return scores_dtype == DT_F16 ? rh(v16 * score) : v16 * score;
+}
+static void store_reduced(void* y, int scores_dtype, int64_t i, float v) {
+    if (scores_dtype == DT_F16)
+        ((uint16_t*)y)[i] = f2h(v);
+    else
+        ((float*)y)[i] = v;
+}
+
 /* Engine prologue, linear.rs:847-865: x.astype(F16) * suh (f16 multiply),
  * Hadamard-128 with scale 1/sqrt(128) in MLX's f16 schedule. */
 int exl3o_prologue(const void* x, int x_dtype, int64_t rows, int in, const uint16_t* suh,
@@ -412,17 +433,15 @@ int exl3o_forward(int mode, const void* x, int x_dtype, int64_t rows, const uint
                 }
             }
         }
+        /* linear.rs:992-995: y.astype(x.dtype), then + bias (f16) under
+         * MLX's promotion: f16 + f16 in f16; f32 + f16 and bf16 + f16 in f32
+         * (the result of bf16 activations with a bias is f32). */
+        const int y_dtype = exl3o_result_dtype(x_dtype, bias != NULL);
         for (int n = 0; n < out; ++n) {
             float v = row[n];
-            if (x_dtype == DT_F16) {
-                if (bias) v = rh(v + h2f(bias[n]));
-            } else if (x_dtype == DT_BF16) {
-                v = exl3o_bf16_to_f32(exl3o_f32_to_bf16(v));
-                if (bias) v = v + h2f(bias[n]);
-            } else if (bias) {
-                v = v + h2f(bias[n]);
-            }
-            store_y(y, x_dtype, m * out + n, v);
+            if (x_dtype == DT_BF16) v = exl3o_bf16_to_f32(exl3o_f32_to_bf16(v));
+            if (bias) v = x_dtype == DT_F16 ? rh(v + h2f(bias[n])) : v + h2f(bias[n]);
+            store_y(y, y_dtype, m * out + n, v);
         }
     }
 done:
@@ -479,14 +498,14 @@ void exl3o_geglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_
     for (int64_t i = 0; i < n; ++i) out[i] = f2h(geglu1(h2f(gate[i]), h2f(up[i])));
 }
 
-int exl3o_moe_forward(const uint16_t* x, int64_t rows, int in, int hidden, int experts,
+int exl3o_moe_forward(const void* x, int x_dtype, int64_t rows, int in, int hidden, int experts,
                       int top_k, int k, int cb, const uint16_t* gu_trellis,
                       const uint16_t* gu_suh, const uint16_t* gu_svh,
                       const uint16_t* down_trellis, const uint16_t* down_suh,
-                      const uint16_t* down_svh, const uint32_t* selected,
-                      const uint16_t* scores, uint16_t* y, int gelu, int logical_hidden,
-                      int threads) {
+                      const uint16_t* down_svh, const uint32_t* selected, const void* scores,
+                      int scores_dtype, void* y, int gelu, int logical_hidden, int threads) {
     if (k < 1 || k > 8 || cb < 0 || cb > 2 || rows < 1 || top_k < 1 || experts < 1) return -1;
+    if (!valid_dtype(x_dtype) || !valid_dtype(scores_dtype)) return -1;
     if (in % 128 || hidden % 128 || in <= 0 || hidden <= 0) return -1;
     if (gelu && logical_hidden <= 0) return -1; /* >= hidden: nothing is zeroed */
     for (int64_t i = 0; i < rows * top_k; ++i)
@@ -521,7 +540,9 @@ int exl3o_moe_forward(const uint16_t* x, int64_t rows, int in, int hidden, int e
             uint32_t e = selected[r * top_k + t];
             for (int p = 0; p < 2; ++p) {
                 const uint16_t* su = gu_suh + ((size_t)e * 2 + p) * in;
-                for (int i = 0; i < in; ++i) xin[i] = rh(h2f(x[r * in + i]) * h2f(su[i]));
+                /* routed_inputs (moe.rs:205-206): half(half(x) * half(scale)) */
+                for (int i = 0; i < in; ++i)
+                    xin[i] = rh(rh(load_x(x, x_dtype, r * in + i)) * h2f(su[i]));
                 exl3o_h128_staged(xin, in);
                 expert_gemv(xin, gu_trellis, in, gu_tn, (int)((p * experts + e) * hidden / 16),
                             hidden, k, table, perm, p ? u : g);
@@ -570,10 +591,10 @@ int exl3o_moe_forward(const uint16_t* x, int64_t rows, int in, int hidden, int e
             for (int i = 0; i < in; ++i) d[i] = rh(d[i]);
             exl3o_h128_staged(d, in);
             const uint16_t* dsv = down_svh + (size_t)e * in;
-            float sc = h2f(scores[r * top_k + t]);
-            for (int i = 0; i < in; ++i) sum[i] += rh(rh(d[i] * h2f(dsv[i])) * sc);
+            const float sc = load_score(scores, scores_dtype, r * top_k + t);
+            for (int i = 0; i < in; ++i) sum[i] += weighted(rh(d[i] * h2f(dsv[i])), sc, scores_dtype);
         }
-        for (int i = 0; i < in; ++i) y[r * in + i] = f2h(sum[i]);
+        for (int i = 0; i < in; ++i) store_reduced(y, scores_dtype, r * in + i, sum[i]);
         free(xin), free(g), free(u), free(d), free(sum);
     }
     return err;
@@ -615,12 +636,13 @@ int exl3o_swiglu_down_input(const float* gate_up, const uint16_t* gu_svh,
     return 0;
 }
 
-/* finish_and_reduce (moe.rs:586-609): y[r] = f16(sum_t f32(f16(f16(H(f16(raw)))
- * * svh) * score)) over the top_k slots r*top_k + t, H the staged H128 with
- * f16(v * scale). */
-int exl3o_finish_and_reduce(const float* raw, const uint16_t* svh, const uint16_t* scores,
-                            int64_t rows, int top_k, int width, uint16_t* y) {
+/* finish_and_reduce (moe.rs:586-609): y[r] = sum_t weighted(f16(f16(H(f16(raw)))
+ * * svh), score) over the top_k slots r*top_k + t in f32 (f16 result for f16
+ * scores), H the staged H128 with f16(v * scale). */
+int exl3o_finish_and_reduce(const float* raw, const uint16_t* svh, const void* scores,
+                            int scores_dtype, int64_t rows, int top_k, int width, void* y) {
     if (rows < 1 || top_k < 1 || width <= 0 || width % 128) return -1;
+    if (!valid_dtype(scores_dtype)) return -1;
     float* v = (float*)malloc(sizeof(float) * (size_t)width);
     float* acc = (float*)malloc(sizeof(float) * (size_t)width);
     if (!v || !acc) {
@@ -633,11 +655,11 @@ int exl3o_finish_and_reduce(const float* raw, const uint16_t* svh, const uint16_
             const int64_t sl = r * top_k + t;
             for (int i = 0; i < width; ++i) v[i] = rh(raw[sl * width + i]);
             exl3o_h128_staged(v, width);
-            const float sc = h2f(scores[sl]);
+            const float sc = load_score(scores, scores_dtype, sl);
             for (int i = 0; i < width; ++i)
-                acc[i] += rh(rh(v[i] * h2f(svh[sl * width + i])) * sc);
+                acc[i] += weighted(rh(v[i] * h2f(svh[sl * width + i])), sc, scores_dtype);
         }
-        for (int i = 0; i < width; ++i) y[r * width + i] = f2h(acc[i]);
+        for (int i = 0; i < width; ++i) store_reduced(y, scores_dtype, r * width + i, acc[i]);
     }
     free(v), free(acc);
     return 0;

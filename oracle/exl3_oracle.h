@@ -51,9 +51,13 @@ void exl3o_h128_f32(float* v, int64_t count);
  * then f16(v * f32(1/sqrt(128))).  Values are returned as f32 holding f16. */
 void exl3o_h128_staged(float* v, int64_t count);
 
+/* Output dtype of a projection (linear.rs:992-995: y.astype(x.dtype) + the f16
+ * bias under MLX's promotion): x_dtype, except DT_BF16 with a bias -> f32. */
+int exl3o_result_dtype(int x_dtype, int has_bias);
+
 /* ---- forward of one EXL3 linear ----
- * x: rows*in values of x_dtype (9 f16, 10 f32, 12 bf16), y: rows*out of the
- * same dtype.  trellis [in/16][out/16][16k] u16; suh [in] f16; svh [out] f16;
+ * x: rows*in values of x_dtype (9 f16, 10 f32, 12 bf16), y: rows*out of
+ * exl3o_result_dtype(x_dtype, bias != NULL).  trellis [in/16][out/16][16k] u16; suh [in] f16; svh [out] f16;
  * bias [out] f16 or NULL.
  * mode 0: ponyexl3/ref/forward.py:14-49 (f32 H128 with suh/svh in f32,
  *         f16 roundings at xh, y and the output) evaluated with f64 sums.
@@ -75,19 +79,21 @@ int exl3o_prologue(const void* x, int x_dtype, int64_t rows, int in, const uint1
  * columns [e*H/16, (e+1)*H/16) and up columns [(E+e)*H/16, ...) (moe.rs:756-760).
  * down_trellis [H/16][E*in/16][16k], expert e at tile columns [e*in/16, ...).
  * gu_suh [E][2][in], gu_svh [E][2][H], down_suh [E][H], down_svh [E][in] f16.
- * selected [rows][top_k] u32, scores [rows][top_k] f16.  x, y: rows*in f16.
+ * selected [rows][top_k] u32, scores [rows][top_k] of scores_dtype, x rows*in of
+ * x_dtype (cast to f16 first, moe.rs:205-206).  y rows*in: f16 for f16 scores,
+ * f32 for f32 or bf16 scores (finish_and_reduce's promotion, moe.rs:602-608).
  * Each routed slot: gate = lin(x), up = lin(x) (f16 outputs), act =
- * f16(silu(gate) * up), down = lin(act) (f16), y = f16(sum_t f32(score*down)).
+ * f16(silu(gate) * up), down = lin(act) (f16), y = sum_t score*down (f16
+ * products and an f32 sum rounded to f16 for f16 scores; f32 otherwise).
  * gelu != 0: forward_gelu (moe.rs:1087-1153) -- gate/up and the down input
  * in the linear's engine glue (staged H128), act = geglu(gate, up) for
  * columns < logical_hidden and 0 beyond. */
-int exl3o_moe_forward(const uint16_t* x, int64_t rows, int in, int hidden, int experts,
+int exl3o_moe_forward(const void* x, int x_dtype, int64_t rows, int in, int hidden, int experts,
                       int top_k, int k, int cb, const uint16_t* gu_trellis,
                       const uint16_t* gu_suh, const uint16_t* gu_svh,
                       const uint16_t* down_trellis, const uint16_t* down_suh,
-                      const uint16_t* down_svh, const uint32_t* selected,
-                      const uint16_t* scores, uint16_t* y, int gelu, int logical_hidden,
-                      int threads);
+                      const uint16_t* down_svh, const uint32_t* selected, const void* scores,
+                      int scores_dtype, void* y, int gelu, int logical_hidden, int threads);
 
 /* glu_down_input with SiLU (moe.rs:435-583): gate_up f32 [slots*2][hidden]
  * (gate row 2s, up row 2s+1), gu_svh [E][2][hidden], down_suh [E][hidden],
@@ -97,9 +103,10 @@ int exl3o_swiglu_down_input(const float* gate_up, const uint16_t* gu_svh,
                             int hidden, int experts, uint16_t* xhat);
 
 /* finish_and_reduce (moe.rs:586-609): raw f32 [rows*top_k][width], svh f16
- * [rows*top_k][width], scores f16 [rows][top_k] -> y f16 [rows][width]. */
-int exl3o_finish_and_reduce(const float* raw, const uint16_t* svh, const uint16_t* scores,
-                            int64_t rows, int top_k, int width, uint16_t* y);
+ * [rows*top_k][width], scores [rows][top_k] of scores_dtype -> y [rows][width],
+ * f16 for f16 scores and f32 for f32 / bf16 scores. */
+int exl3o_finish_and_reduce(const float* raw, const uint16_t* svh, const void* scores,
+                            int scores_dtype, int64_t rows, int top_k, int width, void* y);
 
 /* ---- dense SwiGLU (Array::swiglu, native/ffi/mlx_bridge.cpp:745-749) ----
  * out[i] = (g * sigmoid(g)) * u for f16 g, u in f16 arithmetic: the compiled

@@ -99,6 +99,32 @@ def test_forward_rejects_before_launch():
         lib.exl3_linear_destroy(h)
 
 
+def test_output_dtype_follows_mlx_promotion():
+    """linear.rs:992-995: y.astype(x.dtype) + an f16 bias under MLX's promotion:
+    bf16 + f16 is f32, so a biased projection under bf16 activations returns
+    f32; without a bias the activation dtype comes back.  forward rejects any
+    other y_type before a launch."""
+    lib = mlxl3_amd.load_library()
+    plain = ctypes.c_void_p()
+    biased = ctypes.c_void_p()
+    assert lib.exl3_linear_create(FAKE, 256, 256, 4, 0, FAKE, FAKE, None, ctypes.byref(plain)) == 0
+    assert lib.exl3_linear_create(FAKE, 256, 256, 4, 0, FAKE, FAKE, FAKE, ctypes.byref(biased)) == 0
+    try:
+        for x_type in (9, 10, 12):
+            assert lib.exl3_linear_output_dtype(plain, x_type) == x_type
+        assert [lib.exl3_linear_output_dtype(biased, t) for t in (9, 10, 12)] == [9, 10, 10]
+        assert lib.exl3_linear_output_dtype(biased, 7) == -1
+        assert lib.exl3_linear_output_dtype(None, 9) == -1
+        for h, x_type, y_type in ((biased, 12, 12), (plain, 12, 10), (plain, 9, 10)):
+            assert lib.exl3_linear_forward(h, FAKE, x_type, 1, FAKE, y_type, FAKE, 1 << 20,
+                                           None) == -1
+            msg = lib.exl3_last_error().decode()
+            assert f"EXL3 output dtype {y_type} differs" in msg, msg
+    finally:
+        lib.exl3_linear_destroy(plain)
+        lib.exl3_linear_destroy(biased)
+
+
 def test_decode_rejects_bad_k_and_cb():
     lib = mlxl3_amd.load_library()
     assert lib.exl3_decode_tiles(FAKE, 1, 0, 0, None, FAKE, None) == -1
@@ -159,11 +185,18 @@ def test_moe_create_workspace_and_forward_rejects():
         assert 0 < one < many
         assert lib.exl3_moe_workspace_bytes(h, 0) == 0
         # rows < 1, null routes, short workspace: rejected before any launch
-        assert lib.exl3_moe_forward(h, FAKE, 0, FAKE, FAKE, FAKE, FAKE, one, None) == -1
-        assert lib.exl3_moe_forward(h, FAKE, 1, None, FAKE, FAKE, FAKE, one, None) == -1
+        assert lib.exl3_moe_forward(h, FAKE, 9, 0, FAKE, FAKE, 9, FAKE, FAKE, one, None) == -1
+        assert lib.exl3_moe_forward(h, FAKE, 9, 1, None, FAKE, 9, FAKE, FAKE, one, None) == -1
         assert "invalid SwitchGLU input/routes" in lib.exl3_last_error().decode()
-        assert lib.exl3_moe_forward(h, FAKE, 100, FAKE, FAKE, FAKE, FAKE, one, None) == -1
+        # activation and score dtypes: f16, bf16 or f32 only
+        assert lib.exl3_moe_forward(h, FAKE, 11, 1, FAKE, FAKE, 9, FAKE, FAKE, one, None) == -1
+        assert "unsupported dtype codes 11 (x), 9 (scores)" in lib.exl3_last_error().decode()
+        assert lib.exl3_moe_forward(h, FAKE, 12, 1, FAKE, FAKE, 3, FAKE, FAKE, one, None) == -1
+        assert "unsupported dtype codes 12 (x), 3 (scores)" in lib.exl3_last_error().decode()
+        assert lib.exl3_moe_forward(h, FAKE, 10, 100, FAKE, FAKE, 12, FAKE, FAKE, one, None) == -1
         assert "workspace too small" in lib.exl3_last_error().decode()
+        assert lib.exl3_moe_in_features(h) == 256 and lib.exl3_moe_hidden_features(h) == 256
+        assert lib.exl3_moe_in_features(None) == 0
     finally:
         lib.exl3_moe_destroy(h)
 
@@ -215,9 +248,11 @@ def test_standalone_ops_reject_before_launch():
     assert "invalid fused SwiGLU dimensions" in err()
     assert lib.exl3_swiglu_down_input(FAKE, None, FAKE, FAKE, 4, 128, 2, FAKE, None) == -1
     assert "invalid fused SwiGLU scales/routes" in err()
-    assert lib.exl3_finish_and_reduce(FAKE, FAKE, FAKE, 2, 2, 100, FAKE, None) == -1
+    assert lib.exl3_finish_and_reduce(FAKE, FAKE, FAKE, 9, 2, 2, 100, FAKE, None) == -1
     assert "invalid expert reduction dimensions" in err()
-    assert lib.exl3_finish_and_reduce(FAKE, FAKE, FAKE, 2, 0, 128, FAKE, None) == -1
+    assert lib.exl3_finish_and_reduce(FAKE, FAKE, FAKE, 9, 2, 0, 128, FAKE, None) == -1
+    assert lib.exl3_finish_and_reduce(FAKE, FAKE, FAKE, 11, 2, 2, 128, FAKE, None) == -1
+    assert "unsupported score dtype code 11" in err()
 
 
 def test_group_and_mlp_reject_before_launch():
@@ -254,3 +289,63 @@ def test_group_and_mlp_reject_before_launch():
     finally:
         for h in hs + [d_bad, g_k]:
             lib.exl3_linear_destroy(h)
+
+
+def _switch_args(experts=4, n_in=256, hidden=128, k=3, top_k=2, **over):
+    """CPU tensors of a valid SwitchGLU bank's shapes (moe.rs:851-879)."""
+    import torch
+
+    a = dict(
+        gu_trellis=torch.zeros(n_in // 16, experts * hidden // 8, 16 * k, dtype=torch.int16),
+        gu_suh=torch.zeros(experts, 2, n_in, dtype=torch.float16),
+        gu_svh=torch.zeros(experts, 2, hidden, dtype=torch.float16),
+        down_trellis=torch.zeros(hidden // 16, experts * n_in // 16, 16 * k, dtype=torch.int16),
+        down_suh=torch.zeros(experts, hidden, dtype=torch.float16),
+        down_svh=torch.zeros(experts, n_in, dtype=torch.float16),
+        top_k=top_k, k=k)
+    a.update(over)
+    return a
+
+
+@pytest.mark.parametrize(
+    "over,msg",
+    [
+        (dict(gu_suh="rank2"), "gate/up input scales must have rank 3"),
+        (dict(gu_svh="rank2"), "gate/up output scales must have rank 3"),
+        (dict(k=7), "invalid or overflowing SwitchGLU dimensions"),
+        (dict(top_k=5), "invalid or overflowing SwitchGLU dimensions"),
+        (dict(gu_suh=(4, 3, 256)), "invalid SwitchGLU dimensions"),
+        (dict(gu_svh=(3, 2, 128)), "invalid SwitchGLU dimensions"),
+        (dict(down_suh=(4, 256)), "SwitchGLU trellis/scales disagree"),
+        (dict(down_svh=(4, 128)), "SwitchGLU trellis/scales disagree"),
+        (dict(gu_trellis=(16, 64, 32)), "SwitchGLU trellis/scales disagree"),
+        (dict(down_trellis=(8, 64, 32)), "SwitchGLU trellis/scales disagree"),
+        (dict(k=2), "SwitchGLU trellis/scales disagree"),  # last dimension 16*k
+        (dict(down_trellis="int32"), "expert trellis must contain 16-bit integers"),
+    ],
+)
+def test_switch_glu_constructor_rejects_like_the_reference(over, msg):
+    """Exl3SwitchGlu::new_with_activation's checks (moe.rs:851-879) run in the
+    Python mirror before any tensor reaches the device or the C ABI."""
+    import torch
+
+    base = _switch_args()
+    args = dict(base)
+    for name, v in over.items():
+        if v == "rank2":
+            args[name] = base[name].reshape(base[name].shape[0], -1)
+        elif v == "int32":
+            args[name] = base[name].to(torch.int32)
+        elif isinstance(v, tuple):
+            args[name] = torch.zeros(v, dtype=base[name].dtype)
+        else:
+            args[name] = v
+    with pytest.raises(mlxl3_amd.Exl3Error) as e:
+        mlxl3_amd.Exl3SwitchGlu(**args)
+    assert msg in str(e.value), str(e.value)
+
+
+def test_switch_glu_constructor_accepts_valid_shapes_then_needs_a_device():
+    with pytest.raises(mlxl3_amd.Exl3Error) as e:
+        mlxl3_amd.Exl3SwitchGlu(**_switch_args())
+    assert "must be a device tensor" in str(e.value)

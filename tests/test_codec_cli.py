@@ -153,3 +153,43 @@ def test_prepare_view_rejections_of_the_reference_harness():
     for (_, msg), row in zip(cases, rows):
         assert msg in row.get("error", ""), (msg, row)
     assert rows[-1] == {"data": []}
+
+
+def _bank_checkpoint(tmp_path):
+    """A synthetic checkpoint (host files only) with a 2-expert 128->128 bank and
+    two projections of different input widths."""
+    from mlxl3_amd import synth
+
+    tensors = {}
+    for e in range(2):
+        for p, (i, o) in zip(("gate_proj", "up_proj", "down_proj"), ((128, 128), (128, 128), (128, 128))):
+            t, suh, svh, _ = synth.linear_layer(7, e * 16 + len(p), i, o, 2)
+            tensors.update(synth.exl3_tensors(f"m.experts.{e}.{p}", t, suh, svh))
+    for name, (i, o) in (("q", (256, 128)), ("k", (128, 128))):
+        t, suh, svh, _ = synth.linear_layer(9, len(name), i, o, 2)
+        tensors.update(synth.exl3_tensors(f"m.attn.{name}", t, suh, svh))
+    storage = {p: {"quant_format": "exl3"} for p in ("m.attn.q", "m.attn.k")}
+    return synth.write_checkpoint(tmp_path / "ckpt", [tensors], storage)
+
+
+def test_checkpoint_ops_check_input_widths_before_any_upload(tmp_path):
+    """Exl3SwitchGlu::forward rejects a row that is not the bank's input width
+    (moe.rs:911-918) and each projection's forward rejects a row that is not its
+    own width (linear.rs:739-743, Exl3Group::forward :2388-2391): the driver
+    answers with those errors before any device allocation, so a short x never
+    reaches a kernel."""
+    root = str(_bank_checkpoint(tmp_path))
+    rows = run([
+        {"op": "mlx-checkpoint-switch", "path": root, "prefix": "m.experts", "key_heads": 2,
+         "selected": [0], "beta": [15360], "x": [0] * 64},
+        {"op": "mlx-checkpoint-group", "path": root, "prefixes": ["m.attn.q", "m.attn.k"],
+         "x": [0] * 128},
+        {"op": "mlx-checkpoint-group", "path": root, "prefixes": ["m.attn.k", "m.attn.q"],
+         "x": [0] * 128},
+        {"op": "permutation"},
+    ])
+    assert rows[0] == {"error": "invalid SwitchGLU input/routes"}, rows[0]
+    # widths 256 and 128 cannot group: each projection checks its own width
+    assert rows[1] == {"error": "invalid EXL3 linear input for 256 inputs"}, rows[1]
+    assert rows[2] == {"error": "invalid EXL3 linear input for 256 inputs"}, rows[2]
+    assert "data" in rows[3]

@@ -1,12 +1,13 @@
 """Parity at the measurement plan's full shapes (the configurations bench.py
 times), against the CPU oracle.
 
-* C2 (QMM prefill): {4096->14336, 14336->4096} x K{3,5} x M{128, 2048}, 1 %
-  x20 outlier channels.  Rows of a QMM are independent of each other, so the
-  oracle is run on a handful of rows of the full-size call;
-* C5 (verify block, MCG): 5120->27648 and 27648->5120 at M = 4 and 16, K = 2
-  and 4, all rows vs the oracle (these go through the multi-row QMV with its
-  separate prologue launch);
+* C2 (QMM prefill): the whole sweep, {4096->14336, 14336->4096} x K{3,4,5} x
+  M{16, 128, 512, 2048}, 1 % x20 outlier channels (M = 16 runs the multi-row
+  QMV).  Rows of a QMM are independent of each other, so the oracle is run on
+  a handful of rows of the full-size call;
+* C5 (verify block, MCG): every distinct projection shape of the layer
+  (gate/up 5120->27648, down 27648->5120, q/o 5120->5120, k/v 5120->1024) at
+  M = 4, 8 and 16, K = 2 and 4, all rows vs the oracle (the multi-row QMV);
 * C3 (chained dense layers): two chained Llama-style layers
   (a=rms(x); q,k,v=W a; h=x+W_o rms(q); b=rms(h); u=swiglu(W_g b, W_u b);
   x'=h+W_d rms(u)) on the GPU against the same chain with the oracle's linears
@@ -60,8 +61,8 @@ def check(y, ref, label):
 
 
 @pytest.mark.parametrize("n_in, n_out", [(4096, 14336), (14336, 4096)])
-@pytest.mark.parametrize("k", [3, 5])
-@pytest.mark.parametrize("rows", [128, 2048])
+@pytest.mark.parametrize("k", [3, 4, 5])
+@pytest.mark.parametrize("rows", [16, 128, 512, 2048])
 def test_c2_qmm_full_shape(n_in, n_out, k, rows):
     torch = torch_mod()
     print(f"C2 {n_in}x{n_out} K={k} M={rows}", flush=True)
@@ -76,9 +77,9 @@ def test_c2_qmm_full_shape(n_in, n_out, k, rows):
     check(y[pick], ref, f"C2 {n_in}x{n_out} K{k} M{rows} rows{pick.tolist()}")
 
 
-@pytest.mark.parametrize("n_in, n_out", [(5120, 27648), (27648, 5120)])
+@pytest.mark.parametrize("n_in, n_out", [(5120, 27648), (27648, 5120), (5120, 5120), (5120, 1024)])
 @pytest.mark.parametrize("k", [2, 4])
-@pytest.mark.parametrize("rows", [4, 16])
+@pytest.mark.parametrize("rows", [4, 8, 16])
 def test_c5_verify_block_full_shape(n_in, n_out, k, rows):
     torch = torch_mod()
     print(f"C5 {n_in}x{n_out} K={k} M={rows}", flush=True)

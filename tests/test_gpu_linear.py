@@ -99,19 +99,69 @@ def test_qmv_rows_vs_oracle_and_batch_equals_serial(rows):
         assert np.array_equal(yr.view(np.uint16), y[r:r + 1].view(np.uint16)), r
 
 
+def bf16_bits(v):
+    """float32 -> bfloat16 bits, round to nearest even."""
+    b = np.asarray(v, np.float32).view(np.uint32).astype(np.uint64)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def ulp_of(v, bf16):
+    """Spacing of the output format at |v| (bf16: 7 fraction bits, f16 otherwise)."""
+    return float(np.spacing(np.float16(v))) * (8.0 if bf16 else 1.0)
+
+
+@pytest.mark.parametrize("rows", [1, 2, 17, 512])
 @pytest.mark.parametrize("dtype_name", ["bfloat16", "float32"])
-def test_qmv_dtypes_and_bias(dtype_name):
+@pytest.mark.parametrize("bias", [False, True])
+def test_activation_dtypes_and_bias_vs_oracle(rows, dtype_name, bias):
+    """bf16 / f32 activations through the QMV (rows 1, 2) and the QMM (17, 512):
+    the output dtype follows linear.rs:992-995 under MLX promotion (bf16 + f16
+    bias -> f32), values vs the oracle at rel-L2 <= 1e-3 and max-abs <= 2 ulp
+    at max|y| of the last format the value was rounded to (bf16 for bf16
+    activations, with or without the f32 bias add: a one-ulp f16 flip in the
+    inner result can move the bf16 cast by one bf16 ulp; f16 otherwise)."""
     torch = torch_mod()
     dtype = getattr(torch, dtype_name)
-    lin, (tr, suh, svh, b) = make_layer(3000, 256, 256, 3, 1, bias=True)
-    x = synth.activations(5, 0, 2, 256).astype(np.float32)
-    xt = torch.from_numpy(x).to(dtype)
-    y = run(lin, xt.float().numpy(), dtype).float().cpu().numpy()
-    xin = xt.float().numpy()
-    ref = oracle.forward(xin.astype(np.float32), tr, suh, svh, 3, 1, bias=b)
-    if dtype_name == "bfloat16":
-        ref = torch.from_numpy(ref).to(torch.bfloat16).float().numpy()
-    check(y, ref, 4e-3, 64, f"{dtype_name}+bias")
+    print(f"dtypes rows={rows} {dtype_name} bias={bias}", flush=True)
+    lin, (tr, suh, svh, b) = make_layer(3000 + rows, 512, 384, 3, 1, bias=bias)
+    x32 = synth.activations(5, rows, rows, 512).astype(np.float32) * np.float32(1.37)
+    xt = torch.from_numpy(x32).to(dtype)
+    y = lin.forward(xt.cuda())
+    torch.cuda.synchronize()
+    want_dtype = torch.float32 if (bias and dtype == torch.bfloat16) else dtype
+    assert y.dtype == want_dtype, (y.dtype, want_dtype)
+    if dtype == torch.bfloat16:
+        xb = xt.view(torch.int16).numpy().view(np.uint16)
+        ref = oracle.forward(xb, tr, suh, svh, 3, 1, bias=b, x_dtype="bf16")
+    else:
+        ref = oracle.forward(x32, tr, suh, svh, 3, 1, bias=b)
+    if ref.dtype == np.uint16:  # bf16 bits
+        ref = (ref.astype(np.uint32) << 16).view(np.float32)
+    got = y.float().cpu().numpy()
+    bf16_out = dtype == torch.bfloat16  # the result passed through a bf16 cast
+    rel = np.linalg.norm(got.astype(np.float64) - ref) / np.linalg.norm(ref.astype(np.float64))
+    ulps = np.abs(got.astype(np.float64) - ref).max() / ulp_of(np.abs(ref).max(), bf16_out)
+    exact = float(np.mean(got == ref))
+    print(f"  rel_l2={rel:.3e} max_abs={ulps:.2f} ulp exact={exact:.4f}", flush=True)
+    assert rel <= 1e-3 and ulps <= 2, (rel, ulps)
+
+
+def test_bf16_bias_result_is_the_f32_sum_of_the_bf16_cast():
+    """The GPU's f32 result of bf16 activations with a bias equals, bit for bit,
+    float32(its own bias-free bf16 output) + float32(bias): the cast happens
+    before the promoted add (linear.rs:993-995), in both kernel families."""
+    torch = torch_mod()
+    import mlxl3_amd
+
+    lin_b, (tr, suh, svh, b) = make_layer(3100, 512, 384, 4, 0, bias=True)
+    lin_n = mlxl3_amd.Exl3Linear(lin_b.trellis, lin_b.suh, lin_b.svh, None, 4, 0)
+    for rows in (3, 40):
+        x = torch.from_numpy(synth.activations(6, rows, rows, 512)).to(torch.bfloat16).cuda()
+        yb, yn = lin_b.forward(x), lin_n.forward(x)
+        torch.cuda.synchronize()
+        assert yb.dtype == torch.float32 and yn.dtype == torch.bfloat16
+        want = yn.float() + torch.from_numpy(b.astype(np.float32)).cuda()
+        assert torch.equal(yb, want), rows
 
 
 @pytest.mark.parametrize("rows", [17, 64, 130, 512])

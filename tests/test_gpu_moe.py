@@ -144,6 +144,69 @@ def test_moe_c4_full_shape():
     check(y[pick], ref, "moe C4")
 
 
+def _bf16_bits(v):
+    b = np.asarray(v, np.float32).view(np.uint32).astype(np.uint64)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("rows,block_rows", [(3, "16"), (40, "64")])
+@pytest.mark.parametrize("x_name,scores_name", [("bfloat16", "float16"), ("float32", "float32"),
+                                                ("float16", "bfloat16"), ("bfloat16", "float32")])
+def test_moe_activation_and_score_dtypes(rows, block_rows, x_name, scores_name, monkeypatch):
+    """x in f16/bf16/f32 is read as half(x) (moe.rs:205-206); scores keep their
+    dtype and promote the weighted sum (finish_and_reduce, moe.rs:602-608):
+    f16 scores -> f16 result, f32 or bf16 scores -> f32 result.  Values vs the
+    oracle at the MoE tolerance, and the result dtype exactly."""
+    torch = torch_mod()
+    monkeypatch.setenv("EXL3_MOE_BLOCK_ROWS", block_rows)
+    print(f"moe dtypes x={x_name} scores={scores_name} rows={rows}", flush=True)
+    layer = synth.moe_layer(61, 500, 256, 256, 6, 3)
+    x32 = synth.normal(61, 510, rows * 256).reshape(rows, 256).astype(np.float32) * np.float32(1.3)
+    sel, sc32 = synth.moe_routes(61, 520, rows, 6, 2, dtype=np.float32)
+    xt = torch.from_numpy(x32).to(getattr(torch, x_name))
+    st = torch.from_numpy(sc32).to(getattr(torch, scores_name))
+    moe = make_moe(layer, 2, 3, 0)
+    y = moe.forward(xt.cuda(), dev(sel), st.cuda())
+    torch.cuda.synchronize()
+    want = torch.float16 if scores_name == "float16" else torch.float32
+    assert y.dtype == want
+    if x_name == "bfloat16":
+        xo, xd = xt.view(torch.int16).numpy().view(np.uint16), "bf16"
+    else:
+        xo, xd = xt.numpy(), None
+    if scores_name == "bfloat16":
+        so, sd = st.view(torch.int16).numpy().view(np.uint16), "bf16"
+    else:
+        so, sd = st.numpy(), None
+    ref = oracle.moe_forward(xo, sel, so, *layer, 3, 0, x_dtype=xd, scores_dtype=sd)
+    assert ref.dtype == (np.float16 if want == torch.float16 else np.float32)
+    check(y.cpu().numpy(), ref, f"moe x={x_name} scores={scores_name}")
+
+
+def test_finish_and_reduce_op_score_dtypes():
+    """The finish_and_reduce op with f32 and bf16 scores: f32 products and sum,
+    f32 result, bit-exact vs the oracle (one staged Hadamard per slot, the same
+    f32 operations in the same order)."""
+    import mlxl3_amd
+
+    torch = torch_mod()
+    rng = np.random.default_rng(11)
+    rows, top_k, width = 5, 3, 384
+    raw = rng.normal(0, 60, (rows * top_k, width)).astype(np.float32)
+    svh = rng.uniform(0.5, 1.5, (rows * top_k, width)).astype(np.float16)
+    sc = rng.uniform(0, 1, (rows, top_k)).astype(np.float32)
+    for name in ("float32", "bfloat16"):
+        st = torch.from_numpy(sc).to(getattr(torch, name))
+        y = mlxl3_amd.finish_and_reduce(torch.from_numpy(raw).cuda(), torch.from_numpy(svh).cuda(),
+                                        st.cuda())
+        torch.cuda.synchronize()
+        assert y.dtype == torch.float32
+        so = st.view(torch.int16).numpy().view(np.uint16) if name == "bfloat16" else sc
+        want = oracle.finish_and_reduce(raw, svh, so, scores_dtype="bf16" if name == "bfloat16"
+                                        else None)
+        np.testing.assert_array_equal(y.cpu().numpy(), want)
+
+
 # ---- GELU banks (from_gemma_checkpoint, forward_gelu) ----
 
 

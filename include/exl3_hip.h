@@ -103,6 +103,22 @@ int exl3_linear_forward(const exl3_linear* handle, const void* x, int32_t x_type
                         void* y, int32_t y_type, void* workspace, size_t workspace_bytes,
                         void* stream);
 
+/* Allocation-free exl3_linear_forward (no counterpart in the reference: for
+ * callers that cannot allocate -- code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The same kernels and results as
+ * exl3_linear_forward, with its workspace taken from a fixed device array of
+ * exl3_linear_noalloc_max_bytes() bytes that the library holds on every GPU
+ * it runs on until the process ends; no hipMalloc, hipFree or allocating
+ * library routine is called.  Calls whose workspace
+ * (exl3_linear_workspace_bytes) exceeds that size fail with
+ * EXL3_EUNSUPPORTED before any launch.  All calls on one GPU share the array:
+ * calls that overlap on one GPU (several streams or threads) race and must be
+ * serialised by the caller.  The first call on a device clears the array's
+ * counters with a kernel on `stream`. */
+size_t exl3_linear_noalloc_max_bytes(void);
+int exl3_linear_forward_noalloc(const exl3_linear* handle, const void* x, int32_t x_type,
+                                int64_t rows, void* y, int32_t y_type, void* stream);
+
 /* Exl3Group::new/forward, linear.rs:2285-2382: up to 8 projections with the
  * same input width, K and codebook applied to one x (q/k/v, gate/up); ys[i]
  * receives parts[i]'s output in exl3_linear_output_dtype(parts[i], x_type)

@@ -80,6 +80,8 @@ _SIGNATURES = {
     "exl3_workspace_init": (_i32, [_vp, _sz, _vp]),
     "exl3_linear_output_dtype": (_i32, [_vp, _i32]),
     "exl3_linear_forward": (_i32, [_vp, _vp, _i32, _i64, _vp, _i32, _vp, _sz, _vp]),
+    "exl3_linear_noalloc_max_bytes": (_sz, []),
+    "exl3_linear_forward_noalloc": (_i32, [_vp, _vp, _i32, _i64, _vp, _i32, _vp]),
     "exl3_group_workspace_bytes": (_sz, [_vp, _i32, _i64]),
     "exl3_group_forward": (_i32, [_vp, _i32, _vp, _i32, _i64, _vp, _vp, _sz, _vp]),
     "exl3_swiglu": (_i32, [_vp, _vp, _vp, _i64, _vp]),

@@ -8,12 +8,53 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 
 #include "../../include/exl3_hip.h"
 #include "exl3_launch.hpp"
 
 using namespace exl3;
+
+// ---------------------------------------------------------------------------
+// allocation-free workspace (exl3_linear_forward_noalloc)
+// ---------------------------------------------------------------------------
+// A file-scope device array that stands in for the caller's workspace: its
+// first kWorkspaceCounterBytes are the split-K counters (cleared once per
+// device, then left at zero by every call), the rest the per-call scratch.
+// Every GPU holds its own copy from module load to process exit.  In host code
+// the array's name is not a device address: the address comes from
+// hipGetSymbolAddress, once per device, and only that pointer is used.
+static constexpr size_t kNoAllocBytes = kWorkspaceCounterBytes + ((size_t)32 << 20);
+static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+
+static constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mutex;
+static void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device
+
+// The scratch address on the current device; on first use the counter region
+// is cleared on `stream` (a fill kernel, so the call may be captured).
+static int noalloc_scratch(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return fail(EXL3_EDEVICE, "no usable HIP device for the allocation-free workspace");
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      (void)hipGetLastError();
+      return fail(EXL3_EDEVICE, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+    }
+    launch_fill_zero((uint32_t*)ptr, kWorkspaceCounterBytes / 4, stream);
+    if (int rc = check_launch("allocation-free workspace init")) return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return EXL3_OK;
+}
 
 // ---------------------------------------------------------------------------
 // errors
@@ -514,6 +555,26 @@ int exl3_linear_forward(const exl3_linear* h, const void* x, int32_t x_type, int
   Group g;
   if (int rc = make_group(&h, 1, g)) return rc;
   return group_forward(g, x, x_type, rows, &y, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+size_t exl3_linear_noalloc_max_bytes(void) { return kNoAllocBytes; }
+
+int exl3_linear_forward_noalloc(const exl3_linear* h, const void* x, int32_t x_type, int64_t rows,
+                                void* y, int32_t y_type, void* stream) {
+  if (!h) return fail(EXL3_EINVAL, "null EXL3 linear handle");
+  if (!valid_dtype(x_type)) return fail(EXL3_EINVAL, "unsupported activation dtype code %d", x_type);
+  Group g;
+  if (int rc = make_group(&h, 1, g)) return rc;
+  if (int rc = check_rows(g, rows)) return rc;
+  const size_t need = kWorkspaceCounterBytes + group_scratch_bytes(g, rows);
+  if (need > kNoAllocBytes)
+    return fail(EXL3_EUNSUPPORTED,
+                "allocation-free EXL3 forward of %lld rows needs %zu bytes of workspace, more "
+                "than its fixed %zu; use exl3_linear_forward with a caller workspace",
+                (long long)rows, need, kNoAllocBytes);
+  void* ws = nullptr;
+  if (int rc = noalloc_scratch((hipStream_t)stream, &ws)) return rc;
+  return exl3_linear_forward(h, x, x_type, rows, y, y_type, ws, kNoAllocBytes, stream);
 }
 
 int exl3_group_forward(const exl3_linear* const* parts, int32_t count, const void* x,

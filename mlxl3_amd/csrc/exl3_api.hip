@@ -240,63 +240,8 @@ static bool qmv_separate_prologue(const Group& g, int64_t rows, int splits) {
   return rows * blocks >= 64;
 }
 
-// Balanced QMV (exl3_qmvb.hpp) schedule of one projection: G workgroups of
-// kQmvbParts wave groups, the V = (out/128) * (in/64) block-steps cut into
-// equal ranges; at most 256 workgroups (one per CU), at least 4 block-steps
-// per wave group, ranges no longer than in/64 (so a range spans at most two
-// column blocks; wider shapes keep the split-K kernel).  `slots` = the most
-// wave groups any column block receives sums from.  The schedule depends on
-// the shape only (never on the row count), so rows of a batch equal the same
-// rows alone.  EXL3_QMVB_WGS overrides G (tuning).
-struct QmvbShape {
-  int wgs, slots;
-  bool ok;
-};
-
-static QmvbShape qmvb_shape(int in, int out) {
-  const int NQ = in / 64, NB = out / 128;
-  const int64_t V = (int64_t)NB * NQ;
-  int64_t G = std::min<int64_t>(256, std::max<int64_t>(1, V / (kQmvbParts * 4)));
-  if (const char* env = getenv("EXL3_QMVB_WGS")) {
-    const int v = atoi(env);
-    if (v >= 1 && (int64_t)v * kQmvbParts <= V) G = v;
-  }
-  const int64_t VW = G * kQmvbParts;
-  // ranges no longer than NQ; trellis byte offsets in 32 bits
-  if ((V + VW - 1) / VW > NQ || (int64_t)in * out / 8 * 8 >= ((int64_t)1 << 32))
-    return QmvbShape{0, 0, false};
-  int slots = 1;
-  for (int b = 0; b < NB; ++b)
-    slots = std::max(slots, qmvb_group_of((int64_t)b * NQ + NQ - 1, V, VW) -
-                                qmvb_group_of((int64_t)b * NQ, V, VW) + 1);
-  return QmvbShape{(int)G, slots, true};
-}
-
-// The balanced QMV serves launches of one projection (no SwiGLU edge) unless
-// EXL3_QMV_LEGACY selects the split-K kernel (A/B comparisons); groups keep
-// the split-K kernel, whose member table covers several trellises.
-static bool qmv_balanced(const Group& g, bool glu) {
-  static const bool legacy = getenv("EXL3_QMV_LEGACY") != nullptr;
-  return !legacy && g.count == 1 && !glu && qmvb_shape(g.in, g.total_out).ok;
-}
-
-// The balanced QMV computes xhat in each workgroup (LDS at absolute input
-// positions) for one or two rows whose xhat fits in 64 KB; otherwise one
-// separate prologue launch writes it to the workspace.
-static bool qmvb_fused(const Group& g, int64_t rows) {
-  const QmvbShape sh = qmvb_shape(g.in, g.total_out);
-  const int64_t steps_wg = ((int64_t)(g.total_out / 128) * (g.in / 64) + sh.wgs - 1) / sh.wgs;
-  return rows <= 2 && (size_t)rows * steps_wg * 64 * sizeof(uint16_t) <= (64u << 10);
-}
-
 // Scratch bytes (after the counter region) of one group launch.
 static size_t group_scratch_bytes(const Group& g, int64_t rows) {
-  if (rows <= kQmvMaxRows && qmv_balanced(g, false)) {
-    const QmvbShape sh = qmvb_shape(g.in, g.total_out);
-    const size_t xhat =
-        qmvb_fused(g, rows) ? 0 : g.count * align_up(sizeof(uint16_t) * (size_t)rows * g.in);
-    return xhat + align_up(sizeof(float) * (size_t)(g.total_out / 128) * sh.slots * rows * 128);
-  }
   if (rows <= kQmvMaxRows) {
     int splits, kw;
     group_qmv_shape(g, &splits, &kw);
@@ -331,63 +276,10 @@ static Member member_of(const exl3_linear* h, void* y, int cblk0, int x_type) {
   return m;
 }
 
-// One balanced QMV launch (rows <= 16) of one projection, after a prologue
-// launch unless the prologue is fused.
-static int run_group_qmvb(const Group& g, const void* x, int x_type, int64_t rows,
-                          void* const* ys, uint32_t* counters, char* scratch,
-                          hipStream_t stream) {
-  QmvParams p{};
-  int cblk0 = 0;
-  for (int i = 0; i < g.count; ++i) {
-    p.mem[i] = member_of(g.parts[i], ys[i], cblk0, x_type);
-    cblk0 += g.parts[i]->out / 128;
-  }
-  const bool fused = qmvb_fused(g, rows);
-  if (!fused) {
-    const size_t xbytes = align_up(sizeof(uint16_t) * (size_t)rows * g.in);
-    PrologueParams pp{};
-    pp.x = x;
-    pp.x_dtype = x_type;
-    pp.in = g.in;
-    pp.rows = (int)rows;
-    for (int i = 0; i < g.count; ++i) {
-      pp.suh[i] = g.parts[i]->suh;
-      pp.xhat[i] = (uint16_t*)(scratch + i * xbytes);
-      p.mem[i].xhat = pp.xhat[i];
-    }
-    launch_prologue(pp, g.count, stream);
-    if (int rc = check_launch("EXL3 prologue launch")) return rc;
-    scratch += g.count * xbytes;
-  }
-  const QmvbShape sh = qmvb_shape(g.in, g.total_out);
-  p.members = g.count;
-  p.x = x;
-  p.partials = (float*)scratch;
-  p.counters = counters;
-  p.in = g.in;
-  p.total_out = g.total_out;
-  p.M = (int)rows;
-  p.splits = 1;
-  p.slots = sh.slots;
-  p.x_dtype = x_type;
-  // LDS: the fused prologue's xhat rows, and at least 80 KB + 256 so that no
-  // CU holds two workgroups of a launch of up to 256 workgroups
-  // (local steps of a workgroup: at most ceil(V / G) 64-row steps)
-  const int64_t steps_wg = ((int64_t)(g.total_out / 128) * (g.in / 64) + sh.wgs - 1) / sh.wgs;
-  size_t lds = fused ? (size_t)rows * steps_wg * 64 * sizeof(uint16_t) : 0;
-  if (sh.wgs > 64) lds = std::max<size_t>(lds, (80u << 10) + 256);
-  const bool single = rows == 1 && fused;
-  const int variant = single ? 0 : fused ? 1 : 2;
-  kQmvb[variant][g.k - 1][g.cb](p, dim3(sh.wgs), lds, stream);
-  return check_launch("EXL3 QMV launch");
-}
-
 // One QMV launch (rows <= 16) over the group; `glu` for a (gate, up) pair.
 static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows,
                          void* const* ys, uint32_t* counters, char* scratch, const Glu& glu,
                          hipStream_t stream) {
-  if (qmv_balanced(g, glu.on))
-    return run_group_qmvb(g, x, x_type, rows, ys, counters, scratch, stream);
   QmvParams p{};
   int cblk0 = 0;
   for (int i = 0; i < g.count; ++i) {

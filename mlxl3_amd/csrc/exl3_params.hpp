@@ -1,7 +1,6 @@
 // Kernel parameter blocks (plain structs passed by value to the kernels).
 #pragma once
 
-#include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace exl3 {
@@ -42,7 +41,6 @@ struct QmvParams {
   uint32_t* counters;  // [total_out/128] (GLU: [out/128]), zero between calls
   int in, total_out, M, splits;
   int x_dtype;
-  int slots;           // balanced QMV: contributor slots per column block
   Glu glu;
 };
 
@@ -65,13 +63,6 @@ struct PrologueParams {
   uint16_t* xhat[kMaxMembers];  // [rows][in] f16 each
   size_t suh_stride;            // scale elements per row: 0 (one scale per column) or in
 };
-
-// Balanced QMV schedule: the wave group holding block-step v when V
-// block-steps are cut into VW contiguous ranges [floor(r V / VW),
-// floor((r+1) V / VW)) (host and device use the same formula).
-__host__ __device__ __forceinline__ int qmvb_group_of(int64_t v, int64_t V, int64_t VW) {
-  return (int)(((v + 1) * VW + V - 1) / V) - 1;
-}
 
 // The member owning global column block `cblk`, chosen with compile-time
 // indices only (a dynamically indexed parameter array would be copied to

@@ -1,7 +1,6 @@
 // Instantiations of the multi-row QMV and the decode hook over K x codebook.
 #include "exl3_launch.hpp"
 #include "exl3_qmv.hpp"
-#include "exl3_qmvb.hpp"
 
 namespace exl3 {
 
@@ -10,11 +9,6 @@ namespace exl3 {
   template __global__ void qmv_kernel<K, CB, 1, true>(QmvParams);  \
   template __global__ void qmv_kernel<K, CB, 2, true>(QmvParams);  \
   template __global__ void qmv_kernel<K, CB, 4, true>(QmvParams);
-#define EXL3_QMVB_INST(K, CB)                                                       \
-  template __global__ void qmvb_kernel<K, CB, kQmvbParts, false, false>(QmvParams); \
-  template __global__ void qmvb_kernel<K, CB, kQmvbParts, false, true>(QmvParams);  \
-  template __global__ void qmvb_kernel<K, CB, kQmvbParts, true, true>(QmvParams);
-EXL3_INSTANTIATE(EXL3_QMVB_INST)
 #define EXL3_DEC_INST(K, CB)                                                             \
   template __global__ void decode_tiles_kernel<K, CB>(const uint32_t*, int64_t, uint16_t*, \
                                                       uint16_t*);
@@ -98,34 +92,6 @@ template <int K, int CB>
 static void run_qmv4(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) {
   hipLaunchKernelGGL((qmv_kernel<K, CB, 4, true>), grid, dim3(1024), lds, s, p);
 }
-// The balanced QMV asks for more than 64 KB of dynamic LDS (it pins one
-// workgroup per CU), which needs the kernel's limit raised once (to 96 KB;
-// a failure is consumed here and shows as a failed launch).
-template <int K, int CB, bool PRE, bool MULTI>
-static void run_qmvb(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) {
-  static const hipError_t attr = [] {
-    const hipError_t e = hipFuncSetAttribute(
-        (const void*)qmvb_kernel<K, CB, kQmvbParts, PRE, MULTI>,
-        hipFuncAttributeMaxDynamicSharedMemorySize, 96 << 10);
-    if (e != hipSuccess) (void)hipGetLastError();
-    return e;
-  }();
-  (void)attr;
-  hipLaunchKernelGGL((qmvb_kernel<K, CB, kQmvbParts, PRE, MULTI>), grid, dim3(256 * kQmvbParts),
-                     lds, s, p);
-}
-template <int K, int CB>
-static void run_qmvb_single(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) {
-  run_qmvb<K, CB, false, false>(p, grid, lds, s);
-}
-template <int K, int CB>
-static void run_qmvb_multi(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) {
-  run_qmvb<K, CB, false, true>(p, grid, lds, s);
-}
-template <int K, int CB>
-static void run_qmvb_pre(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) {
-  run_qmvb<K, CB, true, true>(p, grid, lds, s);
-}
 template <int K, int CB>
 static void run_decode(const uint32_t* packed, int64_t tiles, uint16_t* st, uint16_t* val,
                        dim3 grid, hipStream_t s) {
@@ -155,8 +121,6 @@ void launch_qmv_inner(const uint16_t* values, const uint16_t* x, int rows, int c
 
 const QmvFn kQmv[3][8][3] = {EXL3_TABLE(run_qmv1), EXL3_TABLE(run_qmv2), EXL3_TABLE(run_qmv4)};
 const QmvFn kQmvSingle[8][3] = EXL3_TABLE(run_qmv1s);
-const QmvFn kQmvb[3][8][3] = {EXL3_TABLE(run_qmvb_single), EXL3_TABLE(run_qmvb_multi),
-                              EXL3_TABLE(run_qmvb_pre)};
 const DecodeFn kDecode[8][3] = EXL3_TABLE(run_decode);
 
 #endif

@@ -340,4 +340,12 @@ __device__ __forceinline__ void h128_wave(float& v0, float& v1, int lane) {
   }
 }
 
+// Slot of a 16-byte A chunk in its LDS row: chunk c of row r sits at
+// c ^ a_swizzle(r).  A fragment read (ds_read_b128, 16 rows x one chunk,
+// rows 128 bytes apart) is served 16 lanes (256 bytes, all 64 banks) at a
+// time on gfx950, so rows r and r + 8 (same bank offset r * 128 mod 256)
+// need different slots; r & 7 alone maps them to the same one (a 2-way
+// conflict that halved the read rate, 128 vs 256 B/clk measured).
+__device__ __forceinline__ int a_swizzle(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
 }  // namespace exl3

@@ -17,6 +17,8 @@ namespace exl3 {
 #define EXL3_MOE_INST(K, CB)                                          \
   template __global__ void moe_mm_kernel<K, CB, 2, 1>(MoeMmParams);  \
   template __global__ void moe_mm_kernel<K, CB, 1, 1>(MoeMmParams);  \
+  template __global__ void moe_mm_kernel<K, CB, 2, 2>(MoeMmParams);  \
+  template __global__ void moe_mm_kernel<K, CB, 1, 2>(MoeMmParams);  \
   template __global__ void moe_mm_kernel<K, CB, 2, 4>(MoeMmParams);  \
   template __global__ void moe_mm_kernel<K, CB, 1, 4>(MoeMmParams);
 // K = 7 is not a SwitchGLU width (switch_glu_layout rejects it).
@@ -40,9 +42,11 @@ typedef void (*MoeKernel)(MoeMmParams);
   {EXL3_MOE_ROW(N, MB, 1), EXL3_MOE_ROW(N, MB, 2), EXL3_MOE_ROW(N, MB, 3),               \
    EXL3_MOE_ROW(N, MB, 4), EXL3_MOE_ROW(N, MB, 5), EXL3_MOE_ROW(N, MB, 6),               \
    {nullptr, nullptr, nullptr}, EXL3_MOE_ROW(N, MB, 8)}
-// [MB == 4][K-1][codebook]
-static const MoeKernel kGateUp[2][8][3] = {EXL3_MOE_TABLE(2, 1), EXL3_MOE_TABLE(2, 4)};
-static const MoeKernel kDown[2][8][3] = {EXL3_MOE_TABLE(1, 1), EXL3_MOE_TABLE(1, 4)};
+// [block rows 16, 32, 64][K-1][codebook]
+static const MoeKernel kGateUp[3][8][3] = {EXL3_MOE_TABLE(2, 1), EXL3_MOE_TABLE(2, 2),
+                                           EXL3_MOE_TABLE(2, 4)};
+static const MoeKernel kDown[3][8][3] = {EXL3_MOE_TABLE(1, 1), EXL3_MOE_TABLE(1, 2),
+                                         EXL3_MOE_TABLE(1, 4)};
 
 struct exl3_moe {
   const uint16_t *gu_trellis, *gu_suh, *gu_svh;
@@ -83,11 +87,16 @@ bool moe_layout(const exl3_moe* h, int64_t rows, MoeLayout& L) {
   if (rows < 1) return false;
   const int64_t slots = rows * h->top_k;
   if (slots > (int64_t)1 << 24) return false;
-  // 64-row blocks once the average expert sees 8 or more rows
-  L.block_rows = slots >= 8 * (int64_t)h->experts ? kMoeMaxBlockRows : 16;
+  // Rows per block by the average rows an expert sees: 16 below 8, 32 up to
+  // 24 (most experts then fit one block, and the 32-row kernel's 113 VGPRs
+  // leave room for two workgroups per CU where the 64-row kernel's ~170 allow
+  // one: 185 -> 162 us on the 256-token top-8 bank of 128 experts), 64 above
+  // (fewer blocks, so fewer decodes of each expert's weights).
+  const int64_t E = h->experts;
+  L.block_rows = slots < 8 * E ? 16 : slots <= 24 * E ? 32 : kMoeMaxBlockRows;
   if (const char* env = getenv("EXL3_MOE_BLOCK_ROWS")) {
     const int v = atoi(env);
-    if (v == 16 || v == 64) L.block_rows = v;
+    if (v == 16 || v == 32 || v == 64) L.block_rows = v;
   }
   // each expert's last block may be partial: sum ceil(c_e/b) <= slots/b + E
   const int64_t max_blocks = slots / L.block_rows + h->experts + 1;
@@ -235,10 +244,10 @@ int exl3_moe_forward(const exl3_moe* h, const void* x, int32_t x_type, int64_t r
   if (!workspace || workspace_bytes < L.total)
     return fail(EXL3_EINVAL, "workspace too small: need %zu bytes, got %zu", L.total,
                 workspace_bytes);
-  const int mbi = L.block_rows == kMoeMaxBlockRows ? 1 : 0;
+  const int mbi = L.block_rows == kMoeMaxBlockRows ? 2 : L.block_rows == 32 ? 1 : 0;
   const MoeKernel gateup = kGateUp[mbi][h->k - 1][h->cb], down = kDown[mbi][h->k - 1][h->cb];
   if (!gateup || !down) return fail(EXL3_EUNSUPPORTED, "no SwitchGLU kernel for K=%d", h->k);
-  const int64_t wide = (int64_t)L.max_blocks * (std::max(h->in, h->hidden) / 128) *
+  const int64_t wide = (int64_t)(L.max_blocks + 7) * (std::max(h->in, h->hidden) / 128) *
                        std::max(L.splits_gu, L.splits_down);
   if (wide * 512 >= ((int64_t)1 << 31))
     return fail(EXL3_EUNSUPPORTED, "SwitchGLU launch of %lld rows is too large", (long long)rows);
@@ -287,7 +296,8 @@ int exl3_moe_forward(const exl3_moe* h, const void* x, int32_t x_type, int64_t r
   q.xd = (uint16_t*)(ws + L.xd);
   q.gelu = h->gelu;
   q.logical_hidden = h->logical_hidden;
-  gateup<<<L.max_blocks * q.col_blocks * q.splits, 512, 0, s>>>(q);
+  const int grid_blocks = (L.max_blocks + 7) / 8 * 8;  // whole blocks per XCD
+  gateup<<<grid_blocks * q.col_blocks * q.splits, 512, 0, s>>>(q);
   if (int rc = check_launch("moe gate/up")) return rc;
 
   // down: input width `hidden`, per-expert output `in`
@@ -302,7 +312,7 @@ int exl3_moe_forward(const exl3_moe* h, const void* x, int32_t x_type, int64_t r
   q.scores = scores;
   q.scores_dtype = scores_type;
   q.z = ws + L.z;
-  down<<<L.max_blocks * q.col_blocks * q.splits, 256, 0, s>>>(q);
+  down<<<grid_blocks * q.col_blocks * q.splits, 256, 0, s>>>(q);
   if (int rc = check_launch("moe down")) return rc;
 
   moe_reduce_kernel<<<dim3((unsigned)rows, (h->in + 255) / 256), 256, 0, s>>>(

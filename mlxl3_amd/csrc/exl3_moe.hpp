@@ -3,7 +3,7 @@
 // SwiGLU glue, down projection, weighted top-k reduction -- re-designed for
 // gfx950 as five launches:
 //   1. plan:    one workgroup counting-sorts the rows*top_k slots by expert,
-//               cuts each expert's run into blocks of <= 16 or 64 rows (block
+//               cuts each expert's run into blocks of <= 16, 32 or 64 rows (block
 //               table) and clears the tile arrival counters of the two expert
 //               QMMs;
 //   2. gather:  f16(x[token] * gu_suh[e][p]) -> staged Hadamard-128 for the gate
@@ -50,7 +50,7 @@ struct MoePlanParams {
   int* expert_count;         // [experts] (rows routed to each expert)
   uint32_t* counters;        // [ncounters] tile arrival counters, cleared here
   int ncounters;
-  int block_rows;            // 16 or 64
+  int block_rows;            // 16, 32 or 64
 };
 
 // One workgroup of 1024 threads.  Slots with an expert id >= experts are left
@@ -259,7 +259,7 @@ __device__ __forceinline__ void moe_finish_row(const MoeMmParams& p, int e, int 
 template <int K, int CB, int NPROJ, int MB>
 __global__ __launch_bounds__(256 * NPROJ) void moe_mm_kernel(MoeMmParams p) {
   // A rows of the block pass through LDS, three steps deep: [stage][proj][row]
-  // [8 chunks of 16 bytes], chunk c of row r at slot c ^ (r & 7) so that both
+  // [8 chunks of 16 bytes], chunk c of row r at slot c ^ a_swizzle(r) so that both
   // the row-wise stores and the 16-row fragment reads are conflict-free.
   constexpr int kRows = 16 * MB, kStage = NPROJ * kRows * 128;
   __shared__ __attribute__((aligned(16))) uint8_t as[3][kStage];
@@ -268,10 +268,16 @@ __global__ __launch_bounds__(256 * NPROJ) void moe_mm_kernel(MoeMmParams p) {
   constexpr bool GLU = NPROJ == 2;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int proj = wave >> 2, pair = wave & 3;
-  // workgroup -> (block, column block, split), split fastest
-  const int split = blockIdx.x % p.splits;
-  const int bc = blockIdx.x / p.splits;
-  const int blk = bc / p.col_blocks, cblk = bc % p.col_blocks;
+  // Workgroup -> (block, column block, split).  Workgroups go to the 8 XCDs
+  // round-robin (XCD = id % 8); XCD x takes blocks x, x + 8, x + 16, ...
+  // whole, every column block and split of one, so the block's routed rows
+  // are read from HBM once into that XCD's L2 instead of once per column
+  // block.  The grid holds ceil(max_blocks / 8) * 8 blocks.
+  const int per_blk = p.col_blocks * p.splits;
+  const int wk = blockIdx.x >> 3;
+  const int blk = (wk / per_blk) * 8 + (blockIdx.x & 7);
+  const int wi = wk % per_blk;
+  const int split = wi % p.splits, cblk = wi / p.splits;
   if (blk >= p.counts[0]) return;  // uniform
   const int4 ent = p.table[blk];
   const int e = ent.x, pos0 = ent.y, nrows = ent.z;
@@ -302,7 +308,7 @@ __global__ __launch_bounds__(256 * NPROJ) void moe_mm_kernel(MoeMmParams p) {
     const int pj = cc / (kRows * 8), row = (cc / 8) % kRows, ch = cc & 7;
     lsrc[i] = p.xa + ((size_t)pj * p.slots_pad + pos0 + min(row, nrows - 1)) * p.k_in +
               (size_t)qa * 64 + ch * 8;
-    ldst[i] = (pj * kRows + row) * 128 + ((ch ^ (row & 7)) << 4);
+    ldst[i] = (pj * kRows + row) * 128 + ((ch ^ a_swizzle(row)) << 4);
   }
   const int qlast = nq - 1;
   u32x4 areg[2][kPer];
@@ -323,7 +329,7 @@ __global__ __launch_bounds__(256 * NPROJ) void moe_mm_kernel(MoeMmParams p) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int row = 16 * mb + am;
-      aoff[mb][h] = (proj * kRows + row) * 128 + (((2 * g + h) ^ (row & 7)) << 4);
+      aoff[mb][h] = (proj * kRows + row) * 128 + (((2 * g + h) ^ a_swizzle(row)) << 4);
     }
 
   constexpr int D = kQmvDepth<K>;

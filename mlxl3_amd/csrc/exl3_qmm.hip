@@ -11,6 +11,8 @@ namespace exl3 {
   template __global__ void qmm_kernel<K, CB, 2>(QmmParams); \
   template __global__ void qmm_kernel<K, CB, 4>(QmmParams);
 EXL3_INSTANTIATE(EXL3_QMM_INST)
+template __global__ void prologue_kernel<true>(PrologueParams);
+template __global__ void prologue_kernel<false>(PrologueParams);
 
 // out = swiglu(gate, up) or geglu(gate, up) elementwise in f16, eight
 // elements per thread where the buffers allow 16-byte access.
@@ -74,9 +76,15 @@ static void run_qmm4(const QmmParams& p, dim3 g, hipStream_t s) {
 const QmmFn kQmm[3][8][3] = {EXL3_TABLE(run_qmm1), EXL3_TABLE(run_qmm2), EXL3_TABLE(run_qmm4)};
 
 void launch_prologue(const PrologueParams& p, int members, hipStream_t s) {
-  const int64_t waves = (int64_t)p.rows * ((p.in / 128 + 7) / 8);
-  hipLaunchKernelGGL(prologue_kernel, dim3((unsigned)((waves + 3) / 4), (unsigned)members),
-                     dim3(256), 0, s, p);
+  const int64_t groups = ((int64_t)p.rows * (p.in / 128) + 15) / 16;
+  uintptr_t bits = (uintptr_t)p.x;
+  for (int i = 0; i < members; ++i) bits |= (uintptr_t)p.suh[i] | (uintptr_t)p.xhat[i];
+  if ((bits & 15) == 0)
+    hipLaunchKernelGGL(prologue_kernel<true>, dim3((unsigned)groups, (unsigned)members),
+                       dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(prologue_kernel<false>, dim3((unsigned)groups, (unsigned)members),
+                       dim3(256), 0, s, p);
 }
 
 void launch_glu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n, bool gelu,

@@ -32,15 +32,55 @@
 namespace exl3 {
 
 
-// xhat[i] = prologue(x, suh[i]) for all rows of each member i (grid.y): one
-// wave per (row, run of eight 128-input blocks), pair layout with the run's
-// loads in flight together.  grid (ceil(rows * runs / 4), members), 256 threads.
-// suh_stride = in gives every row its own scales (exl3_prepare128).
+template <int STRIDE>
+__device__ __forceinline__ float bfly_lane(float v, int lane) {
+  float p = xor_lanes<STRIDE>(v);
+  return (lane & STRIDE) ? p - v : v + p;
+}
+
+// Staged Hadamard-128 of a block held as 8 consecutive elements per lane, 16
+// lanes per block (a DPP row): element strides 1, 2, 4 inside the lane, 8..64
+// across lanes 1..8, f16 rounding after strides 8 and 64 (the reference's
+// radix staging, in the same stage order as the pair layout).
+__device__ __forceinline__ void h128_lane8(float (&v)[8], int lane) {
+#pragma unroll
+  for (int s = 1; s < 8; s <<= 1)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (!(j & s)) {
+        const float a0 = v[j], b0 = v[j + s];
+        v[j] = a0 + b0;
+        v[j + s] = a0 - b0;
+      }
+  // stride 8 = lane bit 0, then f16 rounding
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = round_f16(bfly_lane<1>(v[j], lane));
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    v[j] = bfly_lane<2>(v[j], lane);  // stride 16
+    v[j] = bfly_lane<4>(v[j], lane);  // stride 32
+    v[j] = round_f16(bfly_lane<8>(v[j], lane));  // stride 64
+  }
+}
+
+// xhat[i] = prologue(x, suh[i]) for all rows of each member i (grid.y):
+// f16(H128(f16(f16(x) * suh)) / sqrt(128)) per 128-input block.  A lane takes
+// 8 consecutive inputs of one (row, block) job and 16 lanes a job, so the
+// whole Hadamard runs on DPP exchanges inside a 16-lane row and every lane
+// moves 16-byte words (VEC; byte-aligned x, suh or xhat take the element-wise
+// loads instead).  suh_stride = in gives every row its own scales
+// (exl3_prepare128).  grid (ceil(rows * blocks / 16), members), 256 threads.
+template <bool VEC>
 __global__ __launch_bounds__(256) void prologue_kernel(PrologueParams p) {
-  const int nb = p.in >> 7, runs = (nb + 7) >> 3;
-  const int job = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int row = job / runs, run = job - row * runs;
-  if (row >= p.rows) return;  // uniform per wave
+  const int nb = p.in >> 7;
+  const int64_t njobs = (int64_t)p.rows * nb;
+  const int64_t job = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  // past-the-end groups redo the last job (all lanes of a DPP row stay
+  // active) and store nothing
+  const bool live = job < njobs;
+  const int64_t jc = live ? job : njobs - 1;
+  const int row = (int)(jc / nb), b = (int)(jc - (int64_t)row * nb);
+  const int lane = threadIdx.x & 63, c8 = 8 * (threadIdx.x & 15);
   const uint16_t* suh = p.suh[0];
   uint16_t* xhat = p.xhat[0];
 #pragma unroll
@@ -49,8 +89,56 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueParams p) {
       suh = p.suh[i];
       xhat = p.xhat[i];
     }
-  pair_prologue_row(p.x, p.x_dtype, (size_t)row * p.in, suh + (size_t)row * p.suh_stride,
-                    8 * run, min(8 * run + 8, nb), threadIdx.x & 63, xhat + (size_t)row * p.in);
+  const size_t e = (size_t)row * p.in + (size_t)b * 128 + c8;
+  const uint16_t* sp = suh + (size_t)row * p.suh_stride + (size_t)b * 128 + c8;
+  float a[8], sv[8];
+  if constexpr (VEC) {
+    if (p.x_dtype == DT_F32) {
+      const float4v* xp = (const float4v*)((const float*)p.x + e);
+      const float4v x0 = xp[0], x1 = xp[1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i] = x0[i];
+        a[i + 4] = x1[i];
+      }
+    } else {
+      const u32x4 xw = *(const u32x4*)((const uint16_t*)p.x + e);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[2 * i] = raw_act(xw[i] & 0xffffu, p.x_dtype);
+        a[2 * i + 1] = raw_act(xw[i] >> 16, p.x_dtype);
+      }
+    }
+    const u32x4 sw = *(const u32x4*)sp;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sv[2 * i] = h2f((uint16_t)sw[i]);
+      sv[2 * i + 1] = h2f((uint16_t)(sw[i] >> 16));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a[i] = p.x_dtype == DT_F32 ? ((const float*)p.x)[e + i]
+                                 : raw_act(((const uint16_t*)p.x)[e + i], p.x_dtype);
+      sv[i] = h2f(sp[i]);
+    }
+  }
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = round_f16(round_f16(a[i]) * sv[i]);
+  h128_lane8(v, lane);
+  if (!live) return;
+  uint16_t* dst = xhat + e;
+  if constexpr (VEC) {
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o[i] = (uint32_t)f2h(v[2 * i] * kHadScale) | ((uint32_t)f2h(v[2 * i + 1] * kHadScale) << 16);
+    *(u32x4*)dst = o;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dst[i] = f2h(v[i] * kHadScale);
+  }
 }
 
 // The SwiGLU edge between a (gate, up) group and its down projection:
@@ -91,12 +179,6 @@ __global__ __launch_bounds__(256) void swiglu_prepare_kernel(const uint16_t* __r
                                          round_f16(a1 * h2f((uint16_t)(sp[t] >> 16))), lane);
     if (b_begin + t < b_end) x32[(b_begin + t) * 64 + lane] = bits;
   }
-}
-
-template <int STRIDE>
-__device__ __forceinline__ float bfly_lane(float v, int lane) {
-  float p = xor_lanes<STRIDE>(v);
-  return (lane & STRIDE) ? p - v : v + p;
 }
 
 // Rows of a finished tile pass through LDS as f16: Y[row][136] (128 columns
@@ -150,24 +232,7 @@ __device__ __forceinline__ void qmm_finish_chunk(const u32x4 raw, const float (&
     v[2 * i] = h2f((uint16_t)raw[i]);
     v[2 * i + 1] = h2f((uint16_t)(raw[i] >> 16));
   }
-#pragma unroll
-  for (int s = 1; s < 8; s <<= 1)
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (!(j & s)) {
-        const float a0 = v[j], b0 = v[j + s];
-        v[j] = a0 + b0;
-        v[j + s] = a0 - b0;
-      }
-  // stride 8 = lane bit 0, then f16 rounding
-#pragma unroll
-  for (int j = 0; j < 8; ++j) v[j] = round_f16(bfly_lane<1>(v[j], lane));
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    v[j] = bfly_lane<2>(v[j], lane);  // stride 16
-    v[j] = bfly_lane<4>(v[j], lane);  // stride 32
-    v[j] = round_f16(bfly_lane<8>(v[j], lane));  // stride 64
-  }
+  h128_lane8(v, lane);
 #pragma unroll
   for (int j = 0; j < 8; ++j) v[j] = round_f16(round_f16(v[j] * kHadScale) * sv[j]);
   if (!live) return;
@@ -246,8 +311,9 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
   const int row_base = mtile * 64 * MB + role * 16 * MB;  // first row of consumer `role`
 
   // A rows sit in LDS as [row][8 chunks of 16 bytes] with chunk c of row r at
-  // slot c ^ (r & 7): the producers' row-wise writes and the consumers'
-  // fragment reads (16 rows x one chunk) are both free of bank conflicts.
+  // slot c ^ a_swizzle(r): the producers' row-wise writes and the
+  // consumers' fragment reads (16 rows x one chunk) are both free of bank
+  // conflicts.
 
   // Step s of the K loop uses stage s % 3.  In iteration q the producers fill
   // stage (q+2) % 3 with step q+2 while the consumers multiply step q and,
@@ -291,7 +357,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
 #pragma unroll
       for (int i = 0; i < 2 * MB; ++i) {
         const int r = 8 * i + ar;
-        *(u32x4*)(base + r * 128 + ((ac ^ (r & 7)) << 4)) = src[i];
+        *(u32x4*)(base + r * 128 + ((ac ^ a_swizzle(r)) << 4)) = src[i];
       }
     };
     // steps 0 and 1
@@ -343,7 +409,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int r = role * 16 * MB + 16 * mb + n;
-        aoff[mb][h] = r * 128 + (((2 * g + h) ^ (r & 7)) << 4);
+        aoff[mb][h] = r * 128 + (((2 * g + h) ^ a_swizzle(r)) << 4);
       }
     half8 a[2][MB][2], b[2][4];
     auto read_a = [&](half8(&dst)[MB][2], int st) {

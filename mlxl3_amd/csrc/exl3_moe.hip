@@ -29,6 +29,12 @@ EXL3_INST_CB(EXL3_MOE_INST, 4)
 EXL3_INST_CB(EXL3_MOE_INST, 5)
 EXL3_INST_CB(EXL3_MOE_INST, 6)
 EXL3_INST_CB(EXL3_MOE_INST, 8)
+template __global__ void moe_gather_kernel<true>(const void*, int, int, int, const uint32_t*,
+                                                 const int*, const int*, int, const uint16_t*,
+                                                 uint16_t*);
+template __global__ void moe_gather_kernel<false>(const void*, int, int, int, const uint32_t*,
+                                                  const int*, const int*, int, const uint16_t*,
+                                                  uint16_t*);
 }  // namespace exl3
 
 using namespace exl3;
@@ -271,8 +277,15 @@ int exl3_moe_forward(const exl3_moe* h, const void* x, int32_t x_type, int64_t r
   if (int rc = check_launch("moe plan")) return rc;
 
   uint16_t* xgu = (uint16_t*)(ws + L.xgu);
-  moe_gather_kernel<<<(unsigned)((2 * (int64_t)slots + 3) / 4), 256, 0, s>>>(
-      x, x_type, h->in, h->top_k, selected, pp.sorted_slot, pp.counts + 1, slots, h->gu_suh, xgu);
+  const unsigned gather_wgs = (unsigned)((2 * (int64_t)slots * ((h->in / 128 + 7) / 8) + 3) / 4);
+  if ((((uintptr_t)x | (uintptr_t)h->gu_suh) & 15) == 0)
+    moe_gather_kernel<true><<<gather_wgs, 256, 0, s>>>(x, x_type, h->in, h->top_k, selected,
+                                                       pp.sorted_slot, pp.counts + 1, slots,
+                                                       h->gu_suh, xgu);
+  else
+    moe_gather_kernel<false><<<gather_wgs, 256, 0, s>>>(x, x_type, h->in, h->top_k, selected,
+                                                        pp.sorted_slot, pp.counts + 1, slots,
+                                                        h->gu_suh, xgu);
   if (int rc = check_launch("moe gather")) return rc;
 
   MoeMmParams q{};

@@ -119,9 +119,11 @@ __global__ __launch_bounds__(1024) void moe_plan_kernel(MoePlanParams p) {
 
 // Gate/up inputs in sorted order: xgu[proj][pos][in] with proj 0 = gate,
 // 1 = up (routed_inputs, moe.rs:184-250).  One wave per (position,
-// projection): the slot and expert lookups once, then the row's blocks with
-// eight blocks' loads in flight.  grid ceil(2 * slots / 4), 256 threads;
-// positions past the routed count idle.
+// projection, run of 8 128-blocks): the slot and expert lookups once per
+// wave, then 16 lanes per block (prologue8), each lane's two blocks loaded
+// together; positions past the routed count idle.  grid ceil(2 * slots *
+// ceil(in / 1024) / 4), 256 threads.
+template <bool VEC>
 __global__ __launch_bounds__(256) void moe_gather_kernel(const void* __restrict__ x, int x_dtype,
                                                          int in, int top_k,
                                                          const uint32_t* selected,
@@ -129,13 +131,27 @@ __global__ __launch_bounds__(256) void moe_gather_kernel(const void* __restrict_
                                                          const int* routed, int slots_pad,
                                                          const uint16_t* __restrict__ gu_suh,
                                                          uint16_t* __restrict__ xgu) {
-  const int job = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int pos = job >> 1, proj = job & 1;
+  const int nb = in >> 7, runs = (nb + 7) >> 3;
+  const int job = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+  const int pp = job / runs, run = job - pp * runs;
+  const int pos = pp >> 1, proj = pp & 1;
   if (pos >= *routed) return;  // uniform per wave
   const int slot = sorted_slot[pos];
   const uint16_t* suh = gu_suh + ((size_t)selected[slot] * 2 + proj) * in;
-  pair_prologue_row(x, x_dtype, (size_t)(slot / top_k) * in, suh, 0, in >> 7, threadIdx.x & 63,
-                    xgu + ((size_t)proj * slots_pad + pos) * in);
+  const size_t xrow = (size_t)(slot / top_k) * in;
+  uint16_t* dst = xgu + ((size_t)proj * slots_pad + pos) * in;
+  const int lane = threadIdx.x & 63;
+  const int b0 = 8 * run + (lane >> 4), b1 = b0 + 4;
+  const int bl = min(b1, nb - 1);  // clamped: the second block's lanes stay in bounds
+  const int c0 = b0 * 128 + 8 * (lane & 15), c1 = bl * 128 + 8 * (lane & 15);
+  // a group past the row's end (its last run holding fewer than 4 blocks)
+  // recomputes block nb - 1 without storing; both blocks' loads go out first
+  const int c0c = b0 < nb ? c0 : (nb - 1) * 128 + 8 * (lane & 15);
+  float a0[8], s0[8], a1[8], s1[8];
+  load8<VEC>(x, x_dtype, xrow + c0c, suh + c0c, a0, s0);
+  load8<VEC>(x, x_dtype, xrow + c1, suh + c1, a1, s1);
+  finish8<VEC>(a0, s0, dst + c0c, b0 < nb, lane);
+  finish8<VEC>(a1, s1, dst + c1, b1 < nb, lane);
 }
 
 struct MoeMmParams {

@@ -13,6 +13,10 @@ namespace exl3 {
 EXL3_INSTANTIATE(EXL3_QMM_INST)
 template __global__ void prologue_kernel<true>(PrologueParams);
 template __global__ void prologue_kernel<false>(PrologueParams);
+template __global__ void swiglu_prepare_kernel<true>(const uint16_t*, const uint16_t*,
+                                                     const uint16_t*, int, int, uint16_t*);
+template __global__ void swiglu_prepare_kernel<false>(const uint16_t*, const uint16_t*,
+                                                      const uint16_t*, int, int, uint16_t*);
 
 // out = swiglu(gate, up) or geglu(gate, up) elementwise in f16, eight
 // elements per thread where the buffers allow 16-byte access.
@@ -100,9 +104,13 @@ void launch_glu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t
 
 void launch_swiglu_prepare(const uint16_t* gate, const uint16_t* up, const uint16_t* down_suh,
                            int H, int rows, uint16_t* xhat, hipStream_t s) {
-  const int64_t waves = (int64_t)rows * ((H / 128 + 7) / 8);
-  hipLaunchKernelGGL(swiglu_prepare_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s,
-                     gate, up, down_suh, H, rows, xhat);
+  const unsigned groups = (unsigned)(((int64_t)rows * (H / 128) + 15) / 16);
+  if ((((uintptr_t)gate | (uintptr_t)up | (uintptr_t)down_suh | (uintptr_t)xhat) & 15) == 0)
+    hipLaunchKernelGGL(swiglu_prepare_kernel<true>, dim3(groups), dim3(256), 0, s, gate, up,
+                       down_suh, H, rows, xhat);
+  else
+    hipLaunchKernelGGL(swiglu_prepare_kernel<false>, dim3(groups), dim3(256), 0, s, gate, up,
+                       down_suh, H, rows, xhat);
 }
 
 void launch_fill_zero(uint32_t* p, size_t words, hipStream_t s) {

@@ -31,45 +31,10 @@
 
 namespace exl3 {
 
-
-template <int STRIDE>
-__device__ __forceinline__ float bfly_lane(float v, int lane) {
-  float p = xor_lanes<STRIDE>(v);
-  return (lane & STRIDE) ? p - v : v + p;
-}
-
-// Staged Hadamard-128 of a block held as 8 consecutive elements per lane, 16
-// lanes per block (a DPP row): element strides 1, 2, 4 inside the lane, 8..64
-// across lanes 1..8, f16 rounding after strides 8 and 64 (the reference's
-// radix staging, in the same stage order as the pair layout).
-__device__ __forceinline__ void h128_lane8(float (&v)[8], int lane) {
-#pragma unroll
-  for (int s = 1; s < 8; s <<= 1)
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (!(j & s)) {
-        const float a0 = v[j], b0 = v[j + s];
-        v[j] = a0 + b0;
-        v[j + s] = a0 - b0;
-      }
-  // stride 8 = lane bit 0, then f16 rounding
-#pragma unroll
-  for (int j = 0; j < 8; ++j) v[j] = round_f16(bfly_lane<1>(v[j], lane));
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    v[j] = bfly_lane<2>(v[j], lane);  // stride 16
-    v[j] = bfly_lane<4>(v[j], lane);  // stride 32
-    v[j] = round_f16(bfly_lane<8>(v[j], lane));  // stride 64
-  }
-}
-
-// xhat[i] = prologue(x, suh[i]) for all rows of each member i (grid.y):
-// f16(H128(f16(f16(x) * suh)) / sqrt(128)) per 128-input block.  A lane takes
-// 8 consecutive inputs of one (row, block) job and 16 lanes a job, so the
-// whole Hadamard runs on DPP exchanges inside a 16-lane row and every lane
-// moves 16-byte words (VEC; byte-aligned x, suh or xhat take the element-wise
-// loads instead).  suh_stride = in gives every row its own scales
-// (exl3_prepare128).  grid (ceil(rows * blocks / 16), members), 256 threads.
+// xhat[i] = prologue(x, suh[i]) for all rows of each member i (grid.y), 16
+// lanes per (row, 128-block) job (prologue8).  suh_stride = in gives every
+// row its own scales (exl3_prepare128).  grid (ceil(rows * blocks / 16),
+// members), 256 threads.
 template <bool VEC>
 __global__ __launch_bounds__(256) void prologue_kernel(PrologueParams p) {
   const int nb = p.in >> 7;
@@ -80,7 +45,7 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueParams p) {
   const bool live = job < njobs;
   const int64_t jc = live ? job : njobs - 1;
   const int row = (int)(jc / nb), b = (int)(jc - (int64_t)row * nb);
-  const int lane = threadIdx.x & 63, c8 = 8 * (threadIdx.x & 15);
+  const int c8 = 8 * (threadIdx.x & 15);
   const uint16_t* suh = p.suh[0];
   uint16_t* xhat = p.xhat[0];
 #pragma unroll
@@ -90,95 +55,49 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueParams p) {
       xhat = p.xhat[i];
     }
   const size_t e = (size_t)row * p.in + (size_t)b * 128 + c8;
-  const uint16_t* sp = suh + (size_t)row * p.suh_stride + (size_t)b * 128 + c8;
-  float a[8], sv[8];
-  if constexpr (VEC) {
-    if (p.x_dtype == DT_F32) {
-      const float4v* xp = (const float4v*)((const float*)p.x + e);
-      const float4v x0 = xp[0], x1 = xp[1];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a[i] = x0[i];
-        a[i + 4] = x1[i];
-      }
-    } else {
-      const u32x4 xw = *(const u32x4*)((const uint16_t*)p.x + e);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a[2 * i] = raw_act(xw[i] & 0xffffu, p.x_dtype);
-        a[2 * i + 1] = raw_act(xw[i] >> 16, p.x_dtype);
-      }
-    }
-    const u32x4 sw = *(const u32x4*)sp;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sv[2 * i] = h2f((uint16_t)sw[i]);
-      sv[2 * i + 1] = h2f((uint16_t)(sw[i] >> 16));
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      a[i] = p.x_dtype == DT_F32 ? ((const float*)p.x)[e + i]
-                                 : raw_act(((const uint16_t*)p.x)[e + i], p.x_dtype);
-      sv[i] = h2f(sp[i]);
-    }
-  }
-  float v[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = round_f16(round_f16(a[i]) * sv[i]);
-  h128_lane8(v, lane);
-  if (!live) return;
-  uint16_t* dst = xhat + e;
-  if constexpr (VEC) {
-    u32x4 o;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      o[i] = (uint32_t)f2h(v[2 * i] * kHadScale) | ((uint32_t)f2h(v[2 * i + 1] * kHadScale) << 16);
-    *(u32x4*)dst = o;
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) dst[i] = f2h(v[i] * kHadScale);
-  }
+  prologue8<VEC>(p.x, p.x_dtype, e, suh + (size_t)row * p.suh_stride + (size_t)b * 128 + c8,
+                 xhat + e, live, threadIdx.x & 63);
 }
 
 // The SwiGLU edge between a (gate, up) group and its down projection:
 // xhat_down = f16(H128(f16(swiglu(g, u) * down_suh)) / sqrt(128)) (the down
 // projection's prologue applied to the activation, as the reference's
 // flash_up_finish_swiglu_prepare fuses them, exl3.metal:265-291, with
-// Array::swiglu's f16 arithmetic).  One wave per (row, run of eight
-// 128-blocks), pair layout, the run's loads in flight together.
-// grid (ceil(rows * runs / 4)), 256 threads.
+// Array::swiglu's f16 arithmetic).  16 lanes per (row, 128-block) job, 8
+// columns per lane (finish8).  grid (ceil(rows * H / 128 / 16)), 256 threads.
+template <bool VEC>
 __global__ __launch_bounds__(256) void swiglu_prepare_kernel(const uint16_t* __restrict__ gate,
                                                              const uint16_t* __restrict__ up,
                                                              const uint16_t* __restrict__ down_suh,
                                                              int H, int rows,
                                                              uint16_t* __restrict__ xhat) {
-  const int nb = H >> 7, runs = (nb + 7) >> 3;
-  const int job = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int row = job / runs, run = job - row * runs;
-  if (row >= rows) return;  // uniform per wave
-  const int lane = threadIdx.x & 63;
-  const int b_begin = 8 * run, b_end = min(b_begin + 8, nb);
-  const uint32_t* g32 = (const uint32_t*)(gate + (size_t)row * H);
-  const uint32_t* u32 = (const uint32_t*)(up + (size_t)row * H);
-  const uint32_t* s32 = (const uint32_t*)down_suh;
-  uint32_t* x32 = (uint32_t*)(xhat + (size_t)row * H);
-  uint32_t gp[8], up2[8], sp[8];
+  const int nb = H >> 7;
+  const int64_t njobs = (int64_t)rows * nb;
+  const int64_t job = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const bool live = job < njobs;  // past-the-end groups redo the last job unstored
+  const int64_t jc = live ? job : njobs - 1;
+  const int row = (int)(jc / nb), b = (int)(jc - (int64_t)row * nb);
+  const int c = b * 128 + 8 * (threadIdx.x & 15);
+  const size_t e = (size_t)row * H + c;
+  float a[8], sv[8];
+  if constexpr (VEC) {
+    const u32x4 gw = *(const u32x4*)(gate + e), uw = *(const u32x4*)(up + e);
+    const u32x4 sw = *(const u32x4*)(down_suh + c);
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const int b = min(b_begin + t, b_end - 1);  // clamped: loads stay in bounds
-    gp[t] = g32[b * 64 + lane];
-    up2[t] = u32[b * 64 + lane];
-    sp[t] = s32[b * 64 + lane];
-  }
+    for (int i = 0; i < 4; ++i) {
+      a[2 * i] = swiglu_f16(h2f((uint16_t)gw[i]), h2f((uint16_t)uw[i]));
+      a[2 * i + 1] = swiglu_f16(h2f((uint16_t)(gw[i] >> 16)), h2f((uint16_t)(uw[i] >> 16)));
+      sv[2 * i] = h2f((uint16_t)sw[i]);
+      sv[2 * i + 1] = h2f((uint16_t)(sw[i] >> 16));
+    }
+  } else {
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const float a0 = swiglu_f16(h2f((uint16_t)gp[t]), h2f((uint16_t)up2[t]));
-    const float a1 = swiglu_f16(h2f((uint16_t)(gp[t] >> 16)), h2f((uint16_t)(up2[t] >> 16)));
-    const uint32_t bits = pair_h128_bits(round_f16(a0 * h2f((uint16_t)sp[t])),
-                                         round_f16(a1 * h2f((uint16_t)(sp[t] >> 16))), lane);
-    if (b_begin + t < b_end) x32[(b_begin + t) * 64 + lane] = bits;
+    for (int i = 0; i < 8; ++i) {
+      a[i] = swiglu_f16(h2f(gate[e + i]), h2f(up[e + i]));
+      sv[i] = h2f(down_suh[c + i]);
+    }
   }
+  finish8<VEC>(a, sv, xhat + e, live, threadIdx.x & 63);
 }
 
 // Rows of a finished tile pass through LDS as f16: Y[row][136] (128 columns

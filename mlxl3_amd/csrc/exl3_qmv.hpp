@@ -218,84 +218,111 @@ __device__ __forceinline__ void prologue_finish(const PrologueIn& in, int x_dtyp
 // suh load per lane.  The butterflies run in the same ascending order with the
 // same roundings as h128_wave: stride 1 inside the lane, strides 2..64 across
 // lanes 1..32, f16 rounding after strides 8 and 64.
-struct PairIn {
-  uint32_t x0, x1;  // raw activation bits (x1: high word of the second f32)
-  uint32_t s;       // two suh halves
-};
-__device__ __forceinline__ PairIn pair_load(const void* x, int x_dtype, size_t off,
-                                            const uint16_t* __restrict__ suh, int e0, int lane) {
-  PairIn in;
-  if (x_dtype == DT_F32) {
-    const uint2 v = ((const uint2*)((const float*)x + off))[lane];
-    in.x0 = v.x;
-    in.x1 = v.y;
-  } else {
-    in.x0 = ((const uint32_t*)((const uint16_t*)x + off))[lane];
-    in.x1 = 0;
-  }
-  in.s = ((const uint32_t*)(suh + e0))[lane];
-  return in;
-}
-// Staged H128 of a 128-block in the pair layout (lane holds elements 2*lane,
-// 2*lane+1 as v0, v1), then f16(* 1/sqrt 128): the packed f16 bits (element
-// 2*lane low).
-__device__ __forceinline__ uint32_t pair_h128_bits(float v0, float v1, int lane) {
-  {  // stride 1
-    const float t = v0;
-    v0 = t + v1;
-    v1 = t - v1;
-  }
-  static_for<6>([&](auto i_) {
-    constexpr int ls = 1 << decltype(i_)::value;  // element stride 2*ls
-    const float p0 = xor_lanes<ls>(v0), p1 = xor_lanes<ls>(v1);
-    if (lane & ls) {
-      v0 = p0 - v0;
-      v1 = p1 - v1;
-    } else {
-      v0 = v0 + p0;
-      v1 = v1 + p1;
-    }
-    if (ls == 4 || ls == 32) {  // after element strides 8 and 64
-      v0 = round_f16(v0);
-      v1 = round_f16(v1);
-    }
-  });
-  return (uint32_t)f2h(v0 * kHadScale) | ((uint32_t)f2h(v1 * kHadScale) << 16);
-}
-// xhat bits of the lane's two elements, packed (element 2*lane low).
-__device__ __forceinline__ uint32_t pair_finish(const PairIn& in, int x_dtype, int lane) {
-  float a, b;
-  if (x_dtype == DT_F32) {
-    a = __builtin_bit_cast(float, in.x0);
-    b = __builtin_bit_cast(float, in.x1);
-  } else {
-    a = raw_act(in.x0 & 0xffffu, x_dtype);
-    b = raw_act(in.x0 >> 16, x_dtype);
-  }
-  const float v0 = round_f16(round_f16(a) * h2f((uint16_t)in.s));
-  const float v1 = round_f16(round_f16(b) * h2f((uint16_t)(in.s >> 16)));
-  return pair_h128_bits(v0, v1, lane);
+template <int STRIDE>
+__device__ __forceinline__ float bfly_lane(float v, int lane) {
+  float p = xor_lanes<STRIDE>(v);
+  return (lane & STRIDE) ? p - v : v + p;
 }
 
-// Prologue of 128-input blocks [b_begin, b_end) of a row by one wave in the
-// pair layout: the loads of up to eight blocks are in flight together.
-// dst: xhat row (f16).
-__device__ __forceinline__ void pair_prologue_row(const void* x, int x_dtype, size_t xoff,
-                                                  const uint16_t* __restrict__ suh, int b_begin,
-                                                  int b_end, int lane, uint16_t* __restrict__ dst) {
-  for (int b0 = b_begin; b0 < b_end; b0 += 8) {
-    PairIn in[8];
+// Staged Hadamard-128 of a block held as 8 consecutive elements per lane, 16
+// lanes per block (a DPP row): element strides 1, 2, 4 inside the lane, 8..64
+// across lanes 1..8, f16 rounding after strides 8 and 64 (the reference's
+// radix staging: strides in increasing order, f32 between the roundings).
+__device__ __forceinline__ void h128_lane8(float (&v)[8], int lane) {
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int b = min(b0 + t, b_end - 1);  // clamped: loads stay in bounds
-      in[t] = pair_load(x, x_dtype, xoff + b * 128, suh, b * 128, lane);
+  for (int s = 1; s < 8; s <<= 1)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (!(j & s)) {
+        const float a0 = v[j], b0 = v[j + s];
+        v[j] = a0 + b0;
+        v[j + s] = a0 - b0;
+      }
+  // stride 8 = lane bit 0, then f16 rounding
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = round_f16(bfly_lane<1>(v[j], lane));
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    v[j] = bfly_lane<2>(v[j], lane);  // stride 16
+    v[j] = bfly_lane<4>(v[j], lane);  // stride 32
+    v[j] = round_f16(bfly_lane<8>(v[j], lane));  // stride 64
+  }
+}
+
+// Tail of prologue8: dst[0..7] = f16(H128(f16(f16(a) * s)) / sqrt(128)) over
+// the row of 16 lanes (stored only if live).
+template <bool VEC>
+__device__ __forceinline__ void finish8(const float (&a)[8], const float (&sv)[8], uint16_t* dst,
+                                        bool live, int lane) {
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = round_f16(round_f16(a[i]) * sv[i]);
+  h128_lane8(v, lane);
+  if (!live) return;
+  if constexpr (VEC) {
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o[i] = (uint32_t)f2h(v[2 * i] * kHadScale) | ((uint32_t)f2h(v[2 * i + 1] * kHadScale) << 16);
+    *(u32x4*)dst = o;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dst[i] = f2h(v[i] * kHadScale);
+  }
+}
+
+// The inputs of prologue8: a[i] = x[xe + i] (f16, bf16 or f32) and
+// sv[i] = sp[i] (f16), with 16-byte loads under VEC.
+template <bool VEC>
+__device__ __forceinline__ void load8(const void* x, int x_dtype, size_t xe, const uint16_t* sp,
+                                      float (&a)[8], float (&sv)[8]) {
+  if constexpr (VEC) {
+    if (x_dtype == DT_F32) {
+      const float4v* xp = (const float4v*)((const float*)x + xe);
+      const float4v x0 = xp[0], x1 = xp[1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i] = x0[i];
+        a[i + 4] = x1[i];
+      }
+    } else {
+      const u32x4 xw = *(const u32x4*)((const uint16_t*)x + xe);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[2 * i] = raw_act(xw[i] & 0xffffu, x_dtype);
+        a[2 * i + 1] = raw_act(xw[i] >> 16, x_dtype);
+      }
     }
+    const u32x4 sw = *(const u32x4*)sp;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const uint32_t bits = pair_finish(in[t], x_dtype, lane);
-      if (b0 + t < b_end) ((uint32_t*)(dst + (b0 + t) * 128))[lane] = bits;
+    for (int i = 0; i < 4; ++i) {
+      sv[2 * i] = h2f((uint16_t)sw[i]);
+      sv[2 * i + 1] = h2f((uint16_t)(sw[i] >> 16));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a[i] = x_dtype == DT_F32 ? ((const float*)x)[xe + i]
+                               : raw_act(((const uint16_t*)x)[xe + i], x_dtype);
+      sv[i] = h2f(sp[i]);
     }
   }
+}
+
+// f16(H128(f16(f16(x) * suh)) / sqrt(128)) of one 128-input block, held as
+// 8 consecutive inputs per lane and 16 lanes (one DPP row) per block: x[xe..]
+// and sp[0..7] are the lane's inputs and scales, dst[0..7] its xhat.  The
+// whole Hadamard runs on DPP exchanges inside the row, and every lane moves
+// 16-byte words (VEC; callers whose x, scales or output are not 16-byte
+// aligned take the element-wise loads instead).  All 16 lanes of the row
+// must be active; `live` = false computes without storing.
+template <bool VEC>
+__device__ __forceinline__ void prologue8(const void* x, int x_dtype, size_t xe,
+                                          const uint16_t* sp, uint16_t* dst, bool live,
+                                          int lane) {
+  float a[8], sv[8];
+  load8<VEC>(x, x_dtype, xe, sp, a, sv);
+  finish8<VEC>(a, sv, dst, live, lane);
 }
 
 // KW waves share each column pair and split the workgroup's K-range between

@@ -9,12 +9,19 @@ Protocol:
   ceil(2 GiB / trellis bytes) device copies; consecutive steps rotate over the
   copies so every launch streams its weights from HBM, not from the 256 MB
   Infinity Cache;
-* the timed steps run as HIP graph replays on one stream, bracketed by
-  torch.cuda.synchronize() and HIP events recorded on that stream;
+* the timed steps run as HIP graph replays on one stream, in --windows (21)
+  windows of exactly --steps steps, each bracketed by torch.cuda.synchronize()
+  and HIP events recorded on that stream behind a short device spin (so the
+  events time the GPU's work, not the CPU's submission); the headline is the
+  median window (min / mean / max under "timing");
 * value = algorithmic bytes per step / time per step, bytes =
   in*out*K/8 + M*in*2 + M*out*2 + in*2 + out*2 (each tensor once);
-* cpu_baseline: the C oracle (oracle/, decode-at-use GEMV, OpenMP) on the same
-  shape on this host's cores, over a bounded sample;
+* roofline.valu_ceiling: the QMV's measured SQ_INSTS_VALU as an issue-bound
+  time (profiles/traffic.json), i.e. how far the decode arithmetic alone keeps
+  the kernel from the HBM roofline;
+* cpu_baseline: the C oracle (oracle/, decode-at-use GEMV, OpenMP) on this
+  host over bounded samples of the headline and of C1, C2 (M 16/128), one C3
+  layer, C4 and C5 (M 4/16), with this process's CPU share and one thread;
 * ceilings (reference only): this GPU's measured streaming-read bandwidth over
   4 GiB and a dense fp16 GEMM (M=512) / GEMV (M=1) at the same shape through
   torch's library kernels, next to the spec peaks the roofline fractions use.
@@ -66,8 +73,13 @@ def make_rotation(n_in, n_out, k, cb, seed, max_copies=None):
     return lins, weights
 
 
-def time_steps(lins, x, steps, warmup, ws):
-    """Run warmup + timed steps as graph replays; returns (ms per step, y)."""
+def time_steps(lins, x, steps, warmup, ws, windows=1):
+    """Run warmup steps, then `windows` timed windows of exactly `steps` steps
+    each, as graph replays on one stream.  Each window is bracketed by HIP
+    events recorded on that stream behind a short device spin, so the CPU has
+    queued the whole window before its start event runs and the events time the
+    GPU's work only.  Returns (median ms per step over the windows, y,
+    per-window ms per step)."""
     import torch
 
     n = len(lins)
@@ -86,69 +98,236 @@ def time_steps(lins, x, steps, warmup, ws):
         lin.forward(x, workspace=ws)
     torch.cuda.synchronize()
     full, outs = capture(n)
-    rest = steps % n
-    part = capture(rest)[0] if rest else None
+    parts = {}
 
     def run(count):
         for _ in range(count // n):
             full.replay()
         if count % n:
-            (part if count % n == rest else capture(count % n)[0]).replay()
+            if count % n not in parts:
+                parts[count % n] = capture(count % n)[0]
+            parts[count % n].replay()
 
-    run(warmup)
+    run(max(1, warmup))
+    if steps % n:
+        run(steps % n)  # captures the window's partial graph outside the timed region
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record(stream)
-    run(steps)
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
-    return ms, outs[0]
+    per = []
+    for _ in range(windows):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(200000)  # ~100 us of device spin: the window is queued behind it
+        start.record(stream)
+        run(steps)
+        end.record(stream)
+        torch.cuda.synchronize()
+        per.append(start.elapsed_time(end) / steps)
+    med = sorted(per)[len(per) // 2]
+    return med, outs[0], per
 
 
-def measured_traffic(workload):
-    """HBM bytes per launch of the dominant kernel for `workload`, as measured
-    by rocprofv3 FETCH_SIZE + WRITE_SIZE (scaled by a known-size copy) and
-    recorded in profiles/traffic.json; None when not measured."""
-    path = ROOT / "profiles" / "traffic.json"
+def windowed(replay, reps, steps_per_rep, windows):
+    """Median ms per step over `windows` windows of `reps` calls of replay()
+    (each call `steps_per_rep` steps on the current stream), every window
+    bracketed by HIP events behind a short device spin as in time_steps.
+    Returns (median ms per step, per-window ms per step)."""
+    import torch
+
+    stream = torch.cuda.current_stream()
+    per = []
+    for _ in range(windows):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(200000)
+        start.record(stream)
+        for _ in range(reps):
+            replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        per.append(start.elapsed_time(end) / (reps * steps_per_rep))
+    return sorted(per)[len(per) // 2], per
+
+
+def window_stats(per):
+    """min / mean / max of per-window ms per step, rounded for the JSON line."""
+    return {"windows": len(per), "ms_min": round(min(per), 6),
+            "ms_mean": round(sum(per) / len(per), 6), "ms_max": round(max(per), 6)}
+
+
+def _traffic_entry(workload):
     try:
-        return json.loads(path.read_text())[workload]["hbm_bytes_per_launch"]
+        return json.loads((ROOT / "profiles" / "traffic.json").read_text())[workload]
     except (OSError, KeyError, ValueError):
         return None
 
 
-def cpu_baseline(n_in, n_out, k, cb, rows, budget_s=12.0):
+def measured_traffic(workload):
+    """HBM bytes per step of `workload` (summed over its kernels), as measured
+    by rocprofv3 FETCH_SIZE + WRITE_SIZE (scaled by a known-size copy) and
+    recorded in profiles/traffic.json; None when not measured."""
+    e = _traffic_entry(workload)
+    return e.get("hbm_bytes_per_launch") if e else None
+
+
+def valu_ceiling(workload, ms):
+    """The VALU issue bound of the dominant kernel: its measured SQ_INSTS_VALU
+    (wave instructions per launch, profiles/traffic.json) x 4 cycles (a wave64
+    VALU instruction on a 16-lane SIMD) / 1024 SIMDs / 2.4 GHz, against the
+    measured step time; None when not measured."""
+    e = _traffic_entry(workload)
+    if not e or "valu_insts_per_launch" not in e:
+        return None
+    us = e["valu_insts_per_launch"] * 4 / (1024 * 2.4e9) * 1e6
+    return {"valu_insts": e["valu_insts_per_launch"], "us": round(us, 3),
+            "frac": round(us / (ms * 1e3), 4),
+            "note": "SQ_INSTS_VALU x 4 cycles / 1024 SIMDs / 2.4 GHz (issue-bound time at peak clock)"}
+
+
+def cpu_threads():
+    """Threads of the CPU legs: this process's CPU share (its affinity mask),
+    capped by OMP_NUM_THREADS where the host sets it (the GPU boxes set it to
+    their per-GPU share of 16)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def _cpu_time(fn, budget_s, max_calls=1000, warm=False):
+    """Seconds per call of fn() (after one untimed call if `warm`), repeated
+    until budget_s has passed (at least one timed call)."""
+    if warm:
+        fn()
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or calls >= max_calls:
+            return el / calls, calls
+
+
+def cpu_baseline(n_in, n_out, k, cb, rows, scale=1.0):
+    """The oracle (oracle/: the C restatement of codec.rs + ref/forward.py,
+    decode at use, OpenMP) timed on this host over a bounded sample of every
+    configuration of the measurement plan, with the GPU legs' algorithmic bytes
+    and flops: the headline (in x out, K, rows) at all threads of the process's
+    CPU share and at one thread, C1, C2 at M 16 and 128 (both shapes, K 3/4/5),
+    one C3 layer (its 7 linears), C4 (the MoE block) and C5 (one layer at M 4
+    and 16, K 2 and 4).  `scale` multiplies every leg's time budget."""
     import numpy as np
 
     import oracle
     from mlxl3_amd import synth
 
-    tr, suh, svh, _ = synth.linear_layer(1, 0, n_in, n_out, k)
+    threads = cpu_threads()
+    t_start = time.perf_counter()
+
+    def lin(seed, tid, i, o, kk, c=0):
+        return synth.linear_layer(seed, tid, i, o, kk)[:3] + (kk, c)
+
+    def run_lin(L, x, th):
+        tr, su, sv, kk, c = L
+        return oracle.forward(x, tr, su, sv, kk, c, mode=1, threads=th)
+
+    legs = {}
+
+    def leg(name, fn, budget, nbytes, flops, warm=False, factor=1.0):
+        sec, calls = _cpu_time(fn, budget * scale, warm=warm)
+        sec *= factor  # a sample of the workload scaled to all of it
+        legs[name] = {"ms_per_call": round(sec * 1e3, 3), "calls": calls,
+                      "gbs": round(nbytes / sec / 1e9, 3), "gflops": round(flops / sec / 1e9, 3)}
+        return sec, calls
+
+    # headline, all threads and one thread (the warm call builds the codebook
+    # tables once for every leg)
+    L = lin(1, 0, n_in, n_out, k, cb)
     x = synth.activations(1, 0, rows, n_in)
-    threads = min(os.cpu_count() or 1, 16)
-    oracle.forward(x, tr, suh, svh, k, cb, mode=1, threads=threads)  # table build, warm caches
-    calls, t0 = 0, time.perf_counter()
-    while True:
-        oracle.forward(x, tr, suh, svh, k, cb, mode=1, threads=threads)
-        calls += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or calls >= 200:
-            break
-    per_call = el / calls
-    gbs = alg_bytes(n_in, n_out, k, rows) / per_call / 1e9
+    hb, hf = alg_bytes(n_in, n_out, k, rows), 2.0 * rows * n_in * n_out
+    sec, calls = leg("ns", lambda: run_lin(L, x, threads), 5.0, hb, hf, warm=True)
+    sec1, calls1 = _cpu_time(lambda: run_lin(L, x, 1), 3.0 * scale)
+    del L
+    # C1
+    L = lin(1, 0, 4096, 4096, 4)
+    x1 = synth.activations(1, 0, 1, 4096)
+    leg("c1_qmv_4096x4096_k4_m1", lambda: run_lin(L, x1, threads), 1.0,
+        alg_bytes(4096, 4096, 4, 1), 2.0 * 4096 * 4096)
+    # C2 at M 16 and 128
+    for i_, o_ in ((4096, 14336), (14336, 4096)):
+        for kk in (3, 4, 5):
+            L = lin(2, 0, i_, o_, kk)
+            for m in (16, 128):
+                xm = synth.activations(2, m, m, i_, outlier_frac=0.01)
+                leg(f"c2_{i_}x{o_}_k{kk}_m{m}", lambda: run_lin(L, xm, threads), 0.3,
+                    alg_bytes(i_, o_, kk, m), 2.0 * m * i_ * o_)
+    del L
+    # C3: one dense layer's 7 linears at batch 1
+    hid, inter, kv = 4096, 14336, 1024
+    c3 = [lin(3, 3000 + 10 * t, i_, o_, 4)
+          for t, (i_, o_) in enumerate(((hid, hid), (hid, kv), (hid, kv), (hid, hid),
+                                        (hid, inter), (hid, inter), (inter, hid)))]
+    xa, xi = synth.activations(3, 1, 1, hid), synth.activations(3, 2, 1, inter)
+
+    def c3_layer():
+        for L_ in c3:
+            run_lin(L_, xi if L_[0].shape[0] * 16 == inter else xa, threads)
+
+    leg("c3_llama_layer_k4_m1", c3_layer, 2.0,
+        sum(alg_bytes(L_[0].shape[0] * 16, L_[0].shape[1] * 16, 4, 1) for L_ in c3),
+        sum(2.0 * L_[0].shape[0] * 16 * L_[0].shape[1] * 16 for L_ in c3))
+    del c3
+    # C4: the MoE block (256 tokens, top-8 of 128 experts, 2048 -> 768, K=3),
+    # timed on its first 32 tokens and scaled by 8: the oracle decodes each
+    # routed slot's expert tiles at use, so its work is linear in the slots
+    ein, eh, E, top, k4, r4, r4s = 2048, 768, 128, 8, 3, 256, 32
+    bank = synth.moe_layer(4, 500, ein, eh, E, k4)
+    x4 = synth.activations(4, 510, r4, ein)[:r4s]
+    sel, sc = synth.moe_routes(4, 520, r4, E, top)
+    sel, sc = sel[:r4s], sc[:r4s]
+    bank_bytes = (bank[0].size + bank[3].size) * 2
+    leg("c4_moe_2048x768_e128_top8_rows256_k3",
+        lambda: oracle.moe_forward(x4, sel, sc, *bank, k4, 0, threads=threads), 1.0,
+        bank_bytes + r4 * ein * 2 * 2 + (E * 2 * ein + E * 2 * eh + E * eh + E * ein) * 2,
+        2.0 * r4 * top * 3 * ein * eh, factor=r4 / r4s)
+    legs["c4_moe_2048x768_e128_top8_rows256_k3"]["sample"] = (
+        f"first {r4s} of {r4} tokens, time x {r4 // r4s}")
+    del bank
+    # C5: one 27B-class layer (7 linears, MCG) at M 4 and 16, K 2 and 4
+    hid, inter = 5120, 27648
+    for kk in (2, 4):
+        c5 = [lin(5, 5000 + 10 * t, i_, o_, kk, 1)
+              for t, (i_, o_) in enumerate(((hid, hid), (hid, kv), (hid, kv), (hid, hid),
+                                            (hid, inter), (hid, inter), (inter, hid)))]
+        for m in (4, 16):
+            xa5, xi5 = synth.activations(5, m, m, hid), synth.activations(5, 100 + m, m, inter)
+
+            def c5_layer():
+                for L_ in c5:
+                    run_lin(L_, xi5 if L_[0].shape[0] * 16 == inter else xa5, threads)
+
+            leg(f"c5_layer_mcg_k{kk}_m{m}", c5_layer, 1.0,
+                sum(alg_bytes(L_[0].shape[0] * 16, L_[0].shape[1] * 16, kk, m) for L_ in c5),
+                sum(2.0 * m * L_[0].shape[0] * 16 * L_[0].shape[1] * 16 for L_ in c5))
+        del c5
+    wall = time.perf_counter() - t_start
+    gbs = hb / sec / 1e9
     return {
         "value": round(gbs, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{calls} calls of the C oracle forward (engine semantics, decode-at-use, "
-                  f"OpenMP {threads} threads) at in={n_in} out={n_out} K={k} rows={rows}; "
-                  f"{per_call * 1e3:.2f} ms/call",
+        "host_cpus": os.cpu_count(),
+        "threads_1": {"value": round(hb / sec1 / 1e9, 3), "unit": "GB/s",
+                      "ms_per_call": round(sec1 * 1e3, 3), "calls": calls1},
+        "sample": (f"the C oracle (engine semantics, decode at use, OpenMP over {threads} "
+                   f"threads = this process's CPU share; {os.cpu_count()} CPUs on the host) on "
+                   f"the headline linear in={n_in} out={n_out} K={k} rows={rows}: {calls} calls, "
+                   f"{sec * 1e3:.2f} ms/call; plus the legs below (each a bounded sample of whole "
+                   f"calls, same algorithmic bytes and flops as the GPU legs); {wall:.0f} s in all"),
+        "legs": legs,
     }
 
 
-def moe_leg(steps, warmup):
+def moe_leg(steps, warmup, windows=21):
     """C4 expert block (hidden 2048, 128 experts x 768, top-8, 256 tokens, K=3
     3INST): one SwitchGLU forward per step through the C ABI, graph replays
     rotating over copies of the 226 MB bank so each step streams it from HBM."""
@@ -183,8 +362,6 @@ def moe_leg(steps, warmup):
     lib = mlxl3_amd.load_library()
     nws = int(lib.exl3_moe_workspace_bytes(moes[0]._handle, rows))
     ws = torch.zeros(nws + 4096, dtype=torch.uint8, device="cuda")
-    stream = torch.cuda.current_stream()
-
     def call(m):  # on the current stream (the capture stream inside torch.cuda.graph)
         rc = lib.exl3_moe_forward(m._handle, x.data_ptr(), 9, rows, sel.data_ptr(), sc.data_ptr(),
                                   9, y.data_ptr(), ws.data_ptr(), ws.numel(),
@@ -204,13 +381,7 @@ def moe_leg(steps, warmup):
         g.replay()
     torch.cuda.synchronize()
     reps = max(1, math.ceil(steps / len(moes)))
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(reps):
-        g.replay()
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / (reps * len(moes))
+    ms, per = windowed(g.replay, reps, len(moes), windows)
     nbytes = bank_bytes + rows * in_f * 2 * 2 + (experts * 2 * in_f + experts * 2 * hidden
                                                   + experts * hidden + experts * in_f) * 2
     gbs = nbytes / (ms * 1e-3) / 1e9
@@ -218,6 +389,7 @@ def moe_leg(steps, warmup):
         "workload": f"moe_switchglu_{in_f}x{hidden}_e{experts}_top{top_k}_rows{rows}_k{k}_3inst",
         "ms_per_step": round(ms, 6),
         "steps": reps * len(moes),
+        "timing": window_stats(per),
         "bank_copies_rotated": copies,
         "bytes_per_step": nbytes,
         "gflop_per_step": round(2.0 * rows * top_k * 3 * in_f * hidden / 1e9, 3),
@@ -233,7 +405,7 @@ def moe_leg(steps, warmup):
     }
 
 
-def mlp_leg(steps, warmup, rows=1):
+def mlp_leg(steps, warmup, rows=1, windows=21):
     """Dense SwiGLU MLP of a decoder layer at the north-star shape (gate/up
     4096 -> 14336, down 14336 -> 4096, K=4 3INST): exl3_mlp_forward (the SwiGLU
     in the gate/up epilogue) against the unfused composition of the reference
@@ -310,14 +482,8 @@ def mlp_leg(steps, warmup, rows=1):
             graph.replay()
         torch.cuda.synchronize()
         reps = max(1, math.ceil(steps / copies))
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        stream = torch.cuda.current_stream()
-        start.record(stream)
-        for _ in range(reps):
-            graph.replay()
-        end.record(stream)
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / (reps * copies), reps * copies
+        ms, _ = windowed(graph.replay, reps, copies, windows)
+        return ms, reps * copies
 
     ms_fused, n = timed(fused)
     y_fused = y.clone()
@@ -325,6 +491,14 @@ def mlp_leg(steps, warmup, rows=1):
     assert torch.equal(y_fused.view(torch.int16), y.view(torch.int16)), "fused != unfused"
     nbytes = per_copy + (2 * in_f + 2 * hidden + hidden + in_f) * 2 + rows * in_f * 2 * 2
     gbs = nbytes / (ms_fused * 1e-3) / 1e9
+    flops = 2.0 * rows * 3 * in_f * hidden
+    tflops = flops / (ms_fused * 1e-3) / 1e12
+    if flops / nbytes >= 315:  # above the ridge point (2516.6 TFLOP/s / 8 TB/s): MFMA-bound
+        roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP16_MFMA_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4), "traffic": None}
+    else:
+        roof = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
     return {
         "workload": f"mlp_swiglu_{in_f}x{hidden}_k{k}_3inst_m{rows}",
         "ms_per_step": round(ms_fused, 6),
@@ -332,8 +506,8 @@ def mlp_leg(steps, warmup, rows=1):
         "steps": n,
         "weight_copies_rotated": copies,
         "bytes_per_step": nbytes,
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "gflop_per_step": round(flops / 1e9, 3),
+        "roofline": roof,
     }
 
 
@@ -609,6 +783,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--windows", type=int, default=21,
+                    help="timed windows of `steps` steps each; the headline is their median")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-qmm", action="store_true", help="skip the QMM M=512 leg")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE SwitchGLU leg")
@@ -652,7 +828,7 @@ def main():
     ws = torch.zeros(max(l.workspace_bytes(max(rows, 512)) for l in lins[:1]) + 4096,
                      dtype=torch.uint8, device="cuda")
     torch.cuda.synchronize()
-    ms, _ = time_steps(lins, x, args.steps, args.warmup, ws)
+    ms, _, per = time_steps(lins, x, args.steps, args.warmup, ws, windows=args.windows)
     nbytes = alg_bytes(n_in, n_out, k, rows)
     gbs = nbytes / (ms * 1e-3) / 1e9
 
@@ -674,6 +850,9 @@ def main():
             "in": n_in, "out": n_out, "k": k, "codebook": cb, "rows": rows,
             "weight_copies_rotated": len(lins), "bytes_per_step": nbytes,
         },
+        "timing": dict(window_stats(per), steps_per_window=args.steps,
+                       protocol="median over windows of exactly `steps` graph-replayed steps, "
+                                "each bracketed by HIP events on the launch stream"),
         "roofline": {
             "bound": "hbm",
             "achieved": round(gbs, 2),
@@ -681,6 +860,8 @@ def main():
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(f"qmv_{n_in}x{n_out}_k{k}_{['3inst', 'mcg', 'mul1'][cb]}_m{rows}"),
+            "valu_ceiling": valu_ceiling(
+                f"qmv_{n_in}x{n_out}_k{k}_{['3inst', 'mcg', 'mul1'][cb]}_m{rows}", ms),
         },
     }
     del lins, _w
@@ -692,13 +873,15 @@ def main():
         xq = torch.from_numpy(synth.activations(2, 1, m, n_in, outlier_frac=0.01)).cuda()
         wsq = torch.zeros(qlins[0].workspace_bytes(m) + 4096, dtype=torch.uint8, device="cuda")
         qsteps = max(16, args.steps // 20)
-        qms, _ = time_steps(qlins, xq, qsteps, max(4, args.warmup // 20), wsq)
+        qms, _, qper = time_steps(qlins, xq, qsteps, max(4, args.warmup // 20), wsq,
+                                  windows=args.windows)
         tflops = 2.0 * m * n_in * n_out / (qms * 1e-3) / 1e12
         result["qmm"] = {
             "workload": f"qmm_{n_in}x{n_out}_k{k}_m{m}",
             "tflops": round(tflops, 2),
             "ms_per_step": round(qms, 6),
             "steps": qsteps,
+            "timing": window_stats(qper),
             "roofline": {
                 "bound": "mfma",
                 "achieved": round(tflops, 2),

@@ -18,15 +18,21 @@
 //   mlx-switch                        GPU Exl3SwitchGlu forward (bank in the request)
 //   mlx-checkpoint-switch/-group      the same on projections of a checkpoint
 //   mlx-swiglu-prepare, mlx-expert-reduce   the SwitchGLU glue steps
+//   metal-checkpoint-linear, metal-exl3-linear, metal-checkpoint-expert,
+//   metal-checkpoint-group            checkpoint projections, dense experts and
+//                                     projection bundles under the direct-Metal
+//                                     path's geometry and input checks
 // Any other op answers "unknown or unavailable codec operation <op>", as a
 // reference build without the feature does.  The GPU is initialised on the
 // first request that needs it.
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <iostream>
+#include <memory>
 #include <sstream>
 #include <string>
 #include <vector>
@@ -359,6 +365,168 @@ std::vector<uint16_t> moe_run(exl3_moe* h, const std::vector<uint16_t>& xv,
   return y.read<uint16_t>(xv.size());
 }
 
+// CodecRequest::input_view (main.rs:261-270) with TensorStorage::matrix
+// (gpu/view.rs:30-41): the x_layout view of x (f16 bits) or of x_f32 (f32,
+// rounded to f16 as the preparation kernels cast it), gathered row-major.
+// Views of more than 2^32 - 1 elements (a zero stride lets a view exceed its
+// storage) fail with `too_large` before anything is gathered.
+std::vector<uint16_t> gather_view(const Request& r, uint32_t* rows, uint32_t* cols,
+                                  const char* too_large) {
+  if (!r.x_layout.given) bail("missing input matrix layout");
+  if (r.has_x_f32 && !r.x.empty()) bail("conflicting input buffer dtypes");
+  if (!layout_fits(r.x_layout, r.has_x_f32 ? r.x_f32.size() : r.x.size()))
+    bail("matrix view outside initialized storage");
+  const Request::Layout& l = r.x_layout;
+  *rows = l.shape[0];
+  *cols = l.shape[1];
+  if ((uint64_t)l.shape[0] * l.shape[1] > UINT32_MAX) bail(too_large);
+  std::vector<uint16_t> out((size_t)l.shape[0] * l.shape[1]);
+  for (uint64_t i = 0; i < l.shape[0]; ++i)
+    for (uint64_t j = 0; j < l.shape[1]; ++j) {
+      const int64_t e = l.offset + (int64_t)i * l.strides[0] + (int64_t)j * l.strides[1];
+      out[i * l.shape[1] + j] = r.has_x_f32 ? __builtin_bit_cast(uint16_t, (_Float16)r.x_f32[e])
+                                            : r.x[e];
+    }
+  return out;
+}
+
+// The direct-Metal projection path's geometry, FlashProjection::load /
+// load_exl3 (gpu/projection.rs:134-205): its split policy decides which
+// projections it accepts, so the checks run before anything is uploaded.
+struct FlashGeometry {
+  uint32_t input = 0, output = 0, splits = 1;
+  int k = 0, cb = 0;
+  bool generic = false;
+};
+
+// flash_support::reference_splits (flash_support.rs:815-823)
+uint32_t reference_splits(uint32_t input_tiles, uint32_t output_tiles) {
+  uint32_t s = 1;
+  while ((uint64_t)output_tiles * s < 8192 && (uint64_t)input_tiles / ((uint64_t)s * 2) >= 128)
+    s *= 2;
+  return s;
+}
+// contracts::exl3_projection_splits (contracts.rs:1995-2011); 0 for None
+uint32_t exl3_projection_splits(uint32_t input, uint32_t output) {
+  if (input == 0 || output == 0 || input % 128 || output % 128) return 0;
+  const uint32_t it = input / 16, ot = output / 16;
+  const uint32_t target = ot <= 64 ? std::max(ot / 2, 32u) : std::min(std::max(ot, 32u), 256u);
+  uint32_t s = 1;
+  while (it / s / 2 >= target) s *= 2;
+  return s;
+}
+// contracts::exl3_projection_extents / projection_extents
+// (contracts.rs:2014-2027, :2082-2101) for a batch of `batch` rows
+bool flash_extents(const FlashGeometry& g, uint64_t batch) {
+  if (batch == 0) return false;
+  if (g.generic) {
+    if (!exl3_projection_splits(g.input, g.output)) return false;
+    if (g.splits == 0 || (g.splits & (g.splits - 1)) || g.splits > g.input / 128) return false;
+  } else if (g.input > INT32_MAX || g.output > INT32_MAX || g.input % 128 || g.output % 128 ||
+             (g.splits != 1 && g.splits != 2)) {
+    return false;
+  }
+  const uint64_t count = batch * g.output;
+  return batch * g.input <= UINT32_MAX && count <= UINT32_MAX && count * g.splits <= UINT32_MAX;
+}
+
+FlashGeometry flash_geometry(const exl3_checkpoint* c, const std::string& name, bool exl3_loader) {
+  const bool flash_ckpt = std::strcmp(exl3_checkpoint_model_type(c), "qwen4_exp") == 0;
+  if (!exl3_loader && !flash_ckpt) bail("requires a Flash reference checkpoint");
+  FlashGeometry g;
+  g.generic = exl3_loader && !flash_ckpt;
+  exl3_tensor_info t;
+  if (exl3_checkpoint_tensor(c, (name + ".trellis").c_str(), &t) != EXL3_OK)
+    bail("missing projection trellis");
+  if (t.ndim != 3) bail("invalid trellis rank");
+  if ((std::strcmp(t.dtype, "I16") != 0 && std::strcmp(t.dtype, "U16") != 0) || t.shape[2] % 16)
+    bail("invalid packed trellis");
+  if (t.shape[0] > UINT32_MAX / 16) bail("input width overflow");
+  if (t.shape[1] > UINT32_MAX / 16) bail("output width overflow");
+  g.input = (uint32_t)(t.shape[0] * 16);
+  g.output = (uint32_t)(t.shape[1] * 16);
+  const int64_t k = t.shape[2] / 16;
+  // contracts::qmv_words (contracts.rs:1875-1886), as a u32 word count
+  if (g.input == 0 || g.output == 0 || k < 1 || k > 8 ||
+      (uint64_t)t.shape[0] * t.shape[1] * 16 * k > UINT32_MAX)
+    bail("invalid packed geometry or index overflow");
+  g.k = (int)k;
+  exl3_tensor_info m;
+  g.cb = exl3_checkpoint_tensor(c, (name + ".mul1").c_str(), &m) == EXL3_OK  ? 2
+         : exl3_checkpoint_tensor(c, (name + ".mcg").c_str(), &m) == EXL3_OK ? 1
+                                                                             : 0;
+  const bool mtp_hidden = !g.generic && name == "mtp.fc_hidden";
+  if (mtp_hidden && (g.input != 2560 || g.output != 2560 || g.k == 7))
+    bail("unsupported MTP hidden projection");
+  if (mtp_hidden) {
+    g.splits = 2;
+  } else if (g.k == 7) {
+    g.splits = 1;
+  } else if (g.generic) {
+    g.splits = exl3_projection_splits(g.input, g.output);
+    if (!g.splits) bail("invalid EXL3 dimensions");
+  } else {
+    g.splits = reference_splits(g.input / 16, g.output / 16);
+  }
+  if (!flash_extents(g, 1)) bail("unsupported projection geometry/split count");
+  return g;
+}
+
+struct LinearGuard {
+  exl3_linear* h = nullptr;
+  ~LinearGuard() { exl3_linear_destroy(h); }
+};
+
+// y[rows][out] (f16) of one loaded projection on f16 rows
+std::vector<uint16_t> linear_run(const exl3_linear* h, const std::vector<uint16_t>& xv,
+                                 int64_t rows) {
+  const int64_t out = exl3_linear_out_features(h);
+  DeviceBuffer x(xv), y((size_t)rows * out * 2);
+  const size_t wb = exl3_linear_workspace_bytes(h, rows);
+  DeviceBuffer ws(wb);
+  zero_workspace(ws);
+  lib_check(exl3_linear_forward(h, x.p, EXL3_F16, rows, y.p, EXL3_F16, ws.p, wb, nullptr));
+  return y.read<uint16_t>((size_t)rows * out);
+}
+
+// {"grouped": .., "outputs": [..]} of loaded projections on one f16 row: one
+// exl3_group_forward launch for a compatible bundle of at most 8 projections
+// (Exl3Group::forward), else each projection's own forward.  The two can
+// differ in the last bit where the group's wider output changes the split-K
+// order, so both bundle ops take the same route for the same bundle.
+std::string group_outputs(const std::vector<exl3_linear*>& parts, bool grouped,
+                          const std::vector<uint16_t>& xv) {
+  const bool one_launch = grouped && parts.size() <= 8;
+  DeviceBuffer x(xv);
+  std::vector<std::unique_ptr<DeviceBuffer>> ys;
+  std::vector<void*> yp;
+  for (auto* h : parts) {
+    ys.emplace_back(new DeviceBuffer((size_t)exl3_linear_out_features(h) * 2));
+    yp.push_back(ys.back()->p);
+  }
+  if (one_launch) {
+    const size_t wb = exl3_group_workspace_bytes(parts.data(), (int)parts.size(), 1);
+    DeviceBuffer ws(wb);
+    zero_workspace(ws);
+    lib_check(exl3_group_forward(parts.data(), (int)parts.size(), x.p, EXL3_F16, 1, yp.data(),
+                                 ws.p, wb, nullptr));
+  } else {
+    for (size_t i = 0; i < parts.size(); ++i) {
+      const size_t wb = exl3_linear_workspace_bytes(parts[i], 1);
+      DeviceBuffer ws(wb);
+      zero_workspace(ws);
+      lib_check(exl3_linear_forward(parts[i], x.p, EXL3_F16, 1, yp[i], EXL3_F16, ws.p, wb,
+                                    nullptr));
+    }
+  }
+  std::string out = std::string("{\"grouped\":") + (grouped ? "true" : "false") + ",\"outputs\":[";
+  for (size_t i = 0; i < ys.size(); ++i) {
+    if (i) out += ',';
+    out += json_list(ys[i]->read<uint16_t>(exl3_linear_out_features(parts[i])));
+  }
+  return out + "]}";
+}
+
 // ---- operations ------------------------------------------------------------
 std::string run(const Request& r) {
   if (r.mode > 2) bail("invalid EXL3 codebook " + std::to_string(r.mode));
@@ -424,30 +592,24 @@ std::string run(const Request& r) {
     return json_list(out.read<uint16_t>((size_t)tiles * 16 * r.k));
   }
   if (r.op == "metal-prepare-view") {  // main.rs:1294-1302, gpu/view.rs:181-195, :257-272
-    // input_view (main.rs:261-270), TensorStorage::matrix (gpu/view.rs:30-41)
+    uint32_t rows = 0, cols = 0;
     if (!r.x_layout.given) bail("missing input matrix layout");
     if (r.has_x_f32 && !r.x.empty()) bail("conflicting input buffer dtypes");
     if (!layout_fits(r.x_layout, r.has_x_f32 ? r.x_f32.size() : r.x.size()))
       bail("matrix view outside initialized storage");
     if (!r.scale_layout.given) bail("missing scale matrix layout");
     if (!layout_fits(r.scale_layout, r.data.size())) bail("matrix view outside initialized storage");
-    const Request::Layout &xl = r.x_layout, &sl = r.scale_layout;
-    if (xl.shape[0] != sl.shape[0] || xl.shape[1] != sl.shape[1])
+    const Request::Layout& sl = r.scale_layout;
+    if (r.x_layout.shape[0] != sl.shape[0] || r.x_layout.shape[1] != sl.shape[1])
       bail("invalid H128 view shape or scale dtype");
-    const uint64_t rows = xl.shape[0], cols = xl.shape[1], n = rows * cols;
-    if (n > UINT32_MAX) bail("H128 view size overflow");
+    const std::vector<uint16_t> xs = gather_view(r, &rows, &cols, "H128 view size overflow");
+    const uint64_t n = (uint64_t)rows * cols;
     if (cols == 0 || cols % 128) bail("H128 view width must be positive and 128-aligned");
     if (n == 0) return "[]";
-    // gather both views into rows x cols (x as f16: astype rounds to nearest even)
-    std::vector<uint16_t> xs(n), ss(n);
+    std::vector<uint16_t> ss(n);
     for (uint64_t i = 0; i < rows; ++i)
-      for (uint64_t j = 0; j < cols; ++j) {
-        const int64_t xi = xl.offset + (int64_t)i * xl.strides[0] + (int64_t)j * xl.strides[1];
-        const int64_t si = sl.offset + (int64_t)i * sl.strides[0] + (int64_t)j * sl.strides[1];
-        xs[i * cols + j] = r.has_x_f32 ? __builtin_bit_cast(uint16_t, (_Float16)r.x_f32[xi])
-                                       : r.x[xi];
-        ss[i * cols + j] = r.data[si];
-      }
+      for (uint64_t j = 0; j < cols; ++j)
+        ss[i * cols + j] = r.data[sl.offset + (int64_t)i * sl.strides[0] + (int64_t)j * sl.strides[1]];
     DeviceBuffer x(xs), sc(ss), o(n * 2);
     lib_check(exl3_prepare128(x.as<uint16_t>(), (int64_t)n, (int)cols, sc.as<uint16_t>(),
                               (int64_t)n, o.as<uint16_t>(), nullptr));
@@ -676,41 +838,100 @@ std::string run(const Request& r) {
       lib_check(exl3_linear_load(c.c, p.c_str(), &h));
       parts.push_back(h);
     }
-    DeviceBuffer x(r.x);
-    std::vector<DeviceBuffer*> ys;
-    struct YCleanup {
-      std::vector<DeviceBuffer*>& ys;
-      ~YCleanup() {
-        for (auto* b : ys) delete b;
-      }
-    } ycleanup{ys};
-    std::vector<void*> yp;
-    for (auto* h : parts) {
-      ys.push_back(new DeviceBuffer((size_t)exl3_linear_out_features(h) * 2));
-      yp.push_back(ys.back()->p);
+    return group_outputs(parts, grouped, r.x);
+  }
+  // The direct-Metal projection ops (main.rs:1304-1337): a projection of a
+  // checkpoint (FlashProjection::load for a Flash reference checkpoint, load_exl3
+  // for any) or a dense expert (FlashExpert: down(swiglu(gate x, up x))) on f16
+  // rows or on a strided f16/f32 view, f16 out.  The geometry and input checks
+  // are the direct path's (gpu/projection.rs:134-333, :1577-1608); the
+  // arithmetic is this library's Exl3Linear, which that path matches bit for bit.
+  if (r.op == "metal-checkpoint-linear" || r.op == "metal-exl3-linear" ||
+      r.op == "metal-checkpoint-expert") {
+    const bool view = r.x_layout.given || r.has_x_f32;
+    const char* view_batch = "invalid Flash projection view batch or index overflow";
+    std::vector<uint16_t> xs;
+    uint32_t vrows = 0, vcols = 0;
+    if (view) xs = gather_view(r, &vrows, &vcols, view_batch);
+    CheckpointGuard c;
+    lib_check(exl3_checkpoint_open(r.path.c_str(), &c.c));
+    const bool expert = r.op == "metal-checkpoint-expert";
+    const FlashGeometry g = flash_geometry(
+        c.c, expert ? r.prefix + ".gate_proj" : r.prefix, r.op == "metal-exl3-linear");
+    if (expert) {
+      const FlashGeometry u = flash_geometry(c.c, r.prefix + ".up_proj", false);
+      const FlashGeometry d = flash_geometry(c.c, r.prefix + ".down_proj", false);
+      // contracts::compatible_flash_expert
+      if (!(u.input == g.input && u.output == g.output && d.input == g.output &&
+            d.output == g.input))
+        bail("incompatible Flash expert projection geometry");
     }
-    if (grouped && parts.size() <= 8) {
-      const size_t wb = exl3_group_workspace_bytes(parts.data(), (int)parts.size(), 1);
-      DeviceBuffer ws(wb);
-      zero_workspace(ws);
-      lib_check(exl3_group_forward(parts.data(), (int)parts.size(), x.p, EXL3_F16, 1, yp.data(),
-                                   ws.p, wb, nullptr));
+    uint64_t rows;
+    if (view) {
+      if (vcols != g.input) bail("invalid projection view width");
+      rows = vrows;
+      if (!flash_extents(g, rows)) bail(view_batch);
     } else {
-      for (size_t i = 0; i < parts.size(); ++i) {
-        const size_t wb = exl3_linear_workspace_bytes(parts[i], 1);
-        DeviceBuffer ws(wb);
-        zero_workspace(ws);
-        lib_check(exl3_linear_forward(parts[i], x.p, EXL3_F16, 1, yp[i], EXL3_F16, ws.p, wb,
-                                      nullptr));
+      if (r.x.size() % g.input) bail("input is not a complete row");
+      rows = r.x.size() / g.input;
+      if (!flash_extents(g, rows)) bail("invalid Flash projection batch or index overflow");
+      xs = r.x;
+    }
+    if (!expert) {
+      LinearGuard h;
+      lib_check(exl3_linear_load(c.c, r.prefix.c_str(), &h.h));
+      return json_list(linear_run(h.h, xs, (int64_t)rows));
+    }
+    LinearGuard gate, up, down;
+    lib_check(exl3_linear_load(c.c, (r.prefix + ".gate_proj").c_str(), &gate.h));
+    lib_check(exl3_linear_load(c.c, (r.prefix + ".up_proj").c_str(), &up.h));
+    lib_check(exl3_linear_load(c.c, (r.prefix + ".down_proj").c_str(), &down.h));
+    const std::vector<uint16_t> gy = linear_run(gate.h, xs, (int64_t)rows);
+    const std::vector<uint16_t> uy = linear_run(up.h, xs, (int64_t)rows);
+    DeviceBuffer gb(gy), ub(uy), act(gy.size() * 2);
+    lib_check(exl3_swiglu(gb.as<uint16_t>(), ub.as<uint16_t>(), act.as<uint16_t>(),
+                          (int64_t)gy.size(), nullptr));
+    return json_list(linear_run(down.h, act.read<uint16_t>(gy.size()), (int64_t)rows));
+  }
+  // metal-checkpoint-group (main.rs:1173-1199): ProjectionGroup::load
+  // (gpu/projection.rs:2386-2443) of load_exl3 projections sharing one input
+  // width, one f16 row (x or a [1, width] view), one f16 output per
+  // projection; "grouped" when there are two or more generic projections of
+  // one K (not 7) and codebook.
+  if (r.op == "metal-checkpoint-group") {
+    const bool view = r.x_layout.given || r.has_x_f32;
+    std::vector<uint16_t> xs;
+    uint32_t vrows = 0, vcols = 0;
+    if (view) xs = gather_view(r, &vrows, &vcols, "invalid ordinary projection bundle input");
+    CheckpointGuard c;
+    lib_check(exl3_checkpoint_open(r.path.c_str(), &c.c));
+    std::vector<FlashGeometry> geo;
+    for (const std::string& p : r.prefixes) geo.push_back(flash_geometry(c.c, p, true));
+    if (geo.empty()) bail("empty projection bundle");
+    for (const FlashGeometry& g : geo)
+      if (g.input != geo[0].input) bail("projection bundle requires one input width and Metal context");
+    bool grouped = geo.size() >= 2 && geo[0].k != 7;
+    for (const FlashGeometry& g : geo)
+      grouped = grouped && g.generic && g.k == geo[0].k && g.cb == geo[0].cb;
+    if (view) {
+      if (vrows != 1 || vcols != geo[0].input) bail("invalid ordinary projection bundle input");
+    } else if (r.x.size() != geo[0].input) {
+      bail("invalid grouped input row length");
+    } else {
+      xs = r.x;
+    }
+    std::vector<exl3_linear*> parts;
+    struct Cleanup {
+      std::vector<exl3_linear*>& parts;
+      ~Cleanup() {
+        for (auto* h : parts) exl3_linear_destroy(h);
       }
+    } cleanup{parts};
+    for (const std::string& p : r.prefixes) {
+      parts.push_back(nullptr);
+      lib_check(exl3_linear_load(c.c, p.c_str(), &parts.back()));
     }
-    std::string out = std::string("{\"grouped\":") + (grouped ? "true" : "false") +
-                      ",\"outputs\":[";
-    for (size_t i = 0; i < ys.size(); ++i) {
-      if (i) out += ',';
-      out += json_list(ys[i]->read<uint16_t>(exl3_linear_out_features(parts[i])));
-    }
-    return out + "]}";
+    return group_outputs(parts, grouped, xs);
   }
   bail("unknown or unavailable codec operation " + r.op);
 }

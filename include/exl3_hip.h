@@ -199,6 +199,27 @@ int exl3_moe_forward(const exl3_moe* handle, const void* x, int32_t x_type, int6
                      const uint32_t* selected, const void* scores, int32_t scores_type, void* y,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* The mapped expert QMV, expert_mapped (linear.rs:2817-2852; its layout,
+ * expert_mapped_layout :3054-3336, for a route-major bank): x [rows][in] of
+ * x_type (f16, bf16 or f32) with rows = routes * projections, per-row input
+ * scales suh [rows][in] f16, a bank trellis [in/16][bank_tiles][16k] u16 and
+ * routes selected u32[routes].  Row r = route * projections + p multiplies
+ * tile columns selected[route] * out/16 + p * stride_tiles + t (t < out/16)
+ * by xhat_r = f16(H128(f16(f16(x_r) * suh_r)) / sqrt(128)).  raw != 0: y is
+ * the f32 product [rows][out] (svh unused, may be NULL); else y [rows][out] of
+ * x_type is f16(H128(f16(yhat)) / sqrt(128)) * svh_r (svh [rows][out] f16)
+ * cast to x's dtype.  Checks as expert_mapped_layout, plus a 128-aligned
+ * input and every projection's columns inside the bank; rows whose expert
+ * index leaves the bank (device data) produce zeros.  Rows are independent
+ * of each other (the K-split depends on `in` only). */
+size_t exl3_expert_mapped_workspace_bytes(int32_t in, int32_t out, int64_t rows);
+int exl3_expert_mapped(const uint16_t* trellis, int32_t in, int32_t bank_tiles, int32_t k,
+                       int32_t cb, const void* x, int32_t x_type, int64_t rows,
+                       const uint16_t* suh, const uint32_t* selected, int32_t routes,
+                       int32_t projections, int32_t out, int32_t stride_tiles,
+                       const uint16_t* svh, int32_t raw, void* y, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
 /* The input prologue of every EXL3 projection as an op of its own,
  * exl3_prepare128 (exl3.metal:204-216; the `metal-prepare128` codec op,
  * main.rs:1338-1342, gpu.rs:1537-1558): out[i] = f16(H128(f16(x[i] * s)) /

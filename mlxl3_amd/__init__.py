@@ -105,6 +105,12 @@ _SIGNATURES = {
     "exl3_swiglu_down_input": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp]),
     "exl3_finish_and_reduce": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp]),
     "exl3_prepare128": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _vp]),
+    "exl3_expert_mapped_workspace_bytes": (_sz, [_i32, _i32, _i64]),
+    "exl3_expert_mapped": (
+        _i32,
+        [_vp, _i32, _i32, _i32, _i32, _vp, _i32, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _vp,
+         _i32, _vp, _vp, _sz, _vp],
+    ),
     "exl3_decode_tiles": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _vp]),
     "exl3_codewords": (_i32, [_vp, _i64, _i32, _vp, _vp]),
     "exl3_pack_tiles": (_i32, [_vp, _i64, _i32, _vp, _vp]),
@@ -581,6 +587,44 @@ def prepare128(x, scales):
     _check(load_library().exl3_prepare128(_ptr(x), x.numel(), int(width), _ptr(scales),
                                           scales.numel(), _ptr(out), _stream_ptr(x.device)))
     return out
+
+
+def expert_mapped(x, trellis, suh, selected, projections: int, out: int, stride_tiles: int,
+                  k: int, cb: int = 0, svh=None, raw: bool = False, workspace=None):
+    """expert_mapped (linear.rs:2817-2852) over a route-major bank
+    (exl3_expert_mapped): x [rows, in] (f16, bf16 or f32) with rows = routes *
+    projections, trellis [in/16, bank_tiles, 16k] (int16/uint16 words), suh
+    [rows, in] f16, selected [routes] (int32/uint32 expert indices); row r =
+    route * projections + p multiplies tile columns selected[route] * out/16 +
+    p * stride_tiles + t.  raw: the f32 products [rows, out]; else the
+    output epilogue with svh [rows, out] (f16), in x's dtype."""
+    torch = _torch()
+    x = _require_device(x, "x", (torch.float16, torch.bfloat16, torch.float32))
+    trellis = _require_device(trellis, "trellis", (torch.int16, torch.uint16))
+    suh = _require_device(suh, "suh", (torch.float16,))
+    selected = _require_device(selected, "selected", (torch.int32, torch.uint32))
+    if x.dim() != 2 or trellis.dim() != 3 or suh.shape != x.shape or selected.dim() != 1:
+        raise Exl3Error(-1, "invalid expert routes or input scales")
+    rows, n_in = x.shape
+    if trellis.shape[0] * 16 != n_in or trellis.shape[2] != 16 * k:
+        raise Exl3Error(-1, "invalid expert trellis")
+    if not raw:
+        if svh is None:
+            raise Exl3Error(-1, "invalid expert output scales")
+        svh = _require_device(svh, "svh", (torch.float16,))
+        if tuple(svh.shape) != (rows, out):
+            raise Exl3Error(-1, "invalid expert output scales")
+    lib = load_library()
+    y = torch.empty(rows, out, dtype=torch.float32 if raw else x.dtype, device=x.device)
+    need = int(lib.exl3_expert_mapped_workspace_bytes(n_in, int(out), rows))
+    if workspace is None:
+        workspace = torch.zeros(max(need, 1), dtype=torch.uint8, device=x.device)
+    _check(lib.exl3_expert_mapped(
+        _ptr(trellis), n_in, int(trellis.shape[1]), int(k), int(cb), _ptr(x), _dtype_code(x.dtype),
+        rows, _ptr(suh), _ptr(selected), int(selected.numel()), int(projections), int(out),
+        int(stride_tiles), None if raw else _ptr(svh), int(bool(raw)), _ptr(y), _ptr(workspace),
+        workspace.numel(), _stream_ptr(x.device)))
+    return y
 
 
 def geglu(gate, up):

@@ -20,7 +20,8 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libexl3_hip.so"
 CODEC = HERE / "exl3_codec"  # the codec JSON-lines driver (links LIB)
-SOURCES = ["exl3_api.hip", "exl3_qmv.hip", "exl3_qmm.hip", "exl3_moe.hip", "exl3_checkpoint.cpp"]
+SOURCES = ["exl3_api.hip", "exl3_qmv.hip", "exl3_qmm.hip", "exl3_moe.hip", "exl3_mapped.hip",
+           "exl3_checkpoint.cpp"]
 ARCH = "gfx950"
 
 # -ffp-contract=off: every f32 multiply/add in the glue is rounded separately,

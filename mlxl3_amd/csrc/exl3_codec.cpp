@@ -18,6 +18,7 @@
 //   mlx-switch                        GPU Exl3SwitchGlu forward (bank in the request)
 //   mlx-checkpoint-switch/-group      the same on projections of a checkpoint
 //   mlx-swiglu-prepare, mlx-expert-reduce   the SwitchGLU glue steps
+//   mlx-expert                        GPU mapped expert QMV (exl3_expert_mapped)
 //   metal-checkpoint-linear, metal-exl3-linear, metal-checkpoint-expert,
 //   metal-checkpoint-group            checkpoint projections, dense experts and
 //                                     projection bundles under the direct-Metal
@@ -28,6 +29,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -70,6 +72,8 @@ struct Request {
   std::vector<uint64_t> widths;
   std::string path, prefix;
   std::vector<std::string> prefixes;
+  uint64_t projections_per_route = 0, projection_stride_tiles = 0;
+  bool return_raw = false;
 };
 
 std::vector<uint32_t> u32_array(const Value* v, const char* field) {
@@ -200,6 +204,15 @@ Request parse_request(const std::string& line) {
   r.down_svh = u16_array(v.find("down_svh"), "down_svh");
   r.path = string_field(v.find("path"), "path");
   r.prefix = string_field(v.find("prefix"), "prefix");
+  r.projections_per_route =
+      uint_field(v.find("projections_per_route"), "projections_per_route", 0, UINT64_MAX);
+  r.projection_stride_tiles =
+      uint_field(v.find("projection_stride_tiles"), "projection_stride_tiles", 0, UINT64_MAX);
+  if (const Value* rr = v.find("return_raw")) {
+    if (rr->kind != exl3::json::Kind::Bool)
+      bail("invalid codec request: return_raw must be a boolean");
+    r.return_raw = rr->b;
+  }
   if (const Value* ps = v.find("prefixes")) {
     if (!ps->is_array()) bail("invalid codec request: prefixes must be an array");
     for (const Value& e : ps->arr) r.prefixes.push_back(string_field(&e, "prefixes"));
@@ -230,6 +243,23 @@ std::string json_list(const std::vector<T>& v) {
   for (size_t i = 0; i < v.size(); ++i) {
     if (i) o += ',';
     o += std::to_string(v[i]);
+  }
+  return o + "]";
+}
+
+// f32 values as JSON numbers that read back to the same f32 (9 significant
+// digits); non-finite values as null, as serde_json writes them
+std::string json_f32_list(const std::vector<float>& v) {
+  std::string o = "[";
+  char buf[32];
+  for (size_t i = 0; i < v.size(); ++i) {
+    if (i) o += ',';
+    if (std::isfinite(v[i])) {
+      snprintf(buf, sizeof buf, "%.9g", (double)v[i]);
+      o += buf;
+    } else {
+      o += "null";
+    }
   }
   return o + "]";
 }
@@ -738,6 +768,42 @@ std::string run(const Request& r) {
                               dn.as<uint16_t>(), ds.as<uint16_t>(), dv.as<uint16_t>(), (int)input,
                               (int)hidden, (int)experts, (int)top_k, (int)r.k, cb, &g.h));
     return json_list(moe_run(g.h, r.x, r.selected, r.beta, rows));
+  }
+  if (r.op == "mlx-expert") {  // main.rs:540-597
+    check_k(r.k);
+    if (r.projections_per_route == 0 || r.projections_per_route > INT32_MAX)
+      bail(r.projections_per_route ? "out of range integral type conversion attempted"
+                                   : "invalid projection count");
+    const uint64_t rows = (uint64_t)r.selected.size() * r.projections_per_route;
+    if (rows / r.projections_per_route != r.selected.size()) bail("expert row count overflow");
+    if (rows > INT32_MAX) bail("out of range integral type conversion attempted");
+    if (rows == 0) bail("missing expert routes");
+    const uint64_t input_dims = r.x.size() / rows, output_dims = r.cols;
+    if (r.x.size() > INT32_MAX || output_dims > INT32_MAX || r.projection_stride_tiles > INT32_MAX)
+      bail("out of range integral type conversion attempted");
+    const uint64_t input_tiles = input_dims / 16, per_tile = 16 * r.k;
+    if (input_tiles * per_tile == 0) bail("invalid expert trellis dimensions");
+    const uint64_t source_tiles = r.data.size() / (input_tiles * per_tile);
+    // Array::from_u16 / from_f16_bits of each tensor (array.rs:884-888)
+    expect_len(r.data.size(), input_tiles * source_tiles * per_tile);
+    expect_len(r.x.size(), rows * input_dims);
+    expect_len(r.suh.size(), rows * input_dims);
+    if (!r.return_raw) expect_len(r.svh.size(), rows * output_dims);
+    DeviceBuffer tr(r.data), x(r.x), su(r.suh), sel(r.selected),
+        sv(r.return_raw ? std::vector<uint16_t>() : r.svh),
+        y(rows * output_dims * (r.return_raw ? 4 : 2));
+    const size_t wb = exl3_expert_mapped_workspace_bytes((int)input_dims, (int)output_dims,
+                                                         (int64_t)rows);
+    DeviceBuffer ws(wb);
+    lib_check(exl3_expert_mapped(tr.as<uint16_t>(), (int)input_dims, (int)source_tiles, (int)r.k,
+                                 cb, x.p, EXL3_F16, (int64_t)rows, su.as<uint16_t>(),
+                                 sel.as<uint32_t>(), (int)r.selected.size(),
+                                 (int)r.projections_per_route, (int)output_dims,
+                                 (int)r.projection_stride_tiles,
+                                 r.return_raw ? nullptr : sv.as<uint16_t>(), r.return_raw ? 1 : 0,
+                                 y.p, ws.p, wb, nullptr));
+    if (r.return_raw) return "{\"f32\":" + json_f32_list(y.read<float>(rows * output_dims)) + "}";
+    return "{\"f16\":" + json_list(y.read<uint16_t>(rows * output_dims)) + "}";
   }
   if (r.op == "mlx-swiglu-prepare") {  // validate_moe_codec main.rs:239-252, run :598-613
     const uint64_t hidden = r.cols, width = hidden * 2;

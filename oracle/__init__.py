@@ -90,6 +90,11 @@ def lib():
                                         ctypes.c_int, _u16p, _u16p, _u16p, _u16p, _u16p, _u16p,
                                         _u32p, _vp, ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int]
+        L.exl3o_expert_mapped.restype = ctypes.c_int
+        L.exl3o_expert_mapped.argtypes = [_vp, ctypes.c_int, ctypes.c_int64, ctypes.c_int, _u16p,
+                                          _u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _u32p,
+                                          ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          _vp, ctypes.c_int, _vp, ctypes.c_int]
         _lib = L
     return _lib
 
@@ -246,6 +251,34 @@ def moe_forward(x, selected, scores, gu_trellis, gu_suh, gu_svh, down_trellis, d
                                  sc.ctypes.data, scode, y.ctypes.data, int(gelu), logical, threads)
     if rc:
         raise ValueError(f"oracle MoE forward failed ({rc})")
+    return y
+
+
+def expert_mapped(x, suh, trellis, selected, projections: int, out: int, stride_tiles: int,
+                  k: int, cb: int, svh=None, raw: bool = False, x_dtype=None,
+                  threads: int = 0) -> np.ndarray:
+    """expert_mapped (linear.rs:2817-2852) over a route-major bank trellis
+    [in/16][bank_tiles][16k]: x [rows][in] (float16, float32, or bf16 bits with
+    x_dtype="bf16"), suh [rows][in], selected [routes], rows = routes *
+    projections.  raw: float32 [rows][out]; else [rows][out] of x's dtype
+    (bf16 as uint16 bits) with svh [rows][out]."""
+    x = np.ascontiguousarray(x)
+    code = _dtype_code(x, x_dtype)
+    rows, n_in = x.shape
+    tr = _u16(trellis)
+    sel = np.ascontiguousarray(selected, np.uint32).ravel()
+    if raw:
+        y = np.empty((rows, out), np.float32)
+    else:
+        y = np.empty((rows, out), _NP_OF_CODE[code])
+    sv = None if svh is None else np.ascontiguousarray(_u16(svh)).ravel()
+    rc = lib().exl3o_expert_mapped(x.ctypes.data, code, rows, n_in, _u16(suh).ravel(), tr.ravel(),
+                                   int(tr.shape[1]), k, cb, sel, int(sel.size), int(projections),
+                                   int(out), int(stride_tiles),
+                                   None if sv is None else sv.ctypes.data, int(bool(raw)),
+                                   y.ctypes.data, threads)
+    if rc:
+        raise ValueError(f"oracle expert_mapped failed ({rc})")
     return y
 
 

@@ -473,6 +473,73 @@ static void expert_gemv(const float* xin, const uint16_t* trellis, int in, int t
         }
 }
 
+/* expert_mapped (linear.rs:2817-2852; expert_mapped_layout :3054-3336 for a
+ * route-major bank, the MLX path): row r = route * projections + p of x
+ * [rows][in] gets xhat = f16(x) * suh[r] (f16) -> MLX f16 H128 (the prologue
+ * of exl3o_prologue with the row's scales), times the bank's tile columns
+ * selected[route] * out/16 + p * stride_tiles + t (t < out/16) in f32
+ * (expert_gemv); raw: y f32 = that product; else f16(yhat) -> f16 H128 ->
+ * * svh[r] (f16) -> x's dtype (the linear's mode-1 epilogue without bias).
+ * Rows whose columns leave the bank are zero (the HIP build's choice for
+ * device-side expert indices the reference does not check). */
+int exl3o_expert_mapped(const void* x, int x_dtype, int64_t rows, int in, const uint16_t* suh,
+                        const uint16_t* trellis, int bank_tiles, int k, int cb,
+                        const uint32_t* selected, int routes, int projections, int out,
+                        int stride_tiles, const uint16_t* svh, int raw, void* y, int threads) {
+    if (!valid_dtype(x_dtype) || k < 1 || k > 8 || k == 7 || cb < 0 || cb > 2) return -1;
+    if (in <= 0 || in % 128 || out <= 0 || out % 128 || bank_tiles <= 0) return -1;
+    if (projections <= 0 || routes <= 0 || (int64_t)routes * projections != rows) return -1;
+    if (stride_tiles < 0 || (int64_t)(projections - 1) * stride_tiles + out / 16 > bank_tiles)
+        return -1;
+    if (!x || !suh || !trellis || !selected || !y || (!raw && !svh)) return -1;
+    const uint16_t* table = codebook_table(cb);
+    if (!table) return -3;
+    uint16_t perm[256];
+    exl3o_permutation(perm);
+    const size_t xsz = x_dtype == DT_F32 ? 4 : 2;
+    int err = 0;
+#ifdef _OPENMP
+    if (threads <= 0) threads = omp_get_max_threads();
+#else
+    (void)threads;
+#endif
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
+    for (int64_t r = 0; r < rows; ++r) {
+        uint16_t* xhat = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)in);
+        float* xin = (float*)malloc(sizeof(float) * (size_t)in);
+        float* yh = (float*)malloc(sizeof(float) * (size_t)out);
+        if (!xhat || !xin || !yh) {
+#pragma omp atomic write
+            err = -3;
+        } else {
+            exl3o_prologue((const char*)x + (size_t)r * in * xsz, x_dtype, 1, in,
+                           suh + (size_t)r * in, xhat);
+            for (int i = 0; i < in; ++i) xin[i] = h2f(xhat[i]);
+            const int64_t route = r / projections, p = r - route * projections;
+            const int64_t base = (int64_t)selected[route] * (out / 16) + p * stride_tiles;
+            if (base + out / 16 <= bank_tiles)
+                expert_gemv(xin, trellis, in, bank_tiles, (int)base, out, k, table, perm, yh);
+            else
+                for (int n = 0; n < out; ++n) yh[n] = 0.0f;
+            if (raw) {
+                memcpy((float*)y + (size_t)r * out, yh, sizeof(float) * (size_t)out);
+            } else {
+                for (int n = 0; n < out; ++n) yh[n] = rh(yh[n]);
+                exl3o_h128_staged(yh, out);
+                for (int n = 0; n < out; ++n) {
+                    float v = rh(yh[n] * h2f(svh[(size_t)r * out + n]));
+                    if (x_dtype == DT_BF16) v = exl3o_bf16_to_f32(exl3o_f32_to_bf16(v));
+                    store_y(y, x_dtype, r * out + n, v);
+                }
+            }
+        }
+        free(xhat);
+        free(xin);
+        free(yh);
+    }
+    return err;
+}
+
 /* Exl3SwitchGlu::forward (moe.rs:905-975) for SiLU: routed_inputs
  * (moe.rs:184-250: f16(x*suh), MLX f16 H128 schedule), expert QMM raw outputs,
  * glu_down_input (moe.rs:435-563: f16(raw) -> f32 H128 -> f16(v*s*svh),

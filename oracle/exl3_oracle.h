@@ -88,6 +88,16 @@ int exl3o_prologue(const void* x, int x_dtype, int64_t rows, int in, const uint1
  * gelu != 0: forward_gelu (moe.rs:1087-1153) -- gate/up and the down input
  * in the linear's engine glue (staged H128), act = geglu(gate, up) for
  * columns < logical_hidden and 0 beyond. */
+/* expert_mapped (linear.rs:2817-2852, route-major bank): rows = routes *
+ * projections rows of x (x_dtype) with per-row suh [rows][in] f16, bank
+ * trellis [in/16][bank_tiles][16k], tile columns selected[route] * out/16 +
+ * p * stride_tiles + t; raw: y f32 [rows][out]; else y [rows][out] of x_dtype
+ * after the epilogue with per-row svh [rows][out].  Rows past the bank: 0. */
+int exl3o_expert_mapped(const void* x, int x_dtype, int64_t rows, int in, const uint16_t* suh,
+                        const uint16_t* trellis, int bank_tiles, int k, int cb,
+                        const uint32_t* selected, int routes, int projections, int out,
+                        int stride_tiles, const uint16_t* svh, int raw, void* y, int threads);
+
 int exl3o_moe_forward(const void* x, int x_dtype, int64_t rows, int in, int hidden, int experts,
                       int top_k, int k, int cb, const uint16_t* gu_trellis,
                       const uint16_t* gu_suh, const uint16_t* gu_svh,

@@ -278,6 +278,16 @@ int exl3_qmv_inner(const uint16_t* packed, int32_t rows, int32_t cols, int32_t k
                    const uint16_t* x, uint16_t* y, void* workspace, size_t workspace_bytes,
                    void* stream);
 
+/* Fault hook for tests and harnesses (no counterpart in the reference; it
+ * plays the part of a failing Metal launch under protect(),
+ * mlx_bridge.cpp:56-66): every later launch whose name contains `text` fails
+ * with EXL3_EDEVICE and "<name>: forced launch failure" -- the entry points'
+ * first launches before anything is issued (nothing written, usable without a
+ * GPU), later ones after issuing (the kernels that write the output are then
+ * never launched, and the workspace stays valid for the next call).  NULL
+ * disarms.  EXL3_FAIL_LAUNCH in the environment arms it at load. */
+void exl3_debug_fail_launch(const char* text);
+
 /* ------------------------------------------------------------------------
  * Checkpoints (safetensors EXL3 model directories).
  *

@@ -105,6 +105,7 @@ _SIGNATURES = {
     "exl3_swiglu_down_input": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp]),
     "exl3_finish_and_reduce": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp]),
     "exl3_prepare128": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _vp]),
+    "exl3_debug_fail_launch": (None, [ctypes.c_char_p]),
     "exl3_expert_mapped_workspace_bytes": (_sz, [_i32, _i32, _i64]),
     "exl3_expert_mapped": (
         _i32,
@@ -587,6 +588,13 @@ def prepare128(x, scales):
     _check(load_library().exl3_prepare128(_ptr(x), x.numel(), int(width), _ptr(scales),
                                           scales.numel(), _ptr(out), _stream_ptr(x.device)))
     return out
+
+
+def debug_fail_launch(text: Optional[str]) -> None:
+    """Arm the library's fault hook (exl3_debug_fail_launch): launches whose
+    name contains `text` fail with EXL3_EDEVICE ("<name>: forced launch
+    failure"); None disarms."""
+    load_library().exl3_debug_fail_launch(None if text is None else text.encode())
 
 
 def expert_mapped(x, trellis, suh, selected, projections: int, out: int, stride_tiles: int,

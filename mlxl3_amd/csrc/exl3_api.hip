@@ -3,6 +3,11 @@
 // count, split-K choice, workspace layout and the C ABI of include/exl3_hip.h.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+#include <cstring>
+#include <mutex>
+#include <string>
+
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
@@ -69,7 +74,39 @@ int exl3::fail(int code, const char* fmt, ...) {
   return code;
 }
 
+// Fault hook: launches whose name contains the armed text fail with
+// EXL3_EDEVICE before (launch_gate) or after (check_launch) they are issued,
+// so tests can follow the error path, with or without a GPU.  Armed by
+// exl3_debug_fail_launch or, at load, by EXL3_FAIL_LAUNCH.
+static std::atomic<bool> g_fault_armed{false};
+static std::mutex g_fault_mutex;
+static std::string g_fault_text;
+
+static bool fault_forced(const char* what) {
+  if (!g_fault_armed.load(std::memory_order_relaxed)) return false;
+  std::lock_guard<std::mutex> lock(g_fault_mutex);
+  return g_fault_armed.load(std::memory_order_relaxed) &&
+         std::strstr(what, g_fault_text.c_str()) != nullptr;
+}
+
+void exl3_debug_fail_launch(const char* text) {
+  std::lock_guard<std::mutex> lock(g_fault_mutex);
+  g_fault_text = text ? text : "";
+  g_fault_armed.store(text != nullptr, std::memory_order_relaxed);
+}
+
+static const bool g_fault_from_env = [] {
+  if (const char* env = getenv("EXL3_FAIL_LAUNCH")) exl3_debug_fail_launch(env);
+  return true;
+}();
+
+int exl3::launch_gate(const char* what) {
+  if (fault_forced(what)) return fail(EXL3_EDEVICE, "%s: forced launch failure", what);
+  return EXL3_OK;
+}
+
 int exl3::check_launch(const char* what) {
+  if (fault_forced(what)) return fail(EXL3_EDEVICE, "%s: forced launch failure", what);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(EXL3_EDEVICE, "%s: %s", what, hipGetErrorString(e));
   return EXL3_OK;
@@ -280,6 +317,7 @@ static Member member_of(const exl3_linear* h, void* y, int cblk0, int x_type) {
 static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows,
                          void* const* ys, uint32_t* counters, char* scratch, const Glu& glu,
                          hipStream_t stream) {
+  if (int rc = launch_gate("EXL3 QMV launch")) return rc;
   QmvParams p{};
   int cblk0 = 0;
   for (int i = 0; i < g.count; ++i) {
@@ -330,6 +368,7 @@ static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows
 static int run_group_qmm(const Group& g, const void* x, int x_type, int64_t rows,
                          void* const* ys, uint32_t* counters, char* scratch,
                          const uint16_t* given_xhat, hipStream_t stream) {
+  if (int rc = launch_gate("EXL3 QMM launch")) return rc;
   const size_t xbytes = align_up(sizeof(uint16_t) * (size_t)rows * g.in);
   QmmParams q{};
   if (!given_xhat) {
@@ -461,6 +500,7 @@ static int mlp_forward(const exl3_linear* gate, const exl3_linear* up, const exl
   char* scratch = base + 3 * act_bytes;
   if (int rc = run_group_qmm(g, x, EXL3_F16, rows, gu_y, counters, scratch, nullptr, stream))
     return rc;
+  if (int rc = launch_gate("SwiGLU prepare launch")) return rc;
   launch_swiglu_prepare((const uint16_t*)gu_y[0], (const uint16_t*)gu_y[1], down->suh, gate->out,
                         (int)rows, act, stream);
   if (int rc = check_launch("SwiGLU prepare launch")) return rc;
@@ -598,6 +638,7 @@ int exl3_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t
   if (count < 0) return fail(EXL3_EINVAL, "negative element count");
   if (count == 0) return EXL3_OK;
   if (!gate || !up || !out) return fail(EXL3_EINVAL, "null SwiGLU buffer");
+  if (int rc = launch_gate("SwiGLU launch")) return rc;
   launch_glu(gate, up, out, count, false, (hipStream_t)stream);
   return check_launch("SwiGLU launch");
 }
@@ -607,6 +648,7 @@ int exl3_geglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t 
   if (count < 0) return fail(EXL3_EINVAL, "negative element count");
   if (count == 0) return EXL3_OK;
   if (!gate || !up || !out) return fail(EXL3_EINVAL, "null GEGLU buffer");
+  if (int rc = launch_gate("GEGLU launch")) return rc;
   launch_glu(gate, up, out, count, true, (hipStream_t)stream);
   return check_launch("GEGLU launch");
 }
@@ -620,6 +662,7 @@ int exl3_prepare128(const uint16_t* x, int64_t elements, int32_t width, const ui
     return fail(EXL3_EINVAL, "expected complete 128-aligned rows and column or element scales");
   if (elements == 0) return EXL3_OK;
   if (!x || !scales || !out) return fail(EXL3_EINVAL, "null prepare128 buffer");
+  if (int rc = launch_gate("EXL3 prepare128 launch")) return rc;
   PrologueParams pp{};
   pp.x = x;
   pp.x_dtype = EXL3_F16;

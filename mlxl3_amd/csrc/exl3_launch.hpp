@@ -48,8 +48,11 @@ void launch_fill_zero(uint32_t* p, size_t words, hipStream_t s);
 
 // Records the thread-local error message and returns `code`.
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
-// Converts a pending launch error into EXL3_EDEVICE.
+// Converts a pending launch error into EXL3_EDEVICE (or the fault hook's
+// forced failure for `what`, after the launch).
 int check_launch(const char* what);
+// The fault hook before a launch: EXL3_EDEVICE when `what` is armed.
+int launch_gate(const char* what);
 
 // Hands a device allocation (hipMalloc) to a handle, which frees it when it is
 // destroyed: the checkpoint loaders own the weights they upload.

@@ -190,6 +190,7 @@ extern "C" int exl3_expert_mapped(const uint16_t* trellis, int32_t in, int32_t b
   uint16_t* xhat = (uint16_t*)ws;
   float* partials = (float*)(ws + align256((size_t)rows * in * 2));
 
+  if (int rc = launch_gate("expert prologue")) return rc;
   PrologueParams pp{};
   pp.x = x;
   pp.x_dtype = x_type;

@@ -273,6 +273,7 @@ int exl3_moe_forward(const exl3_moe* h, const void* x, int32_t x_type, int64_t r
   pp.counters = (uint32_t*)(ws + L.counters);
   pp.ncounters = L.ncounters;
   pp.block_rows = L.block_rows;
+  if (int rc = launch_gate("moe plan")) return rc;
   moe_plan_kernel<<<1, 1024, (3 * h->experts + 1) * sizeof(int), s>>>(pp);
   if (int rc = check_launch("moe plan")) return rc;
 

@@ -22,10 +22,13 @@ from __future__ import annotations
 
 import ctypes
 import enum
+import os
 from pathlib import Path
 from typing import Optional, Sequence
 
-LIB_PATH = Path(__file__).resolve().parent / "libexl3_hip.so"
+# EXL3_LIB selects another build of the same ABI (e.g. the sanitizer build of
+# the host code, mlxl3_amd/sanitize.py).
+LIB_PATH = Path(os.environ.get("EXL3_LIB") or Path(__file__).resolve().parent / "libexl3_hip.so")
 
 __all__ = [
     "codewords",

@@ -3,10 +3,14 @@ codec tests: one subprocess per batch of requests, as the reference's harnesses
 drive `mlxl3-rs codec`."""
 
 import json
+import os
 import subprocess
 from pathlib import Path
 
-CODEC = Path(__file__).resolve().parent.parent / "mlxl3_amd" / "exl3_codec"
+# EXL3_CODEC selects another build of the driver (the sanitizer build of
+# mlxl3_amd/sanitize.py)
+CODEC = Path(os.environ.get("EXL3_CODEC")
+             or Path(__file__).resolve().parent.parent / "mlxl3_amd" / "exl3_codec")
 
 
 def run(requests, timeout=120):

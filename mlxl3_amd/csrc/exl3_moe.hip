@@ -1,8 +1,9 @@
 // MoE SwitchGLU entry points (Exl3SwitchGlu, native/src/moe.rs:611-1085):
 // validation as switch_glu_layout (native/src/contracts.rs:4-28) and
-// Exl3SwitchGlu::new (moe.rs:835-886), workspace layout, and the five
-// launches of the grouped expert path (route plan, gather, gate/up QMM with
-// the fused SwiGLU glue, down QMM with the fused per-slot finish, top-k sum).
+// Exl3SwitchGlu::new (moe.rs:835-886), workspace layout, and the four
+// launches of the grouped expert path (route plan with the gather of the
+// gate/up inputs, gate/up QMM with the fused SwiGLU glue, down QMM with the
+// fused per-slot finish, top-k sum).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -14,12 +15,12 @@
 #include "exl3_moe.hpp"
 
 namespace exl3 {
-#define EXL3_MOE_INST(K, CB)                                          \
-  template __global__ void moe_mm_kernel<K, CB, 2, 1>(MoeMmParams);  \
-  template __global__ void moe_mm_kernel<K, CB, 1, 1>(MoeMmParams);  \
-  template __global__ void moe_mm_kernel<K, CB, 2, 2>(MoeMmParams);  \
-  template __global__ void moe_mm_kernel<K, CB, 1, 2>(MoeMmParams);  \
-  template __global__ void moe_mm_kernel<K, CB, 2, 4>(MoeMmParams);  \
+#define EXL3_MOE_INST(K, CB)                                                          \
+  template __global__ void moe_mm_kernel<K, CB, 2, 1>(MoeMmParams);                  \
+  template __global__ void moe_mm_kernel<K, CB, 1, 1>(MoeMmParams);                  \
+  template __global__ void moe_mm_kernel<K, CB, 2, 2>(MoeMmParams);                  \
+  template __global__ void moe_mm_kernel<K, CB, 1, 2>(MoeMmParams);                  \
+  template __global__ void moe_mm_kernel<K, CB, 2, 4>(MoeMmParams);                  \
   template __global__ void moe_mm_kernel<K, CB, 1, 4>(MoeMmParams);
 // K = 7 is not a SwitchGLU width (switch_glu_layout rejects it).
 EXL3_INST_CB(EXL3_MOE_INST, 1)
@@ -29,12 +30,12 @@ EXL3_INST_CB(EXL3_MOE_INST, 4)
 EXL3_INST_CB(EXL3_MOE_INST, 5)
 EXL3_INST_CB(EXL3_MOE_INST, 6)
 EXL3_INST_CB(EXL3_MOE_INST, 8)
-template __global__ void moe_gather_kernel<true>(const void*, int, int, int, const uint32_t*,
-                                                 const int*, const int*, int, const uint16_t*,
-                                                 uint16_t*);
-template __global__ void moe_gather_kernel<false>(const void*, int, int, int, const uint32_t*,
-                                                  const int*, const int*, int, const uint16_t*,
-                                                  uint16_t*);
+template __global__ void moe_route_kernel<true>(MoePlanParams, MoeGatherParams);
+template __global__ void moe_route_kernel<false>(MoePlanParams, MoeGatherParams);
+template __global__ void moe_reduce_kernel<true>(const void*, int, const uint32_t*, int, int, int,
+                                                 void*);
+template __global__ void moe_reduce_kernel<false>(const void*, int, const uint32_t*, int, int,
+                                                  int, void*);
 }  // namespace exl3
 
 using namespace exl3;
@@ -66,7 +67,7 @@ struct exl3_moe {
 
 void exl3::adopt_device_memory(exl3_moe* h, void* mem) { h->owned = mem; }
 
-// The largest bank the plan kernel's LDS histogram holds (3 ints per expert).
+// The largest bank the route launch's LDS histogram holds (3 ints per expert).
 static constexpr int kMoeMaxExperts = 4096;
 static constexpr size_t kMoeAlign = 256;
 static size_t moe_align(size_t v) { return (v + kMoeAlign - 1) / kMoeAlign * kMoeAlign; }
@@ -273,21 +274,25 @@ int exl3_moe_forward(const exl3_moe* h, const void* x, int32_t x_type, int64_t r
   pp.counters = (uint32_t*)(ws + L.counters);
   pp.ncounters = L.ncounters;
   pp.block_rows = L.block_rows;
+  MoeGatherParams gp;
+  gp.x = x;
+  gp.x_dtype = x_type;
+  gp.in = h->in;
+  gp.top_k = h->top_k;
+  gp.slots = slots;
+  gp.experts = h->experts;
+  gp.selected = selected;
+  gp.gu_suh = h->gu_suh;
+  gp.xgu = (uint16_t*)(ws + L.xgu);
+  const unsigned route_wgs =
+      1u + (unsigned)((2 * (int64_t)slots * ((h->in / 128 + 7) / 8) + 3) / 4);
+  const size_t plan_lds = (3 * (size_t)h->experts + 1) * sizeof(int);
   if (int rc = launch_gate("moe plan")) return rc;
-  moe_plan_kernel<<<1, 1024, (3 * h->experts + 1) * sizeof(int), s>>>(pp);
-  if (int rc = check_launch("moe plan")) return rc;
-
-  uint16_t* xgu = (uint16_t*)(ws + L.xgu);
-  const unsigned gather_wgs = (unsigned)((2 * (int64_t)slots * ((h->in / 128 + 7) / 8) + 3) / 4);
   if ((((uintptr_t)x | (uintptr_t)h->gu_suh) & 15) == 0)
-    moe_gather_kernel<true><<<gather_wgs, 256, 0, s>>>(x, x_type, h->in, h->top_k, selected,
-                                                       pp.sorted_slot, pp.counts + 1, slots,
-                                                       h->gu_suh, xgu);
+    moe_route_kernel<true><<<route_wgs, 256, plan_lds, s>>>(pp, gp);
   else
-    moe_gather_kernel<false><<<gather_wgs, 256, 0, s>>>(x, x_type, h->in, h->top_k, selected,
-                                                        pp.sorted_slot, pp.counts + 1, slots,
-                                                        h->gu_suh, xgu);
-  if (int rc = check_launch("moe gather")) return rc;
+    moe_route_kernel<false><<<route_wgs, 256, plan_lds, s>>>(pp, gp);
+  if (int rc = check_launch("moe plan")) return rc;
 
   MoeMmParams q{};
   q.experts = h->experts;
@@ -304,33 +309,40 @@ int exl3_moe_forward(const exl3_moe* h, const void* x, int32_t x_type, int64_t r
   q.width = h->hidden;
   q.col_blocks = h->hidden / 128;
   q.splits = L.splits_gu;
-  q.xa = xgu;
+  q.xa = gp.xgu;
+  q.a_rows = pp.sorted_slot;
   q.gu_svh = h->gu_svh;
   q.down_suh = h->down_suh;
   q.xd = (uint16_t*)(ws + L.xd);
   q.gelu = h->gelu;
   q.logical_hidden = h->logical_hidden;
   const int grid_blocks = (L.max_blocks + 7) / 8 * 8;  // whole blocks per XCD
+  // down: input width `hidden`, per-expert output `in`
+  MoeMmParams d = q;
+  d.trellis = (const uint32_t*)h->down_trellis;
+  d.tn_total = h->experts * h->in / 16;
+  d.k_in = h->hidden;
+  d.width = h->in;
+  d.col_blocks = h->in / 128;
+  d.splits = L.splits_down;
+  d.xa = q.xd;
+  d.a_rows = nullptr;
+  d.down_svh = h->down_svh;
+  d.scores = scores;
+  d.scores_dtype = scores_type;
+  d.z = ws + L.z;
   gateup<<<grid_blocks * q.col_blocks * q.splits, 512, 0, s>>>(q);
   if (int rc = check_launch("moe gate/up")) return rc;
-
-  // down: input width `hidden`, per-expert output `in`
-  q.trellis = (const uint32_t*)h->down_trellis;
-  q.tn_total = h->experts * h->in / 16;
-  q.k_in = h->hidden;
-  q.width = h->in;
-  q.col_blocks = h->in / 128;
-  q.splits = L.splits_down;
-  q.xa = q.xd;
-  q.down_svh = h->down_svh;
-  q.scores = scores;
-  q.scores_dtype = scores_type;
-  q.z = ws + L.z;
-  down<<<grid_blocks * q.col_blocks * q.splits, 256, 0, s>>>(q);
+  down<<<grid_blocks * d.col_blocks * d.splits, 256, 0, s>>>(d);
   if (int rc = check_launch("moe down")) return rc;
 
-  moe_reduce_kernel<<<dim3((unsigned)rows, (h->in + 255) / 256), 256, 0, s>>>(
-      q.z, scores_type, selected, h->experts, h->top_k, h->in, y);
+  const dim3 rgrid((unsigned)rows, (h->in + 2047) / 2048);
+  if (((uintptr_t)y & 15) == 0)
+    moe_reduce_kernel<true><<<rgrid, 256, 0, s>>>(d.z, scores_type, selected, h->experts,
+                                                   h->top_k, h->in, y);
+  else
+    moe_reduce_kernel<false><<<rgrid, 256, 0, s>>>(d.z, scores_type, selected, h->experts,
+                                                    h->top_k, h->in, y);
   return check_launch("moe reduce");
 }
 

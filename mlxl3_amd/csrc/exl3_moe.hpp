@@ -1,26 +1,27 @@
 // MoE SwitchGLU over EXL3 expert banks: the reference's Exl3SwitchGlu
 // (native/src/moe.rs:611-1085) -- route plan, routed inputs, expert QMMs,
 // SwiGLU glue, down projection, weighted top-k reduction -- re-designed for
-// gfx950 as five launches:
-//   1. plan:    one workgroup counting-sorts the rows*top_k slots by expert,
-//               cuts each expert's run into blocks of <= 16, 32 or 64 rows (block
+// gfx950 as four launches:
+//   1. route:   workgroup 0 counting-sorts the rows*top_k slots by expert, cuts
+//               each expert's run into blocks of <= 16, 32 or 64 rows (block
 //               table) and clears the tile arrival counters of the two expert
-//               QMMs;
-//   2. gather:  f16(x[token] * gu_suh[e][p]) -> staged Hadamard-128 for the gate
-//               (p = 0) and up (p = 1) inputs, in expert-sorted order;
-//   3. gate/up: per (block, 128 hidden columns, K-range) a workgroup of 8 waves
+//               QMMs; the other workgroups gather f16(x[token] * gu_suh[e][p])
+//               -> staged Hadamard-128 for the gate (p = 0) and up (p = 1)
+//               inputs, stored by slot;
+//   2. gate/up: per (block, 128 hidden columns, K-range) a workgroup of 8 waves
 //               decodes the expert's gate (waves 0-3) and up (waves 4-7) tiles of
 //               those columns in registers -- each wave owns a column pair, as in
-//               the QMV -- and multiplies them with the block's rows; the
+//               the QMV -- and multiplies them with the block's rows (read by
+//               slot through the sorted order); the
 //               epilogue is the whole of glu_down_input (moe.rs:435-563): f16,
 //               f32 Hadamard, *scale*svh, SiLU(g)*u, *down_suh, f32 Hadamard,
 //               *scale -> the down projection's xhat (GELU banks,
 //               forward_gelu: staged Hadamards and GEGLU instead);
-//   4. down:    the same kernel with 4 waves over the down bank; the epilogue is
+//   3. down:    the same kernel with 4 waves over the down bank; the epilogue is
 //               finish_and_reduce's per-slot part (moe.rs:586-609): f16, staged
 //               Hadamard, *svh, *score (f16 scores: an f16 product; f32 or bf16
 //               scores: an f32 product, MLX's promotion), stored per slot;
-//   5. reduce:  y[row] = sum over top_k in slot order in f32, then f16 (f16
+//   4. reduce:  y[row] = sum over top_k in slot order in f32, then f16 (f16
 //               scores) or kept f32 (f32 or bf16 scores).
 // Small inputs (decode: a handful of slots) split K over several workgroups
 // whose f32 partials meet in the last arriving one (agent-scope relaxed
@@ -53,27 +54,30 @@ struct MoePlanParams {
   int block_rows;            // 16, 32 or 64
 };
 
-// One workgroup of 1024 threads.  Slots with an expert id >= experts are left
-// out (their contribution is zero).
-__global__ __launch_bounds__(1024) void moe_plan_kernel(MoePlanParams p) {
-  extern __shared__ int lds[];  // cnt[E], off[E], boff[E+1]
+// The route plan, run by one workgroup of NT threads: counting sort of the
+// slots by expert, exclusive scans of the per-expert row and block counts,
+// the block table.  Slots with an expert id >= experts are left out (their
+// contribution is zero).  LDS (dynamic): cnt[E], off[E], boff[E+1].
+template <int NT>
+__device__ __forceinline__ void moe_plan_block(const MoePlanParams& p) {
+  extern __shared__ int lds[];
+  __shared__ int wsum[2][NT / 64];
   int* cnt = lds;
   int* off = lds + p.experts;
   int* boff = lds + 2 * p.experts;
   const int tid = threadIdx.x;
-  for (int i = tid; i < p.ncounters; i += 1024) p.counters[i] = 0u;
-  for (int e = tid; e < p.experts; e += 1024) cnt[e] = 0;
+  for (int i = tid; i < p.ncounters; i += NT) p.counters[i] = 0u;
+  for (int e = tid; e < p.experts; e += NT) cnt[e] = 0;
   __syncthreads();
-  for (int s = tid; s < p.slots; s += 1024) {
+  for (int s = tid; s < p.slots; s += NT) {
     const uint32_t e = p.selected[s];
     p.rank[s] = e < (uint32_t)p.experts ? atomicAdd(&cnt[e], 1) : -1;
   }
   __syncthreads();
   // exclusive scans of the counts and block counts: each thread sums a run of
-  // experts, the 1024 run totals are scanned (waves, then wave totals), and
+  // experts, the NT run totals are scanned (waves, then wave totals), and
   // each thread writes its run's offsets
-  __shared__ int wsum[2][16];
-  const int per = (p.experts + 1023) / 1024;
+  const int per = (p.experts + NT - 1) / NT;
   const int e0 = min(tid * per, p.experts), e1 = min(e0 + per, p.experts);
   int lc = 0, lb = 0;
   for (int e = e0; e < e1; ++e) {
@@ -98,17 +102,17 @@ __global__ __launch_bounds__(1024) void moe_plan_kernel(MoePlanParams p) {
     rc += cnt[e];
     rb += (cnt[e] + p.block_rows - 1) / p.block_rows;
   }
-  if (tid == 1023) {
+  if (tid == NT - 1) {
     boff[p.experts] = rb;
     p.counts[0] = rb;
     p.counts[1] = rc;
   }
   __syncthreads();
-  for (int s = tid; s < p.slots; s += 1024) {
+  for (int s = tid; s < p.slots; s += NT) {
     const int r = p.rank[s];
     if (r >= 0) p.sorted_slot[off[p.selected[s]] + r] = s;
   }
-  for (int e = tid; e < p.experts; e += 1024) {
+  for (int e = tid; e < p.experts; e += NT) {
     p.expert_count[e] = cnt[e];
     for (int b = boff[e]; b < boff[e + 1]; ++b) {
       const int first = off[e] + (b - boff[e]) * p.block_rows;
@@ -117,41 +121,59 @@ __global__ __launch_bounds__(1024) void moe_plan_kernel(MoePlanParams p) {
   }
 }
 
-// Gate/up inputs in sorted order: xgu[proj][pos][in] with proj 0 = gate,
-// 1 = up (routed_inputs, moe.rs:184-250).  One wave per (position,
-// projection, run of 8 128-blocks): the slot and expert lookups once per
-// wave, then 16 lanes per block (prologue8), each lane's two blocks loaded
-// together; positions past the routed count idle.  grid ceil(2 * slots *
-// ceil(in / 1024) / 4), 256 threads.
+struct MoeGatherParams {
+  const void* x;              // [rows][in] activations (f16, bf16 or f32)
+  int x_dtype, in, top_k, slots, experts;
+  const uint32_t* selected;   // [slots]
+  const uint16_t* gu_suh;     // [E][2][in]
+  uint16_t* xgu;              // [2][slots][in]
+};
+
+// Gate/up inputs in slot order: xgu[proj][slot][in] = f16(x[slot / top_k] *
+// gu_suh[e][proj]) -> staged Hadamard-128 (routed_inputs, moe.rs:184-250),
+// proj 0 = gate, 1 = up.  One wave per (slot, projection, run of 8
+// 128-blocks), 16 lanes per block (prologue8), each lane's two blocks loaded
+// together.  The activation loads need no routing data, so they go out before
+// the expert id arrives; slots routed to no valid expert are computed from
+// expert 0's scales and not stored (no block reads them).
 template <bool VEC>
-__global__ __launch_bounds__(256) void moe_gather_kernel(const void* __restrict__ x, int x_dtype,
-                                                         int in, int top_k,
-                                                         const uint32_t* selected,
-                                                         const int* sorted_slot,
-                                                         const int* routed, int slots_pad,
-                                                         const uint16_t* __restrict__ gu_suh,
-                                                         uint16_t* __restrict__ xgu) {
-  const int nb = in >> 7, runs = (nb + 7) >> 3;
-  const int job = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+__device__ __forceinline__ void moe_gather_wave(const MoeGatherParams& p, int job, int lane) {
+  const int nb = p.in >> 7, runs = (nb + 7) >> 3;
   const int pp = job / runs, run = job - pp * runs;
-  const int pos = pp >> 1, proj = pp & 1;
-  if (pos >= *routed) return;  // uniform per wave
-  const int slot = sorted_slot[pos];
-  const uint16_t* suh = gu_suh + ((size_t)selected[slot] * 2 + proj) * in;
-  const size_t xrow = (size_t)(slot / top_k) * in;
-  uint16_t* dst = xgu + ((size_t)proj * slots_pad + pos) * in;
-  const int lane = threadIdx.x & 63;
+  const int slot = pp >> 1, proj = pp & 1;
+  if (slot >= p.slots) return;  // uniform per wave
+  const size_t xrow = (size_t)(slot / p.top_k) * p.in;
   const int b0 = 8 * run + (lane >> 4), b1 = b0 + 4;
   const int bl = min(b1, nb - 1);  // clamped: the second block's lanes stay in bounds
   const int c0 = b0 * 128 + 8 * (lane & 15), c1 = bl * 128 + 8 * (lane & 15);
   // a group past the row's end (its last run holding fewer than 4 blocks)
-  // recomputes block nb - 1 without storing; both blocks' loads go out first
+  // recomputes block nb - 1 without storing
   const int c0c = b0 < nb ? c0 : (nb - 1) * 128 + 8 * (lane & 15);
   float a0[8], s0[8], a1[8], s1[8];
-  load8<VEC>(x, x_dtype, xrow + c0c, suh + c0c, a0, s0);
-  load8<VEC>(x, x_dtype, xrow + c1, suh + c1, a1, s1);
-  finish8<VEC>(a0, s0, dst + c0c, b0 < nb, lane);
-  finish8<VEC>(a1, s1, dst + c1, b1 < nb, lane);
+  load8_act<VEC>(p.x, p.x_dtype, xrow + c0c, a0);
+  load8_act<VEC>(p.x, p.x_dtype, xrow + c1, a1);
+  const uint32_t e = p.selected[slot];
+  const bool live = e < (uint32_t)p.experts;
+  const uint16_t* suh = p.gu_suh + ((size_t)(live ? e : 0u) * 2 + proj) * p.in;
+  load8_scale<VEC>(suh + c0c, s0);
+  load8_scale<VEC>(suh + c1, s1);
+  uint16_t* dst = p.xgu + ((size_t)proj * p.slots + slot) * p.in;
+  finish8<VEC>(a0, s0, dst + c0c, live && b0 < nb, lane);
+  finish8<VEC>(a1, s1, dst + c1, live && b1 < nb, lane);
+}
+
+// Launch 1 of the forward: workgroup 0 builds the route plan while the
+// others gather the gate/up inputs, which are stored by slot and so need
+// nothing from the plan.  grid 1 + ceil(2 * slots * ceil(in / 1024) / 4),
+// 256 threads, (3 * experts + 1) ints of dynamic LDS.
+template <bool VEC>
+__global__ __launch_bounds__(256) void moe_route_kernel(MoePlanParams pp, MoeGatherParams gp) {
+  if (blockIdx.x == 0) {
+    moe_plan_block<256>(pp);
+    return;
+  }
+  const int job = __builtin_amdgcn_readfirstlane((blockIdx.x - 1) * 4 + (threadIdx.x >> 6));
+  moe_gather_wave<VEC>(gp, job, threadIdx.x & 63);
 }
 
 struct MoeMmParams {
@@ -167,6 +189,8 @@ struct MoeMmParams {
   int splits;               // K-ranges per (block, column block)
   int slots_pad;            // position stride of xa / partials
   const uint16_t* xa;       // A rows [nproj][slots_pad][k_in] (f16, rotated)
+  const int* a_rows;        // A row of each sorted position (gate/up: its slot,
+                            // as the route launch stores them); null: the position
   float* partials;          // [splits][nproj][slots_pad][width] (splits > 1)
   uint32_t* counters;       // [blocks][col_blocks], cleared by the plan
   // gate/up epilogue
@@ -322,7 +346,8 @@ __global__ __launch_bounds__(256 * NPROJ) void moe_mm_kernel(MoeMmParams p) {
     lact[i] = c < kChunks && (c / 8) % kRows < 16 * groups;
     const int cc = lact[i] ? c : 0;
     const int pj = cc / (kRows * 8), row = (cc / 8) % kRows, ch = cc & 7;
-    lsrc[i] = p.xa + ((size_t)pj * p.slots_pad + pos0 + min(row, nrows - 1)) * p.k_in +
+    const int at = pos0 + min(row, nrows - 1);
+    lsrc[i] = p.xa + ((size_t)pj * p.slots_pad + (p.a_rows ? p.a_rows[at] : at)) * p.k_in +
               (size_t)qa * 64 + ch * 8;
     ldst[i] = (pj * kRows + row) * 128 + ((ch ^ a_swizzle(row)) << 4);
   }
@@ -389,10 +414,11 @@ __global__ __launch_bounds__(256 * NPROJ) void moe_mm_kernel(MoeMmParams p) {
       }
     }
   };
-  // steps 0..2 of A: step 0 into stage 0, steps 1 and 2 in registers
+  // steps 0..2 of A: step 0 into stage 0, steps 1 and 2 in registers; the
+  // first trellis set goes out first (its addresses need no A row lookup)
+  fetch(setA, 0);
   load_a(areg[0], 0);
   load_a(areg[1], 1);
-  fetch(setA, 0);
   store_a(areg[0], 0);
   load_a(areg[0], 2);
   __syncthreads();
@@ -540,23 +566,63 @@ __global__ __launch_bounds__(64) void finish_and_reduce_kernel(const float* __re
 
 // y[row][i] = sum_t z[row*top_k + t][i] in t order with f32 adds (z f16 for
 // f16 scores, f32 otherwise), stored as f16 or f32 the same way; slots routed
-// to no valid expert contribute zero.  grid (rows, ceil(width/256)).
+// to no valid expert contribute zero.  Each thread owns 8 consecutive columns
+// and issues the loads of 8 slots together (those of invalid slots, in bounds
+// of z, are dropped), so a row costs one load latency per 8 slots.  VEC: y is
+// 16-byte aligned.  grid (rows, ceil(width / 2048)), 256 threads.
+template <bool VEC>
 __global__ __launch_bounds__(256) void moe_reduce_kernel(const void* __restrict__ z,
                                                          int scores_dtype,
                                                          const uint32_t* __restrict__ selected,
                                                          int experts, int top_k, int width,
                                                          void* __restrict__ y) {
-  const int i = blockIdx.y * 256 + threadIdx.x, row = blockIdx.x;
+  const int i = (blockIdx.y * 256 + threadIdx.x) * 8, row = blockIdx.x;
   if (i >= width) return;
-  float acc = 0.f;
-  for (int t = 0; t < top_k; ++t) {
-    const int slot = row * top_k + t;
-    if (selected[slot] < (uint32_t)experts) {
-      const size_t at = (size_t)slot * width + i;
-      acc += scores_dtype == DT_F16 ? h2f(((const uint16_t*)z)[at]) : ((const float*)z)[at];
+  const bool f16 = scores_dtype == DT_F16;
+  float acc[8] = {};
+  for (int t0 = 0; t0 < top_k; t0 += 8) {
+    float v[8][8];
+    bool ok[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int t = min(t0 + c, top_k - 1);
+      const size_t slot = (size_t)row * top_k + t;
+      ok[c] = t0 + c < top_k && selected[slot] < (uint32_t)experts;
+      const size_t at = slot * width + i;
+      if (f16) {
+        const u32x4 w = *(const u32x4*)((const uint16_t*)z + at);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          v[c][2 * k] = h2f((uint16_t)w[k]);
+          v[c][2 * k + 1] = h2f((uint16_t)(w[k] >> 16));
+        }
+      } else {
+        const float4v w0 = *(const float4v*)((const float*)z + at);
+        const float4v w1 = *(const float4v*)((const float*)z + at + 4);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[c][k] = w0[k], v[c][k + 4] = w1[k];
+      }
     }
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+      if (ok[c])
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[k] += v[c][k];
   }
-  store_reduced(y, scores_dtype, (size_t)row * width + i, acc);
+  const size_t o = (size_t)row * width + i;
+  if (!VEC) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) store_reduced(y, scores_dtype, o + k, acc[k]);
+  } else if (f16) {
+    u32x4 w;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      w[k] = (uint32_t)f2h(acc[2 * k]) | ((uint32_t)f2h(acc[2 * k + 1]) << 16);
+    *(u32x4*)((uint16_t*)y + o) = w;
+  } else {
+    *(float4v*)((float*)y + o) = float4v{acc[0], acc[1], acc[2], acc[3]};
+    *(float4v*)((float*)y + o + 4) = float4v{acc[4], acc[5], acc[6], acc[7]};
+  }
 }
 
 }  // namespace exl3

@@ -271,11 +271,10 @@ __device__ __forceinline__ void finish8(const float (&a)[8], const float (&sv)[8
   }
 }
 
-// The inputs of prologue8: a[i] = x[xe + i] (f16, bf16 or f32) and
-// sv[i] = sp[i] (f16), with 16-byte loads under VEC.
+// The activation inputs of prologue8: a[i] = x[xe + i] (f16, bf16 or f32),
+// with 16-byte loads under VEC.
 template <bool VEC>
-__device__ __forceinline__ void load8(const void* x, int x_dtype, size_t xe, const uint16_t* sp,
-                                      float (&a)[8], float (&sv)[8]) {
+__device__ __forceinline__ void load8_act(const void* x, int x_dtype, size_t xe, float (&a)[8]) {
   if constexpr (VEC) {
     if (x_dtype == DT_F32) {
       const float4v* xp = (const float4v*)((const float*)x + xe);
@@ -293,6 +292,18 @@ __device__ __forceinline__ void load8(const void* x, int x_dtype, size_t xe, con
         a[2 * i + 1] = raw_act(xw[i] >> 16, x_dtype);
       }
     }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      a[i] = x_dtype == DT_F32 ? ((const float*)x)[xe + i]
+                               : raw_act(((const uint16_t*)x)[xe + i], x_dtype);
+  }
+}
+
+// The scale inputs of prologue8: sv[i] = sp[i] (f16).
+template <bool VEC>
+__device__ __forceinline__ void load8_scale(const uint16_t* sp, float (&sv)[8]) {
+  if constexpr (VEC) {
     const u32x4 sw = *(const u32x4*)sp;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -301,12 +312,15 @@ __device__ __forceinline__ void load8(const void* x, int x_dtype, size_t xe, con
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      a[i] = x_dtype == DT_F32 ? ((const float*)x)[xe + i]
-                               : raw_act(((const uint16_t*)x)[xe + i], x_dtype);
-      sv[i] = h2f(sp[i]);
-    }
+    for (int i = 0; i < 8; ++i) sv[i] = h2f(sp[i]);
   }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void load8(const void* x, int x_dtype, size_t xe, const uint16_t* sp,
+                                      float (&a)[8], float (&sv)[8]) {
+  load8_act<VEC>(x, x_dtype, xe, a);
+  load8_scale<VEC>(sp, sv);
 }
 
 // f16(H128(f16(f16(x) * suh)) / sqrt(128)) of one 128-input block, held as

@@ -293,20 +293,30 @@ __device__ __forceinline__ void moe_finish_row(const MoeMmParams& p, int e, int 
 // Grouped expert QMM over one block of up to 16*MB rows, one 128-column block
 // and one K-range.  NPROJ = 2 (gate/up, GLU epilogue) or 1 (down).  Wave w
 // serves projection w / 4 and the column pair w % 4 with the QMV's loop: D
-// trellis slices and the matching A fragments of every row group in flight
-// per set, two sets in ping-pong, unconditional (clamped) loads.  Each decoded
-// step feeds the block's ceil(rows/16) row groups.
+// trellis slices in flight per set, two sets in ping-pong, unconditional
+// (clamped) loads.  Each decoded step feeds the block's ceil(rows/16) row
+// groups.  The register budget asks for 4 waves per SIMD (two gate/up
+// workgroups per CU) where that needs no spill; the MUL1 decode (CB = 2) and the
+// 64-row blocks get 3 and 2.
 template <int K, int CB, int NPROJ, int MB>
-__global__ __launch_bounds__(256 * NPROJ) void moe_mm_kernel(MoeMmParams p) {
-  // A rows of the block pass through LDS, three steps deep: [stage][proj][row]
-  // [8 chunks of 16 bytes], chunk c of row r at slot c ^ a_swizzle(r) so that both
-  // the row-wise stores and the 16-row fragment reads are conflict-free.
-  constexpr int kRows = 16 * MB, kStage = NPROJ * kRows * 128;
-  __shared__ __attribute__((aligned(16))) uint8_t as[3][kStage];
-  __shared__ float red[NPROJ][16][128];  // f32 sums of one row group (one K-range)
+__global__ __launch_bounds__(256 * NPROJ)
+__attribute__((amdgpu_waves_per_eu(MB == 4 ? 2 : CB == 2 ? 3 : 4))) void moe_mm_kernel(
+    MoeMmParams p) {
+  // A rows of the block pass through LDS in chunks of C = D steps, two chunks
+  // deep: [buffer][step][proj][row][8 chunks of 16 bytes], chunk c of row r at
+  // slot c ^ a_swizzle(r) so that the 16-row fragment reads are conflict-free.
+  // The rows go global -> LDS directly (global_load_lds_dwordx4: lane l of a
+  // load fills bytes 16l..16l+15 of its 1 KB region, 8 rows of one
+  // projection, the swizzle applied to the global address), one barrier per
+  // chunk.  After the loop the same bytes hold the row-group sums.
+  constexpr int D = kQmvDepth<K>, C = D;
+  constexpr int kRows = 16 * MB, kStep = NPROJ * kRows * 128, kBuf = C * kStep;
+  constexpr int kRed = NPROJ * 16 * 128 * 4;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kBuf > kRed ? 2 * kBuf : kRed];
+  float(*red)[16][128] = (float(*)[16][128])lds;  // f32 sums of one row group (one K-range)
   __shared__ int s_last;
   constexpr bool GLU = NPROJ == 2;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int proj = wave >> 2, pair = wave & 3;
   // Workgroup -> (block, column block, split).  Workgroups go to the 8 XCDs
   // round-robin (XCD = id % 8); XCD x takes blocks x, x + 8, x + 16, ...
@@ -332,36 +342,41 @@ __global__ __launch_bounds__(256 * NPROJ) void moe_mm_kernel(MoeMmParams p) {
   const uint32_t* tp =
       p.trellis + ((size_t)(4 * qa + g) * p.tn_total + tcol) * (8 * K) + (size_t)j * K;
   const int prev_off = j == 0 ? 8 * K - 1 : -1;
-  // A loader: each thread moves kPer 16-byte chunks of a step.  Only the
-  // block's row groups are moved (rows past the block's end inside its last
-  // group repeat its last row; their sums are never used).
-  constexpr int kThreads = 256 * NPROJ, kChunks = NPROJ * kRows * 8;
-  constexpr int kPer = (kChunks + kThreads - 1) / kThreads;
-  const uint16_t* lsrc[kPer];
-  int ldst[kPer];
-  bool lact[kPer];
+  // A loads: a step is NI = NPROJ * kRows / 8 loads of 8 rows, load i covering
+  // projection i / (kRows / 8) and rows 8 * (i % (kRows / 8)) + 0..7; wave w
+  // issues loads w, w + 4 * NPROJ, ...  A load whose rows lie past the
+  // block's row groups is skipped; rows past the block's end inside its last
+  // group repeat its last row (their sums are never used).
+  constexpr int NW = 4 * NPROJ, NI = NPROJ * kRows / 8, kPerW = (NI + NW - 1) / NW;
+  const uint16_t* asrc[kPerW];
+  int adst[kPerW];
+  bool aact[kPerW];
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int c = threadIdx.x + i * kThreads;
-    lact[i] = c < kChunks && (c / 8) % kRows < 16 * groups;
-    const int cc = lact[i] ? c : 0;
-    const int pj = cc / (kRows * 8), row = (cc / 8) % kRows, ch = cc & 7;
+  for (int i = 0; i < kPerW; ++i) {
+    const int li = wave + i * NW;
+    const int pj = li / (kRows / 8), row = 8 * (li % (kRows / 8)) + (lane >> 3);
+    aact[i] = li < NI && (8 * (li % (kRows / 8))) / 16 < groups;  // uniform per wave
     const int at = pos0 + min(row, nrows - 1);
-    lsrc[i] = p.xa + ((size_t)pj * p.slots_pad + (p.a_rows ? p.a_rows[at] : at)) * p.k_in +
-              (size_t)qa * 64 + ch * 8;
-    ldst[i] = (pj * kRows + row) * 128 + ((ch ^ a_swizzle(row)) << 4);
+    const int arow = p.a_rows ? p.a_rows[at] : at;
+    asrc[i] = p.xa + ((size_t)(li < NI ? pj : 0) * p.slots_pad + arow) * p.k_in +
+              (size_t)qa * 64 + (((lane & 7) ^ a_swizzle(row)) << 3);
+    adst[i] = (pj * kRows + 8 * (li % (kRows / 8))) * 128;
   }
   const int qlast = nq - 1;
-  u32x4 areg[2][kPer];
-  auto load_a = [&](u32x4(&dst)[kPer], int q) {
+  // chunk ch of A into buffer b (steps past the range re-read the last one
+  // into slots no one reads, so every wave issues the same loads per chunk)
+  auto load_chunk = [&](int ch, int b) {
 #pragma unroll
-    for (int i = 0; i < kPer; ++i)
-      if (lact[i]) dst[i] = *(const u32x4*)(lsrc[i] + (size_t)min(q, qlast) * 64);
-  };
-  auto store_a = [&](const u32x4(&src)[kPer], int st) {
+    for (int d = 0; d < C; ++d) {
+      const size_t qoff = (size_t)min(ch * C + d, qlast) * 64;
 #pragma unroll
-    for (int i = 0; i < kPer; ++i)
-      if (lact[i]) *(u32x4*)(&as[st][0] + ldst[i]) = src[i];
+      for (int i = 0; i < kPerW; ++i)
+        if (aact[i])
+          __builtin_amdgcn_global_load_lds(
+              (const void*)(asrc[i] + qoff),
+              (__attribute__((address_space(3))) void*)(lds + b * kBuf + d * kStep + adst[i]),
+              16, 0, 0);
+    }
   };
   // fragment (mb, h) of this lane: row 16mb + am of the wave's projection, chunk 2g + h
   int aoff[MB][2];
@@ -373,7 +388,6 @@ __global__ __launch_bounds__(256 * NPROJ) void moe_mm_kernel(MoeMmParams p) {
       aoff[mb][h] = (proj * kRows + row) * 128 + (((2 * g + h) ^ a_swizzle(row)) << 4);
     }
 
-  constexpr int D = kQmvDepth<K>;
   uint32_t setA[D][K + 1], setB[D][K + 1];
   auto fetch = [&](uint32_t(&set)[D][K + 1], int qbase) {
 #pragma unroll
@@ -383,23 +397,25 @@ __global__ __launch_bounds__(256 * NPROJ) void moe_mm_kernel(MoeMmParams p) {
   float4v acc0[MB], acc1[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc0[mb] = acc1[mb] = float4v{0.f, 0.f, 0.f, 0.f};
-  // step q: A of step q+1 (loaded two steps earlier) goes to stage (q+1) % 3,
-  // step q+3 is loaded in its place, step q is multiplied from stage q % 3;
-  // one barrier per step orders the stages
-  auto compute = [&](uint32_t(&set)[D][K + 1], int qbase) {
+  // chunk ch (buffer ch & 1, trellis set `cur`): chunk ch + 1's A and trellis
+  // go out first, into the other buffer and set; then its C steps are
+  // multiplied; the wait and barrier at its end publish chunk ch + 1 and free
+  // buffer ch & 1 for chunk ch + 2
+  const int nch = (nq + C - 1) / C;
+  auto chunk = [&](uint32_t(&cur)[D][K + 1], uint32_t(&nxt)[D][K + 1], int ch, int b) {
+    if (ch + 1 < nch) load_chunk(ch + 1, b ^ 1);  // uniform
+    fetch(nxt, (ch + 1) * C);
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const int q = qbase + d;
+    for (int d = 0; d < C; ++d) {
+      const int q = ch * C + d;
       if (q < nq) {  // uniform
-        store_a(areg[(q + 1) & 1], (q + 1) % 3);
-        load_a(areg[(q + 1) & 1], q + 3);
         uint32_t src[32];
-        extract_states<K>(set[d], src);
+        extract_states<K>(cur[d], src);
         const half8 b00 = decode_fragment<CB, K, 0, 0>(src);
         const half8 b01 = decode_fragment<CB, K, 0, 1>(src);
         const half8 b10 = decode_fragment<CB, K, 1, 0>(src);
         const half8 b11 = decode_fragment<CB, K, 1, 1>(src);
-        const uint8_t* st = &as[q % 3][0];
+        const uint8_t* st = lds + b * kBuf + d * kStep;
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
           if (mb < groups) {
@@ -410,23 +426,20 @@ __global__ __launch_bounds__(256 * NPROJ) void moe_mm_kernel(MoeMmParams p) {
             acc0[mb] = mfma16(a1, b10, acc0[mb]);
             acc1[mb] = mfma16(a1, b11, acc1[mb]);
           }
-        __syncthreads();
       }
+      // steps stay in order (no decode hoisted across steps: register pressure)
+      __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of chunk ch + 1 have landed
+    __syncthreads();
   };
-  // steps 0..2 of A: step 0 into stage 0, steps 1 and 2 in registers; the
-  // first trellis set goes out first (its addresses need no A row lookup)
+  load_chunk(0, 0);
   fetch(setA, 0);
-  load_a(areg[0], 0);
-  load_a(areg[1], 1);
-  store_a(areg[0], 0);
-  load_a(areg[0], 2);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  for (int q0 = 0; q0 < nq; q0 += 2 * D) {
-    fetch(setB, q0 + D);
-    compute(setA, q0);
-    fetch(setA, q0 + 2 * D);
-    compute(setB, q0 + D);
+  for (int ch = 0; ch < nch; ch += 2) {
+    chunk(setA, setB, ch, 0);
+    if (ch + 1 < nch) chunk(setB, setA, ch + 1, 1);  // uniform
   }
 
   // accumulator lane l: rows 4*(l/16)+r, column 32*pair + 16*(n/8) + n%8 + 8*cg

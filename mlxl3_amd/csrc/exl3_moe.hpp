@@ -312,8 +312,11 @@ __attribute__((amdgpu_waves_per_eu(MB == 4 ? 2 : CB == 2 ? 3 : 4))) void moe_mm_
   constexpr int D = kQmvDepth<K>, C = D;
   constexpr int kRows = 16 * MB, kStep = NPROJ * kRows * 128, kBuf = C * kStep;
   constexpr int kRed = NPROJ * 16 * 128 * 4;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kBuf > kRed ? 2 * kBuf : kRed];
-  float(*red)[16][128] = (float(*)[16][128])lds;  // f32 sums of one row group (one K-range)
+  // two separate objects, so that the compiler sees the loads into one buffer
+  // cannot alias the fragment reads of the other (no wait before those reads)
+  __shared__ __attribute__((aligned(16))) uint8_t abuf0[kBuf > kRed ? kBuf : kRed];
+  __shared__ __attribute__((aligned(16))) uint8_t abuf1[kBuf];
+  float(*red)[16][128] = (float(*)[16][128])abuf0;  // f32 sums of one row group (one K-range)
   __shared__ int s_last;
   constexpr bool GLU = NPROJ == 2;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -374,7 +377,7 @@ __attribute__((amdgpu_waves_per_eu(MB == 4 ? 2 : CB == 2 ? 3 : 4))) void moe_mm_
         if (aact[i])
           __builtin_amdgcn_global_load_lds(
               (const void*)(asrc[i] + qoff),
-              (__attribute__((address_space(3))) void*)(lds + b * kBuf + d * kStep + adst[i]),
+              (__attribute__((address_space(3))) void*)((b ? abuf1 : abuf0) + d * kStep + adst[i]),
               16, 0, 0);
     }
   };
@@ -415,7 +418,7 @@ __attribute__((amdgpu_waves_per_eu(MB == 4 ? 2 : CB == 2 ? 3 : 4))) void moe_mm_
         const half8 b01 = decode_fragment<CB, K, 0, 1>(src);
         const half8 b10 = decode_fragment<CB, K, 1, 0>(src);
         const half8 b11 = decode_fragment<CB, K, 1, 1>(src);
-        const uint8_t* st = lds + b * kBuf + d * kStep;
+        const uint8_t* st = (b ? abuf1 : abuf0) + d * kStep;
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
           if (mb < groups) {

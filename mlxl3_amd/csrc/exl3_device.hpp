@@ -348,4 +348,28 @@ __device__ __forceinline__ void h128_wave(float& v0, float& v1, int lane) {
 // conflict that halved the read rate, 128 vs 256 B/clk measured).
 __device__ __forceinline__ int a_swizzle(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector memory
+// instructions of the wave are outstanding and leaves the other counters free.
+constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Byte offset of an LDS location in the workgroup's allocation.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// global_load_lds_dwordx4 as inline assembly: lane l copies the 16 bytes at
+// its global address g into LDS bytes lds + 16l .. lds + 16l + 15 (lds
+// wave-uniform; the s_nop covers the M0 write -> LDS-DMA hazard).  The
+// compiler does not see this LDS write, so it adds no waits of its own for it
+// (it cannot tell the destination from other LDS accesses and would wait for
+// every outstanding load before them): the caller waits with s_waitcnt vmcnt
+// before the barrier that publishes the bytes.  "memory" keeps other memory
+// accesses from moving across the issue.
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(g), "s"(lds)
+               : "memory", "m0");
+}
+
 }  // namespace exl3

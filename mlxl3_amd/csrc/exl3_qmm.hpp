@@ -192,16 +192,19 @@ __device__ __forceinline__ void qmm_produce(const uint32_t (&B)[K + 1], u32x4* d
 template <int K, int CB, int MB>
 __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
   // LDS: three stages of B fragments (16 KB each) and of A rows (64*MB rows x
-  // 128 bytes each); after the K loop the same bytes hold the tile's f16 rows.
+  // 128 bytes each), as two objects so that the compiler can tell the A
+  // stages' direct loads from the B stores (no wait for the loads before
+  // those); after the K loop the A bytes hold the tile's f16 rows.
   constexpr int kBStage = 16384, kAStage = 64 * MB * 128;
-  constexpr int kLoop = 3 * (kBStage + kAStage), kY = 64 * MB * kYStride * 2;
-  constexpr int kLdsBytes = kLoop > kY ? kLoop : kY;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
-  uint16_t* ys = (uint16_t*)lds;  // [64*MB][kYStride] after the loop
+  constexpr int kY = 64 * MB * kYStride * 2;
+  constexpr int kABytes = 3 * kAStage > kY ? 3 * kAStage : kY;
+  __shared__ __attribute__((aligned(16))) uint8_t bls[3 * kBStage];
+  __shared__ __attribute__((aligned(16))) uint8_t als[kABytes];
+  uint16_t* ys = (uint16_t*)als;  // [64*MB][kYStride] after the loop
   __shared__ float s_svh[128], s_bias[128];
   __shared__ int s_last;
-  auto bstage = [&](int st) { return (u32x4*)(lds + st * kBStage); };  // [producer][frag][lane]
-  auto astage = [&](int st) { return lds + 3 * kBStage + st * kAStage; };
+  auto bstage = [&](int st) { return (u32x4*)(bls + st * kBStage); };  // [producer][frag][lane]
+  auto astage = [&](int st) { return als + st * kAStage; };
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int role = wave & 3;
@@ -261,22 +264,42 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
 #pragma unroll
     for (int d = 0; d < PD; ++d)
       load_slice_prev<K>(tp + (size_t)min(d, qlast) * qstride, prev_off, sl[d]);
-    // A: row 8i + (lane >> 3) of the consumer's 16*MB rows, chunk lane & 7
+    // A: row 8i + (lane >> 3) of the consumer's 16*MB rows; the lane's slot is
+    // lane & 7.  K = 4 and 8 (trellis slices of a known 2 and 3 load
+    // instructions) at MB >= 2 copy A global -> LDS directly (lds_dma16: lane l
+    // of a load fills bytes 16l..16l+15 of its 1 KB region, 8 rows; the swizzle
+    // goes to the global side: slot s of row r reads chunk s ^ a_swizzle(r)),
+    // issued when the stage frees and waited for before the iteration's barrier
+    // with the slice issued after it still in flight (same-box A/B, 4096 ->
+    // 14336: M=512 87.1 -> 84.7 us, M=256 57.7 -> 56.3, M=2048 324.6 -> 316);
+    // other K, and MB = 1 (an iteration too short to cover the L2 latency of a
+    // copy issued at its start: 45.9 -> 46.7 us at M=128), go through registers
+    // two steps ahead.
+    constexpr bool kDma = (K == 4 || K == 8) && MB >= 2;
+    constexpr int kSliceLoads = K == 4 ? 2 : 3;  // VMEM instructions of load_slice_prev<K>
     const int ar = lane >> 3, ac = lane & 7;
     const uint16_t* ap[2 * MB];
 #pragma unroll
     for (int i = 0; i < 2 * MB; ++i) {
       const int row = row_base + 8 * i + ar;
-      ap[i] = mm.xhat + (size_t)(row < p.M ? row : 0) * p.in + (size_t)qa * 64 + ac * 8;
+      const int chunk = kDma ? ac ^ a_swizzle(8 * i + ar) : ac;
+      ap[i] = mm.xhat + (size_t)(row < p.M ? row : 0) * p.in + (size_t)qa * 64 + chunk * 8;
     }
+    auto dma_a = [&](int step, int st) {
+      const uint32_t base = __builtin_amdgcn_readfirstlane(
+          lds_offset(astage(st) + role * (16 * MB * 128)));
+#pragma unroll
+      for (int i = 0; i < 2 * MB; ++i)
+        lds_dma16(ap[i] + (size_t)min(step, qlast) * 64, base + i * 1024);
+    };
     // A rows of steps q+2 and q+3 in flight (register sets alternate by step)
-    u32x4 areg[2][2 * MB];
-    auto load_a = [&](u32x4(&dst)[2 * MB], int step) {
+    u32x4 areg[2][kDma ? 1 : 2 * MB];
+    auto load_a = [&](auto& dst, int step) {
 #pragma unroll
       for (int i = 0; i < 2 * MB; ++i)
         dst[i] = *(const u32x4*)(ap[i] + (size_t)min(step, qlast) * 64);
     };
-    auto store_a = [&](const u32x4(&src)[2 * MB], int st) {
+    auto store_a = [&](const auto& src, int st) {
       uint8_t* base = astage(st) + role * (16 * MB * 128);
 #pragma unroll
       for (int i = 0; i < 2 * MB; ++i) {
@@ -285,16 +308,29 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
       }
     };
     // steps 0 and 1
-    load_a(areg[0], 0);
-    load_a(areg[1], 1);
-    qmm_produce<K, CB>(sl[0], bstage(0) + role * 256, lane);
-    load_slice_prev<K>(tp + (size_t)min(PD, qlast) * qstride, prev_off, sl[0]);
-    qmm_produce<K, CB>(sl[1], bstage(1) + role * 256, lane);
-    load_slice_prev<K>(tp + (size_t)min(PD + 1, qlast) * qstride, prev_off, sl[1]);
-    store_a(areg[0], 0);
-    load_a(areg[0], 2);
-    store_a(areg[1], 1);
-    load_a(areg[1], 3);
+    if constexpr (kDma) {
+      dma_a(0, 0);
+      dma_a(1, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      qmm_produce<K, CB>(sl[0], bstage(0) + role * 256, lane);
+      qmm_produce<K, CB>(sl[1], bstage(1) + role * 256, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      load_slice_prev<K>(tp + (size_t)min(PD, qlast) * qstride, prev_off, sl[0]);
+      load_slice_prev<K>(tp + (size_t)min(PD + 1, qlast) * qstride, prev_off, sl[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * kSliceLoads));
+    } else {
+      load_a(areg[0], 0);
+      load_a(areg[1], 1);
+      qmm_produce<K, CB>(sl[0], bstage(0) + role * 256, lane);
+      load_slice_prev<K>(tp + (size_t)min(PD, qlast) * qstride, prev_off, sl[0]);
+      qmm_produce<K, CB>(sl[1], bstage(1) + role * 256, lane);
+      load_slice_prev<K>(tp + (size_t)min(PD + 1, qlast) * qstride, prev_off, sl[1]);
+      store_a(areg[0], 0);
+      load_a(areg[0], 2);
+      store_a(areg[1], 1);
+      load_a(areg[1], 3);
+    }
     __syncthreads();
     // iteration q (slot (q+2) % 4 and A set q % 2 hold step q+2):
     // unconditional, so the load count per iteration is static (past-the-end
@@ -302,11 +338,23 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
     auto iter = [&](int q, auto phase) {
       constexpr int P = decltype(phase)::value;
       const int st = (q + 2) % 3;
-      qmm_produce<K, CB>(sl[(P + 2) % PD], bstage(st) + role * 256, lane);
-      load_slice_prev<K>(tp + (size_t)min(q + 2 + PD, qlast) * qstride, prev_off,
-                         sl[(P + 2) % PD]);
-      store_a(areg[P & 1], st);
-      load_a(areg[P & 1], q + 4);
+      if constexpr (kDma) {
+        // stage st (step q-1) was released by the last barrier
+        dma_a(q + 2, st);
+        __builtin_amdgcn_sched_barrier(0);
+        qmm_produce<K, CB>(sl[(P + 2) % PD], bstage(st) + role * 256, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        load_slice_prev<K>(tp + (size_t)min(q + 2 + PD, qlast) * qstride, prev_off,
+                           sl[(P + 2) % PD]);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(kSliceLoads));  // A of step q+2 has landed
+      } else {
+        qmm_produce<K, CB>(sl[(P + 2) % PD], bstage(st) + role * 256, lane);
+        load_slice_prev<K>(tp + (size_t)min(q + 2 + PD, qlast) * qstride, prev_off,
+                           sl[(P + 2) % PD]);
+        store_a(areg[P & 1], st);
+        load_a(areg[P & 1], q + 4);
+      }
       __syncthreads();
     };
     const int nq4 = nq & ~3;

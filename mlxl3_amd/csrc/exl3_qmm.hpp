@@ -177,6 +177,39 @@ __device__ __forceinline__ void qmm_finish_chunk(const u32x4 raw, const float (&
   *(u32x4*)((uint16_t*)mm.y + yoff) = o;
 }
 
+// load_slice_prev<K> with a fixed count of load instructions, 2 for K <= 4
+// and 3 above (the previous lane's word, then the lane's K words as 1-4 word
+// loads at 4-byte alignment), which the producers' direct A copies wait
+// around.
+typedef uint32_t u32x2a __attribute__((ext_vector_type(2), aligned(4)));
+typedef uint32_t u32x3a __attribute__((ext_vector_type(3), aligned(4)));
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
+template <int N>
+__device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
+  if constexpr (N == 1) {
+    w[0] = __builtin_nontemporal_load(p);
+  } else if constexpr (N == 2) {
+    const u32x2a v = __builtin_nontemporal_load((const u32x2a*)p);
+    w[0] = v[0], w[1] = v[1];
+  } else if constexpr (N == 3) {
+    const u32x3a v = __builtin_nontemporal_load((const u32x3a*)p);
+    w[0] = v[0], w[1] = v[1], w[2] = v[2];
+  } else {
+    static_assert(N == 4, "1-4 words");
+    const u32x4a v = __builtin_nontemporal_load((const u32x4a*)p);
+    w[0] = v[0], w[1] = v[1], w[2] = v[2], w[3] = v[3];
+  }
+}
+template <int K>
+constexpr int kSliceLoads = K <= 4 ? 2 : 3;
+template <int K>
+__device__ __forceinline__ void load_slice_counted(const uint32_t* __restrict__ p, int prev_off,
+                                                   uint32_t (&w)[K + 1]) {
+  w[0] = __builtin_nontemporal_load(p + prev_off);
+  load_words<(K < 4 ? K : 4)>(p, w + 1);
+  if constexpr (K > 4) load_words<K - 4>(p + 4, w + 5);
+}
+
 // Decode one step's 8 tiles of a producer (B[0] = previous lane's last word,
 // B[1..K] own words) into its 4 fragments in LDS.
 template <int K, int CB>
@@ -265,18 +298,17 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
     for (int d = 0; d < PD; ++d)
       load_slice_prev<K>(tp + (size_t)min(d, qlast) * qstride, prev_off, sl[d]);
     // A: row 8i + (lane >> 3) of the consumer's 16*MB rows; the lane's slot is
-    // lane & 7.  K = 4 and 8 (trellis slices of a known 2 and 3 load
-    // instructions) at MB >= 2 copy A global -> LDS directly (lds_dma16: lane l
+    // lane & 7.  At MB >= 2 (trellis slices loaded with a known count of
+    // instructions, load_slice_counted) A goes global -> LDS directly (lds_dma16: lane l
     // of a load fills bytes 16l..16l+15 of its 1 KB region, 8 rows; the swizzle
     // goes to the global side: slot s of row r reads chunk s ^ a_swizzle(r)),
     // issued when the stage frees and waited for before the iteration's barrier
     // with the slice issued after it still in flight (same-box A/B, 4096 ->
     // 14336: M=512 87.1 -> 84.7 us, M=256 57.7 -> 56.3, M=2048 324.6 -> 316);
-    // other K, and MB = 1 (an iteration too short to cover the L2 latency of a
-    // copy issued at its start: 45.9 -> 46.7 us at M=128), go through registers
-    // two steps ahead.
-    constexpr bool kDma = (K == 4 || K == 8) && MB >= 2;
-    constexpr int kSliceLoads = K == 4 ? 2 : 3;  // VMEM instructions of load_slice_prev<K>
+    // MB = 1 (an iteration too short to cover the L2 latency of a copy issued at
+    // its start: 45.9 -> 46.7 us at M=128) goes through registers two steps
+    // ahead.
+    constexpr bool kDma = MB >= 2;
     const int ar = lane >> 3, ac = lane & 7;
     const uint16_t* ap[2 * MB];
 #pragma unroll
@@ -315,10 +347,10 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
       qmm_produce<K, CB>(sl[0], bstage(0) + role * 256, lane);
       qmm_produce<K, CB>(sl[1], bstage(1) + role * 256, lane);
       __builtin_amdgcn_sched_barrier(0);
-      load_slice_prev<K>(tp + (size_t)min(PD, qlast) * qstride, prev_off, sl[0]);
-      load_slice_prev<K>(tp + (size_t)min(PD + 1, qlast) * qstride, prev_off, sl[1]);
+      load_slice_counted<K>(tp + (size_t)min(PD, qlast) * qstride, prev_off, sl[0]);
+      load_slice_counted<K>(tp + (size_t)min(PD + 1, qlast) * qstride, prev_off, sl[1]);
       __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * kSliceLoads));
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * kSliceLoads<K>));
     } else {
       load_a(areg[0], 0);
       load_a(areg[1], 1);
@@ -344,10 +376,10 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
         __builtin_amdgcn_sched_barrier(0);
         qmm_produce<K, CB>(sl[(P + 2) % PD], bstage(st) + role * 256, lane);
         __builtin_amdgcn_sched_barrier(0);
-        load_slice_prev<K>(tp + (size_t)min(q + 2 + PD, qlast) * qstride, prev_off,
-                           sl[(P + 2) % PD]);
+        load_slice_counted<K>(tp + (size_t)min(q + 2 + PD, qlast) * qstride, prev_off,
+                              sl[(P + 2) % PD]);
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(vmcnt_only(kSliceLoads));  // A of step q+2 has landed
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(kSliceLoads<K>));  // A of step q+2 has landed
       } else {
         qmm_produce<K, CB>(sl[(P + 2) % PD], bstage(st) + role * 256, lane);
         load_slice_prev<K>(tp + (size_t)min(q + 2 + PD, qlast) * qstride, prev_off,

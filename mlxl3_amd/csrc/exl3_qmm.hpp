@@ -281,12 +281,9 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
       s_svh[threadIdx.x] = h2f(mm.svh[cblk_l * 128 + threadIdx.x]);
       s_bias[threadIdx.x] = mm.bias ? h2f(mm.bias[cblk_l * 128 + threadIdx.x]) : 0.f;
     }
-    // trellis slices in flight: 4 steps ahead, except the MB = 2 variants
-    // whose allocation spills at the 256 VGPRs two waves per SIMD leave (K = 8
-    // 3INST/MCG, K = 4 MCG): 2 steps there, which is faster than the spill
-    // (134 vs 138 us, K = 8 at 14336 -> 4096, M = 512) but slower than 4
-    // where nothing spills (127 vs 121 us, K = 4 3INST)
-    constexpr int PD = MB == 2 && (K == 8 ? CB != 2 : K == 4 && CB == 1) ? 2 : 4;
+    // trellis slices in flight: 4 steps ahead (with A copied straight to LDS
+    // at MB >= 2 no variant spills at this depth)
+    constexpr int PD = 4;
     const int hsel = (lane >> 3) & 1, j = lane & 7;
     const size_t qstride = (size_t)4 * TN * 8 * K;
     const uint32_t* tp = mm.trellis +

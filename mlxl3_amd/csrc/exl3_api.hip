@@ -221,6 +221,13 @@ static QmmShape choose_qmm_shape(int in, int out, int64_t rows) {
   return best;
 }
 
+// Split-K partials of a QMM launch: per split and output tile, the f32
+// accumulators of its 64*MB rows x 128 columns in fragment order.
+static size_t qmm_partial_bytes(const QmmShape& sh, int out) {
+  if (sh.splits <= 1) return 0;
+  return sizeof(float) * (size_t)sh.splits * sh.mtiles * (out / 128) * 64 * sh.mb * 128;
+}
+
 // Workspace: the first kWorkspaceCounterBytes hold split-K counters that are
 // zero between calls (every call leaves them zero, so one workspace serves
 // every entry point in any order).  The rest is per-call scratch: QMV
@@ -288,7 +295,7 @@ static size_t group_scratch_bytes(const Group& g, int64_t rows) {
     return xhat + align_up(sizeof(float) * (size_t)splits * rows * g.total_out);
   }
   const QmmShape sh = choose_qmm_shape(g.in, g.total_out, rows);
-  size_t partials = sh.splits > 1 ? sizeof(float) * (size_t)sh.splits * rows * g.total_out : 0;
+  const size_t partials = qmm_partial_bytes(sh, g.total_out);
   return (size_t)g.count * align_up(sizeof(uint16_t) * (size_t)rows * g.in) + align_up(partials);
 }
 
@@ -457,8 +464,7 @@ static size_t mlp_ws_bytes(const exl3_linear* gate, const exl3_linear* up,
     need = act + std::max(group_scratch_bytes(g, rows), group_scratch_bytes(d, rows));
   } else {
     const QmmShape sh = choose_qmm_shape(down->in, down->out, rows);
-    const size_t stage2 =
-        sh.splits > 1 ? align_up(sizeof(float) * (size_t)sh.splits * rows * down->out) : 0;
+    const size_t stage2 = align_up(qmm_partial_bytes(sh, down->out));
     // down xhat + gate and up outputs
     need = 3 * act + std::max(group_scratch_bytes(g, rows), stage2);
   }

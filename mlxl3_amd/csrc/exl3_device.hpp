@@ -352,6 +352,12 @@ __device__ __forceinline__ int a_swizzle(int r) { return (r & 7) ^ ((r >> 3) & 1
 // instructions of the wave are outstanding and leaves the other counters free.
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
+// Buffer resource word 3 for raw dword buffer accesses on gfx9-family GPUs,
+// and the cache-policy operand of a coherent (sc1: agent scope, served by the
+// coherence point) buffer access.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+constexpr int kCpolSc1 = 16;
+
 // Byte offset of an LDS location in the workgroup's allocation.
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;

@@ -47,7 +47,7 @@ struct QmvParams {
 struct QmmParams {
   Member mem[kMaxMembers];
   int members;
-  float* partials;     // [splits][M][total_out] f32 (splits > 1)
+  float* partials;     // [splits][tiles][64*MB x 128 f32 in fragment order] (splits > 1)
   uint32_t* counters;  // [mtiles * col_blocks], zero between calls (splits > 1)
   int in, total_out, M;
   int x_dtype;         // the activation dtype (the output's intermediate cast)

@@ -210,6 +210,17 @@ __device__ __forceinline__ void load_slice_counted(const uint32_t* __restrict__ 
   if constexpr (K > 4) load_words<K - 4>(p + 4, w + 5);
 }
 
+// Buffer resource over the split-K partials of (split, tile): the f32
+// accumulators of the tile's 4 consumers in fragment order, [consumer][mb][f]
+// [lane] of 16 bytes (MB * 32 KB).
+template <class P>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t qmm_slab(const P& p, int split, int tile,
+                                                          int MB) {
+  return __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.partials + ((size_t)split * p.mtiles * p.col_blocks + tile) * (MB * 8192)), 0,
+      MB * 32768, kBufferRsrcWord3);
+}
+
 // Decode one step's 8 tiles of a producer (B[0] = previous lane's last word,
 // B[1..K] own words) into its 4 fragments in LDS.
 template <int K, int CB>
@@ -396,6 +407,20 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
     if (nq4 < nq) iter(nq4, std::integral_constant<int, 0>{});
     if (nq4 + 1 < nq) iter(nq4 + 1, std::integral_constant<int, 1>{});
     if (nq4 + 2 < nq) iter(nq4 + 2, std::integral_constant<int, 2>{});
+    if (p.splits > 1) {
+      // split-K arrival: after every consumer's partials are acknowledged
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old == (uint32_t)(p.splits - 1);
+        if (s_last)
+          __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      if (!s_last) return;  // uniform across the workgroup
+    }
   } else {
     // ---- consumer `role`: 16*MB rows x 128 columns ----
     float4v acc[MB][8];
@@ -462,8 +487,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
     }
     if (nq2 < nq) iter(nq2, std::integral_constant<int, 0>{});
     // the stages are free after the loop's last barrier
-    const int colb = cblk * 128;
-    if (p.splits == 1) {
+    auto stage_rows = [&]() {
       // static_for: the accumulator index must stay a compile-time constant
       static_for<MB>([&](auto mb_) {
         constexpr int mb = decltype(mb_)::value;
@@ -475,71 +499,43 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
           qmm_stage_row(v, lane, ys + (role * 16 * MB + 16 * mb + 4 * g + r) * kYStride);
         }
       });
+    };
+    if (p.splits == 1) {
+      stage_rows();
     } else {
-      // split-K: f32 partials out, through agent-scope relaxed atomics
-      float* part = p.partials + (size_t)split * p.M * TO;
+      // split-K: this part's accumulators out in fragment order (16 coalesced
+      // bytes per lane and fragment) through agent-scope coherent stores (sc1)
+      const __amdgpu_buffer_rsrc_t mine = qmm_slab(p, split, tile, MB);
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = row_base + 16 * mb + 4 * g + r;
-          if (row < p.M) {
-#pragma unroll
-            for (int f = 0; f < 8; ++f) {
-              const int c = colb + 32 * (f >> 1) + 16 * (n >> 3) + 8 * (f & 1) + (n & 7);
-              store_coherent(part + (size_t)row * TO + c, acc[mb][f][r]);
-            }
-          }
-        }
+        for (int f = 0; f < 8; ++f)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mb][f]), mine,
+                                                 ((role * MB + mb) * 8 + f) * 1024 + lane * 16, 0,
+                                                 kCpolSc1);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();  // every part stored (the producers count the arrival)
+      __syncthreads();
+      if (!s_last) return;  // uniform across the workgroup
     }
   }
-
-  // ---- split-K exchange: every wave takes part in the barriers ----
   if (p.splits > 1) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      uint32_t old = __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-      s_last = (old == (uint32_t)(p.splits - 1));
-    }
-    __syncthreads();
-    if (!s_last) return;  // uniform across the workgroup
-    if (threadIdx.x == 0)
-      __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // the tile's rows: sum of every split's partial in split order (this
-    // workgroup's own included, read back from memory), f16 into LDS; each
-    // wave takes 8*MB rows, each lane 16 consecutive columns of one row.  The
-    // 16 loads of a split go out together, two splits at a time.
-    const int colb = cblk * 128;
-    constexpr int kChunk = 2;
-    for (int i = 0; i < MB; ++i) {
-      const int rl = wave * 8 * MB + 8 * i + (lane >> 3);  // tile row
-      const int row = mtile * 64 * MB + rl;
-      const int lrow = row < p.M ? row : p.M - 1;  // in-bounds loads for padding rows
-      const int c0 = (lane & 7) * 16;
-      uint32_t* yw = (uint32_t*)(ys + rl * kYStride + c0);
-      float sum[16];
+    // the last part to arrive: every fragment summed over the parts in split
+    // order (coherent 16-byte loads, all 8 waves, 4*MB fragments each), its
+    // four rows rounded to f16 into the tile's rows in LDS
+    const int col = 16 * (n >> 3) + (n & 7);
+    for (int i = 0; i < 4 * MB; ++i) {
+      const int slot = wave * 4 * MB + i;  // (consumer, mb, f)
+      const int cr = slot / (8 * MB), mb = (slot / 8) % MB, f = slot % 8;
+      float4v sum = {0.f, 0.f, 0.f, 0.f};
+      for (int sp = 0; sp < p.splits; ++sp)
+        sum += __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                               qmm_slab(p, sp, tile, MB), slot * 1024 + lane * 16,
+                                               0, kCpolSc1));
+      uint16_t* y = ys + (cr * 16 * MB + 16 * mb + 4 * g) * kYStride + 32 * (f >> 1) +
+                    8 * (f & 1) + col;
 #pragma unroll
-      for (int jj = 0; jj < 16; ++jj) sum[jj] = 0.f;
-      for (int s0 = 0; s0 < p.splits; s0 += kChunk) {
-        float v[kChunk][16];
-#pragma unroll
-        for (int c = 0; c < kChunk; ++c) {
-          const int s = min(s0 + c, p.splits - 1);  // clamped: always a written split
-          const float* ps = p.partials + ((size_t)s * p.M + lrow) * TO + colb + c0;
-#pragma unroll
-          for (int jj = 0; jj < 16; ++jj) v[c][jj] = load_coherent(ps + jj);
-        }
-#pragma unroll
-        for (int c = 0; c < kChunk; ++c)
-          if (s0 + c < p.splits)
-#pragma unroll
-            for (int jj = 0; jj < 16; ++jj) sum[jj] += v[c][jj];
-      }
-#pragma unroll
-      for (int j = 0; j < 16; j += 2)
-        yw[j >> 1] = (uint32_t)f2h(sum[j]) | ((uint32_t)f2h(sum[j + 1]) << 16);
+      for (int r = 0; r < 4; ++r) y[r * kYStride] = f2h(sum[r]);
     }
   }
   __syncthreads();

@@ -175,14 +175,16 @@ static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
 // QMM launch shape: rows per workgroup 64*MB and global K-splits.  One
 // workgroup fills a CU, so a launch runs in rounds of 256 workgroups, each
 // round taking (K-steps per split) x (step time of that MB).  Step times
-// measured on MI355X with every CU busy: MB=1 660 ns, MB=2 900 ns, MB=4
-// 1290 ns (per 64 input rows); a split adds its f32 partials, written and read
-// back through agent-scope atomics at ~2.6 ns per KB.  Splits are only used
-// while the output tiles alone fill at most 256 workgroups, so at most 256
-// tile counters are ever needed.  Checked against a sweep of {4096x14336,
-// 14336x4096} x M{128, 512, 2048} x MB x splits: the chosen shape is the
-// fastest one measured at every point.  EXL3_QMM_MB and EXL3_QMM_SPLITS
-// override.
+// fitted on MI355X with every CU busy: MB=1 660 ns, MB=2 750 ns, MB=4 1250 ns
+// (per 64 input rows); a split adds its f32 partials (64*MB rows x 128 columns
+// per tile, padded), written and read back through 16-byte coherent accesses
+// at ~1.0 ns per KB.  Splits are only used while the output tiles alone fill
+// at most 256 workgroups, so at most 256 tile counters are ever needed.
+// Fitted to a sweep of MB {1,2,4} x splits {1,2,3,4,6,8} over 4096x14336 M
+// {128, 512}, 14336x4096 M {128, 256, 512, 2048}, 27648x5120 and 5120x27648
+// at M=128 and 4096x4096 at M=512: the chosen shape is the fastest measured at
+// every point but 14336x4096 M=128 (55 us against 51 for MB=1, 4 splits).
+// EXL3_QMM_MB and EXL3_QMM_SPLITS override.
 static constexpr int kTileCounters = 256;
 
 struct QmmShape {
@@ -201,16 +203,16 @@ static QmmShape choose_qmm_shape(int in, int out, int64_t rows) {
   double best_cost = 1e300;
   for (int mb : {4, 2, 1}) {
     if (force_mb && mb != force_mb) continue;
-    const double step_ns = mb == 4 ? 1290.0 : mb == 2 ? 900.0 : 660.0;
+    const double step_ns = mb == 4 ? 1250.0 : mb == 2 ? 750.0 : 660.0;
     const int64_t mt = (rows + 64 * mb - 1) / (64 * mb);
     const int64_t base = mt * col_blocks;
-    for (int splits : {1, 2, 4, 8}) {
+    for (int splits : {1, 2, 3, 4, 6, 8}) {
       int s = force_splits ? force_splits : splits;
       s = std::max(1, std::min(s, std::max(1, nq / 4)));
       if (s > 1 && base > kTileCounters) s = 1;
       const int64_t rounds = (base * s + 255) / 256;
       double cost = (double)rounds * ((nq + s - 1) / s) * step_ns;
-      if (s > 1) cost += 0.0026 * 4.0 * (double)s * rows * out;
+      if (s > 1) cost += 1.0 / 1024 * 4.0 * (double)s * mt * 64 * mb * out;
       if (cost < best_cost) {
         best_cost = cost;
         best = QmmShape{mb, (int)mt, s};

@@ -286,6 +286,18 @@ static bool qmv_separate_prologue(const Group& g, int64_t rows, int splits) {
   return rows * blocks >= 64;
 }
 
+// Multi-row QMVs of at least this many rows (one K-part per column pair)
+// exchange their split-K partials in fragment order: 8 KB slabs per split and
+// column block written and read with 16-byte coherent accesses, instead of
+// 4-byte row-major ones.  EXL3_QMV_FRAG_ROWS overrides it (tuning).
+static bool qmv_fragment_exchange(int64_t rows, int kw) {
+  static const int from = [] {
+    const char* env = getenv("EXL3_QMV_FRAG_ROWS");
+    return env ? atoi(env) : 8;
+  }();
+  return kw == 1 && rows >= from;
+}
+
 // Scratch bytes (after the counter region) of one group launch.
 static size_t group_scratch_bytes(const Group& g, int64_t rows) {
   if (rows <= kQmvMaxRows) {
@@ -294,7 +306,12 @@ static size_t group_scratch_bytes(const Group& g, int64_t rows) {
     const size_t xhat = qmv_separate_prologue(g, rows, splits)
                             ? g.count * align_up(sizeof(uint16_t) * (size_t)rows * g.in)
                             : 0;
-    return xhat + align_up(sizeof(float) * (size_t)splits * rows * g.total_out);
+    // partials: 8 KB fragment slabs per split and column block, or one
+    // row-major f32 row per split and row
+    const size_t partials = qmv_fragment_exchange(rows, kw)
+                                ? (size_t)splits * (g.total_out / 128) * 8192
+                                : sizeof(float) * (size_t)splits * rows * g.total_out;
+    return xhat + align_up(partials);
   }
   const QmmShape sh = choose_qmm_shape(g.in, g.total_out, rows);
   const size_t partials = qmm_partial_bytes(sh, g.total_out);
@@ -367,7 +384,13 @@ static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows
   size_t lds = sizeof(uint16_t) * (size_t)rows * max_blocks * 128;
   const int kwi = kw == 4 ? 2 : kw == 2 ? 1 : 0;
   const bool single = rows == 1 && kw == 1 && !glu.on && !p.mem[0].xhat;
-  const QmvFn fn = single ? kQmvSingle[g.k - 1][g.cb] : kQmv[kwi][g.k - 1][g.cb];
+  const bool frag = !single && qmv_fragment_exchange(rows, kw);
+  // the fragment exchange sums a column block's rows (f32, both members of a
+  // SwiGLU pair) in the activation buffer's LDS
+  if (frag) lds = std::max(lds, sizeof(float) * 128 * (size_t)rows * (glu.on ? 2 : 1));
+  const QmvFn fn = single ? kQmvSingle[g.k - 1][g.cb]
+                   : frag ? kQmvFrag[g.k - 1][g.cb]
+                          : kQmv[kwi][g.k - 1][g.cb];
   fn(p, dim3(g.total_out / 128, p.splits), lds, stream);
   return check_launch("EXL3 QMV launch");
 }

@@ -4,11 +4,12 @@
 
 namespace exl3 {
 
-#define EXL3_QMV_INST(K, CB)                                         \
-  template __global__ void qmv_kernel<K, CB, 1, false>(QmvParams); \
-  template __global__ void qmv_kernel<K, CB, 1, true>(QmvParams);  \
-  template __global__ void qmv_kernel<K, CB, 2, true>(QmvParams);  \
-  template __global__ void qmv_kernel<K, CB, 4, true>(QmvParams);
+#define EXL3_QMV_INST(K, CB)                                                \
+  template __global__ void qmv_kernel<K, CB, 1, false, false>(QmvParams); \
+  template __global__ void qmv_kernel<K, CB, 1, true, false>(QmvParams);  \
+  template __global__ void qmv_kernel<K, CB, 1, true, true>(QmvParams);   \
+  template __global__ void qmv_kernel<K, CB, 2, true, false>(QmvParams);  \
+  template __global__ void qmv_kernel<K, CB, 4, true, false>(QmvParams);
 #define EXL3_DEC_INST(K, CB)                                                             \
   template __global__ void decode_tiles_kernel<K, CB>(const uint32_t*, int64_t, uint16_t*, \
                                                       uint16_t*);
@@ -78,19 +79,23 @@ __global__ __launch_bounds__(256) void qmv_inner_kernel(const uint16_t* __restri
 #ifndef __HIP_DEVICE_COMPILE__
 template <int K, int CB>
 static void run_qmv1s(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) {
-  hipLaunchKernelGGL((qmv_kernel<K, CB, 1, false>), grid, dim3(256), lds, s, p);
+  hipLaunchKernelGGL((qmv_kernel<K, CB, 1, false, false>), grid, dim3(256), lds, s, p);
 }
 template <int K, int CB>
 static void run_qmv1(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) {
-  hipLaunchKernelGGL((qmv_kernel<K, CB, 1, true>), grid, dim3(256), lds, s, p);
+  hipLaunchKernelGGL((qmv_kernel<K, CB, 1, true, false>), grid, dim3(256), lds, s, p);
+}
+template <int K, int CB>
+static void run_qmv1f(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) {
+  hipLaunchKernelGGL((qmv_kernel<K, CB, 1, true, true>), grid, dim3(256), lds, s, p);
 }
 template <int K, int CB>
 static void run_qmv2(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) {
-  hipLaunchKernelGGL((qmv_kernel<K, CB, 2, true>), grid, dim3(512), lds, s, p);
+  hipLaunchKernelGGL((qmv_kernel<K, CB, 2, true, false>), grid, dim3(512), lds, s, p);
 }
 template <int K, int CB>
 static void run_qmv4(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) {
-  hipLaunchKernelGGL((qmv_kernel<K, CB, 4, true>), grid, dim3(1024), lds, s, p);
+  hipLaunchKernelGGL((qmv_kernel<K, CB, 4, true, false>), grid, dim3(1024), lds, s, p);
 }
 template <int K, int CB>
 static void run_decode(const uint32_t* packed, int64_t tiles, uint16_t* st, uint16_t* val,
@@ -121,6 +126,7 @@ void launch_qmv_inner(const uint16_t* values, const uint16_t* x, int rows, int c
 
 const QmvFn kQmv[3][8][3] = {EXL3_TABLE(run_qmv1), EXL3_TABLE(run_qmv2), EXL3_TABLE(run_qmv4)};
 const QmvFn kQmvSingle[8][3] = EXL3_TABLE(run_qmv1s);
+const QmvFn kQmvFrag[8][3] = EXL3_TABLE(run_qmv1f);
 const DecodeFn kDecode[8][3] = EXL3_TABLE(run_decode);
 
 #endif

@@ -344,9 +344,11 @@ __device__ __forceinline__ void prologue8(const void* x, int x_dtype, size_t xe,
 // amortises one prologue over KW times more weight stream.
 // MULTI = false is the single-row variant of a plain launch (the batch-1
 // decode): no batched prologue or epilogue code, no separate prologue and no
-// SwiGLU edge.
-template <int K, int CB, int KW, bool MULTI>
+// SwiGLU edge.  FRAG (multi-row only) exchanges the split-K partials in
+// fragment order instead of row-major.
+template <int K, int CB, int KW, bool MULTI, bool FRAG>
 __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
+  static_assert(MULTI || !FRAG, "the fragment exchange is a multi-row form");
   extern __shared__ __attribute__((aligned(16))) _Float16 xs[];  // [M][rows of split]
   __shared__ int s_last;
   __shared__ float4v red[KW > 1 ? KW - 1 : 1][4][2][64];
@@ -523,19 +525,37 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   const int n = lane & 15;
   const int col = 128 * cblk + 16 * (pair * 2 + (n >> 3)) + (n & 7);
   const int TO = p.total_out;
-  float* part = p.partials + (size_t)split * M * TO;
+  // FRAG: partials in fragment order, a slab of 8 KB per (split, column
+  // block): [pair][acc0, acc1][lane] of 16 bytes, one coalesced coherent
+  // 16-byte store per accumulator.  Otherwise row-major, 4 bytes per value.
+  auto frag_slab = [&](int sp, int gcb) {
+    return __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.partials + ((size_t)sp * (TO >> 7) + gcb) * 2048), 0, 8192, kBufferRsrcWord3);
+  };
+  if constexpr (FRAG) {
+    if (writer) {
+      const __amdgpu_buffer_rsrc_t mine = frag_slab(split, cblk);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc0), mine,
+                                             ((pair * 2) * 64 + lane) * 16, 0, kCpolSc1);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc1), mine,
+                                             ((pair * 2 + 1) * 64 + lane) * 16, 0, kCpolSc1);
+    }
+  } else {
+    float* part = p.partials + (size_t)split * M * TO;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    int m = 4 * g + r;
-    if (writer && m < M) {
-      store_coherent(part + (size_t)m * TO + col, acc0[r]);
-      store_coherent(part + (size_t)m * TO + col + 8, acc1[r]);
+    for (int r = 0; r < 4; ++r) {
+      int m = 4 * g + r;
+      if (writer && m < M) {
+        store_coherent(part + (size_t)m * TO + col, acc0[r]);
+        store_coherent(part + (size_t)m * TO + col + 8, acc1[r]);
+      }
     }
   }
 
   // last workgroup of this column block finishes it.  Partials and counters
-  // are exchanged only through agent-scope relaxed atomics (served at the
-  // device coherence point, no L2 writeback); s_waitcnt + barrier order every
+  // are exchanged only through agent-scope coherent accesses (sc1 loads and
+  // stores, relaxed atomics: served at the device coherence point, no L2
+  // writeback); s_waitcnt + barrier order every
   // partial store of the workgroup before its counter increment.
   // A SwiGLU group finishes a column block once both members' splits are in
   // (one counter per block pair).
@@ -582,63 +602,12 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
         }
     }
   };
-  if constexpr (!MULTI) {  // the plain single-row epilogue (no SwiGLU edge)
-    for (int m = wave; m < M; m += 4 * KW) {
-      float v0, v1;
-      sum_row(m, cblk * 128, v0, v1);
-      finish_row128(v0, v1, lane, colb_l, mm.svh, mm.bias, mm.y, mm.y_dtype, p.x_dtype,
-                    (size_t)m * mm.out);
-    }
-    return;
-  }
-  if (!p.glu.on) {
-    // rows in batches of 4 per wave: the split sums of a batch load together,
-    // kRowChunk splits at a time (each row still adds its splits in split
-    // order)
-    constexpr int kRows = 4, kRowChunk = kSplitChunk / 2;
-    for (int m0 = wave; m0 < M; m0 += kRows * 4 * KW) {
-      float v0[kRows], v1[kRows];
-#pragma unroll
-      for (int t = 0; t < kRows; ++t) v0[t] = v1[t] = 0.f;
-      for (int s0 = 0; s0 < p.splits; s0 += kRowChunk) {
-        float a[kRowChunk][kRows], b[kRowChunk][kRows];
-#pragma unroll
-        for (int i = 0; i < kRowChunk; ++i) {
-          const int sp = min(s0 + i, p.splits - 1);  // clamped: always a written split
-#pragma unroll
-          for (int t = 0; t < kRows; ++t) {
-            const int m = min(m0 + t * 4 * KW, M - 1);  // clamped: always a written row
-            const float* ps = p.partials + ((size_t)sp * M + m) * TO + cblk * 128;
-            a[i][t] = load_coherent(ps + lane);
-            b[i][t] = load_coherent(ps + lane + 64);
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < kRowChunk; ++i)
-          if (s0 + i < p.splits)
-#pragma unroll
-            for (int t = 0; t < kRows; ++t) {
-              v0[t] += a[i][t];
-              v1[t] += b[i][t];
-            }
-      }
-#pragma unroll
-      for (int t = 0; t < kRows; ++t) {
-        const int m = m0 + t * 4 * KW;
-        if (m < M)
-          finish_row128(v0[t], v1[t], lane, colb_l, mm.svh, mm.bias, mm.y, mm.y_dtype,
-                        p.x_dtype, (size_t)m * mm.out);
-      }
-    }
-    return;
-  }
-  const Member& gm = p.mem[0];
-  const Member& um = p.mem[1];
-  const int H = gm.out;
-  for (int m = wave; m < M; m += 4 * KW) {
-    float g0, g1, u0, u1;
-    sum_row(m, (gm.cblk0 + cblk_l) * 128, g0, g1);
-    sum_row(m, (um.cblk0 + cblk_l) * 128, u0, u1);
+  // a (gate, up) row of the block: staged H128, *svh, +bias, f16 SwiGLU and,
+  // for the fused MLP, the down projection's prologue
+  auto glu_finish = [&](int m, float g0, float g1, float u0, float u1) {
+    const Member& gm = p.mem[0];
+    const Member& um = p.mem[1];
+    const int H = gm.out;
     finish_vals128(g0, g1, lane, colb_l, gm.svh);
     finish_vals128(u0, u1, lane, colb_l, um.svh);
     g0 = with_bias_f16(g0, gm.bias, colb_l + lane);
@@ -655,6 +624,116 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
     }
     p.glu.out[(size_t)m * H + colb_l + lane] = f2h(a0);
     p.glu.out[(size_t)m * H + colb_l + lane + 64] = f2h(a1);
+  };
+  if constexpr (!MULTI) {  // the plain single-row epilogue (no SwiGLU edge)
+    for (int m = wave; m < M; m += 4 * KW) {
+      float v0, v1;
+      sum_row(m, cblk * 128, v0, v1);
+      finish_row128(v0, v1, lane, colb_l, mm.svh, mm.bias, mm.y, mm.y_dtype, p.x_dtype,
+                    (size_t)m * mm.out);
+    }
+  } else if constexpr (!FRAG) {
+    // rows of the block from row-major partials (the split loads of a batch go
+    // out together, each row adding its splits in split order)
+    if (!p.glu.on) {
+      // rows in batches of 4 per wave: the split sums of a batch load together,
+      // kRowChunk splits at a time (each row still adds its splits in split
+      // order)
+      constexpr int kRows = 4, kRowChunk = kSplitChunk / 2;
+      for (int m0 = wave; m0 < M; m0 += kRows * 4 * KW) {
+        float v0[kRows], v1[kRows];
+#pragma unroll
+        for (int t = 0; t < kRows; ++t) v0[t] = v1[t] = 0.f;
+        for (int s0 = 0; s0 < p.splits; s0 += kRowChunk) {
+          float a[kRowChunk][kRows], b[kRowChunk][kRows];
+#pragma unroll
+          for (int i = 0; i < kRowChunk; ++i) {
+            const int sp = min(s0 + i, p.splits - 1);  // clamped: always a written split
+#pragma unroll
+            for (int t = 0; t < kRows; ++t) {
+              const int m = min(m0 + t * 4 * KW, M - 1);  // clamped: always a written row
+              const float* ps = p.partials + ((size_t)sp * M + m) * TO + cblk * 128;
+              a[i][t] = load_coherent(ps + lane);
+              b[i][t] = load_coherent(ps + lane + 64);
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < kRowChunk; ++i)
+            if (s0 + i < p.splits)
+#pragma unroll
+              for (int t = 0; t < kRows; ++t) {
+                v0[t] += a[i][t];
+                v1[t] += b[i][t];
+              }
+        }
+#pragma unroll
+        for (int t = 0; t < kRows; ++t) {
+          const int m = m0 + t * 4 * KW;
+          if (m < M)
+            finish_row128(v0[t], v1[t], lane, colb_l, mm.svh, mm.bias, mm.y, mm.y_dtype,
+                          p.x_dtype, (size_t)m * mm.out);
+        }
+      }
+      return;
+    }
+    for (int m = wave; m < M; m += 4 * KW) {
+      float g0, g1, u0, u1;
+      sum_row(m, (p.mem[0].cblk0 + cblk_l) * 128, g0, g1);
+      sum_row(m, (p.mem[1].cblk0 + cblk_l) * 128, u0, u1);
+      glu_finish(m, g0, g1, u0, u1);
+    }
+  } else {
+    // Multi-row: the split sums in fragment space -- pair wave w (K-part 0)
+    // loads its two accumulators of every split (16-byte coherent loads, up to
+    // kSplitChunk splits in flight) and adds them in split order -- then the
+    // block's rows through LDS to the row-wise finishing.  The rows (M per
+    // member, f32) take the activation buffer's place: every wave is past
+    // the K loop (the barrier above).
+    float(*const ysum)[128] = reinterpret_cast<float(*)[128]>(xs);
+    auto gather_block = [&](int gcb, float(*dst)[128]) {
+      if (writer) {
+        float4v s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+        for (int c0 = 0; c0 < p.splits; c0 += kSplitChunk) {
+          float4v a[kSplitChunk], b[kSplitChunk];
+#pragma unroll
+          for (int i = 0; i < kSplitChunk; ++i) {
+            const __amdgpu_buffer_rsrc_t src = frag_slab(min(c0 + i, p.splits - 1), gcb);
+            a[i] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   src, ((pair * 2) * 64 + lane) * 16, 0, kCpolSc1));
+            b[i] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   src, ((pair * 2 + 1) * 64 + lane) * 16, 0,
+                                                   kCpolSc1));
+          }
+#pragma unroll
+          for (int i = 0; i < kSplitChunk; ++i)
+            if (c0 + i < p.splits) {
+              s0 += a[i];
+              s1 += b[i];
+            }
+        }
+        const int c = 16 * (pair * 2 + (n >> 3)) + (n & 7);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (4 * g + r < M) {
+            dst[4 * g + r][c] = s0[r];
+            dst[4 * g + r][c + 8] = s1[r];
+          }
+      }
+    };
+    if (!p.glu.on) {
+      gather_block(cblk, ysum);
+      __syncthreads();
+      for (int m = wave; m < M; m += 4 * KW)
+        finish_row128(ysum[m][lane], ysum[m][lane + 64], lane, colb_l, mm.svh, mm.bias, mm.y,
+                      mm.y_dtype, p.x_dtype, (size_t)m * mm.out);
+      return;
+    }
+    float(*const usum)[128] = ysum + M;
+    gather_block(p.mem[0].cblk0 + cblk_l, ysum);
+    gather_block(p.mem[1].cblk0 + cblk_l, usum);
+    __syncthreads();
+    for (int m = wave; m < M; m += 4 * KW)
+      glu_finish(m, ysum[m][lane], ysum[m][lane + 64], usum[m][lane], usum[m][lane + 64]);
   }
 }
 

@@ -473,22 +473,27 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   const int am = min(lane & 15, M - 1);
   const _Float16* xrow = xs + (size_t)am * nrows + 64 * q_lo + g * 16;
   float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  // issue priority falls at the quarters of the K-range (steps t1, t2, t3)
+  // issue priority falls at the quarters of the K-range (steps t1, t2, t3),
+  // set after each set of D steps
   const int t1 = (nquads + 3) / 4, t2 = (2 * nquads + 3) / 4, t3 = (3 * nquads + 3) / 4;
-  auto compute = [&](uint32_t(&set)[D][K + 1], int qbase) {
+  auto lower_priority = [&](int done) {
+    if (done >= t3) __builtin_amdgcn_s_setprio(0);
+    else if (done >= t2) __builtin_amdgcn_s_setprio(1);
+    else if (done >= t1) __builtin_amdgcn_s_setprio(2);
+  };
+  // A whole set is one branch-free block, so the compiler interleaves the
+  // decode chains of its D steps; only the last, partial pass tests each step.
+  auto compute = [&](uint32_t(&set)[D][K + 1], int qbase, bool whole) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const int q = qbase + d;
-      if (q < nquads) {
+      if (whole || q < nquads) {
         half8 a0 = *(const half8*)(xrow + q * 64);
         half8 a1 = *(const half8*)(xrow + q * 64 + 8);
         qmv_step_prev<K, CB>(set[d], a0, a1, acc0, acc1);
-        const int t = q + 1;
-        if (t == t3) __builtin_amdgcn_s_setprio(0);
-        else if (t == t2) __builtin_amdgcn_s_setprio(1);
-        else if (t == t1) __builtin_amdgcn_s_setprio(2);
       }
     }
+    lower_priority(qbase + D);
   };
   // Unconditional loads (past-the-end quads re-read the last one) keep the
   // load count static, so the waits before each decode can be partial.
@@ -496,11 +501,17 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
 #pragma unroll
     for (int d = 0; d < D; ++d) load_slice_prev_s<K>(slice_base(qbase + d), loff, loff_prev, set[d]);
   };
-  for (int q0 = 0; q0 < nquads; q0 += 2 * D) {
+  int q0 = 0;
+  for (; q0 + 2 * D <= nquads; q0 += 2 * D) {
     fetch(setB, q0 + D);
-    compute(setA, q0);
+    compute(setA, q0, true);
     fetch(setA, q0 + 2 * D);
-    compute(setB, q0 + D);
+    compute(setB, q0 + D, true);
+  }
+  if (q0 < nquads) {  // fewer than 2*D steps left; setA holds step q0's slices
+    fetch(setB, q0 + D);
+    compute(setA, q0, false);
+    compute(setB, q0 + D, false);
   }
 
   // K-parts of a pair meet in LDS; part 0 adds them in part order

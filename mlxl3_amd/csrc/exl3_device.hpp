@@ -357,6 +357,8 @@ constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) 
 // coherence point) buffer access.
 constexpr int kBufferRsrcWord3 = 0x00020000;
 constexpr int kCpolSc1 = 16;
+// Cache-policy operand of a streaming (non-temporal) buffer load.
+constexpr int kCpolNt = 2;
 
 // Byte offset of an LDS location in the workgroup's allocation.
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {

@@ -63,26 +63,25 @@ __device__ __forceinline__ void load_slice_prev(const uint32_t* __restrict__ p, 
   }
 }
 
-// The same loads from a wave-uniform base plus per-lane byte offsets (the
-// lane's own words at `loff`, the previous lane's last word at `loff_prev`):
-// the address stays a scalar base + 32-bit vector offset, so a slice costs no
-// vector address arithmetic.
+// The same loads as raw buffer loads: the resource holds the wave-uniform
+// base, `soff` the slice's scalar byte offset, `loff` / `loff_prev` the lane's
+// byte offsets (its own words, the previous lane's last word), so a slice costs
+// no vector address arithmetic and every access is bounded by the resource.
 template <int K>
-__device__ __forceinline__ void load_slice_prev_s(const char* sbase, uint32_t loff,
-                                                  uint32_t loff_prev, uint32_t (&w)[K + 1]) {
-  w[0] = __builtin_nontemporal_load((const uint32_t*)(sbase + loff_prev));
-  const uint32_t* p = (const uint32_t*)(sbase + loff);
-  if constexpr (K == 4) {
-    u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
-    w[1] = v[0], w[2] = v[1], w[3] = v[2], w[4] = v[3];
-  } else if constexpr (K == 8) {
-    u32x4 v0 = __builtin_nontemporal_load((const u32x4*)p);
-    u32x4 v1 = __builtin_nontemporal_load((const u32x4*)p + 1);
-    w[1] = v0[0], w[2] = v0[1], w[3] = v0[2], w[4] = v0[3];
-    w[5] = v1[0], w[6] = v1[1], w[7] = v1[2], w[8] = v1[3];
+__device__ __forceinline__ void load_slice_prev_b(__amdgpu_buffer_rsrc_t w, uint32_t soff,
+                                                  uint32_t loff, uint32_t loff_prev,
+                                                  uint32_t (&out)[K + 1]) {
+  out[0] = __builtin_amdgcn_raw_buffer_load_b32(w, loff_prev, soff, kCpolNt);
+  if constexpr (K == 4 || K == 8) {
+#pragma unroll
+    for (int h = 0; h < K / 4; ++h) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(w, loff + 16 * h, soff, kCpolNt);
+      out[4 * h + 1] = v[0], out[4 * h + 2] = v[1], out[4 * h + 3] = v[2], out[4 * h + 4] = v[3];
+    }
   } else {
 #pragma unroll
-    for (int i = 0; i < K; ++i) w[i + 1] = __builtin_nontemporal_load(p + i);
+    for (int i = 0; i < K; ++i)
+      out[i + 1] = __builtin_amdgcn_raw_buffer_load_b32(w, loff + 4 * i, soff, kCpolNt);
   }
 }
 
@@ -361,7 +360,9 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   const int TN = mm.out >> 4, NB = p.in >> 7;
   const int b0 = split * NB / p.splits, b1 = (split + 1) * NB / p.splits;
   const int row0 = b0 * 128, nrows = (b1 - b0) * 128, nq_wg = nrows >> 6;
-  const int q_lo = kpart * nq_wg / KW, q_hi = (kpart + 1) * nq_wg / KW;
+  // the K-part's quads (one K-part: the workgroup's, a uniform range)
+  const int q_lo = KW == 1 ? 0 : kpart * nq_wg / KW;
+  const int q_hi = KW == 1 ? nq_wg : (kpart + 1) * nq_wg / KW;
   const int nquads = q_hi - q_lo;
   const int M = p.M;
   // Issue priority falls with progress (3 -> 0 over the K-range): the SIMD's
@@ -393,18 +394,33 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   const int g = lane >> 4, hsel = (lane >> 3) & 1, j = lane & 7;
   const int tn0 = cblk_l * 8 + pair * 2;
   const size_t qstride = (size_t)4 * TN * 8 * K;  // words per quad of tile rows
-  // wave-uniform base of the K-part's first quad; per-lane byte offsets
-  const uint32_t* wbase = mm.trellis + ((size_t)((row0 >> 4) + 4 * q_lo) * TN + tn0) * (8 * K);
-  const uint32_t loff = (uint32_t)(((g * TN + hsel) * 8 * K + j * K) * 4);
+  // The weight loads are buffer loads from the workgroup's base (its first
+  // tile row and column block: uniform, so the resource sits in scalar
+  // registers), bounded by the end of the member's trellis.  A lane's byte
+  // offset holds everything that depends on the wave (column pair, K-part) and
+  // the lane; a quad's offset is scalar with one K-part and joins the lane's
+  // offset otherwise.
+  const size_t wg_words = ((size_t)(row0 >> 4) * TN + cblk_l * 8) * (8 * K);
+  const size_t tensor_words = (size_t)NB * 8 * TN * (8 * K);
+  const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(mm.trellis + wg_words), 0,
+      (int)(uint32_t)min((tensor_words - wg_words) * 4, (size_t)0xffffffffu), kBufferRsrcWord3);
+  const uint32_t loff = (uint32_t)((((size_t)4 * q_lo * TN + pair * 2 + g * TN + hsel) * 8 * K +
+                                    j * K) * 4);
   const uint32_t loff_prev = loff + (uint32_t)((j == 0 ? 8 * K - 1 : -1) * 4);
   constexpr int D = kQmvDepth<K>;
   uint32_t setA[D][K + 1], setB[D][K + 1];
   const int qlast = nquads > 0 ? nquads - 1 : 0;
-  auto slice_base = [&](int q) {
-    return (const char*)(wbase + (size_t)min(q, qlast) * qstride);
+  const uint32_t qbytes = (uint32_t)qstride * 4u, last_off = (uint32_t)qlast * qbytes;
+  auto fetch_slice = [&](uint32_t(&set)[K + 1], int q) {
+    const uint32_t o = min((uint32_t)q * qbytes, last_off);  // past-the-end quads re-read the last
+    if constexpr (KW == 1)
+      load_slice_prev_b<K>(wrsrc, o, loff, loff_prev, set);
+    else
+      load_slice_prev_b<K>(wrsrc, 0, loff + o, loff_prev + o, set);
   };
 #pragma unroll
-  for (int d = 0; d < D; ++d) load_slice_prev_s<K>(slice_base(d), loff, loff_prev, setA[d]);
+  for (int d = 0; d < D; ++d) fetch_slice(setA[d], d);
   __builtin_amdgcn_sched_barrier(0);
 
   // prologue into LDS
@@ -499,7 +515,7 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   // load count static, so the waits before each decode can be partial.
   auto fetch = [&](uint32_t(&set)[D][K + 1], int qbase) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) load_slice_prev_s<K>(slice_base(qbase + d), loff, loff_prev, set[d]);
+    for (int d = 0; d < D; ++d) fetch_slice(set[d], qbase + d);
   };
   int q0 = 0;
   for (; q0 + 2 * D <= nquads; q0 += 2 * D) {

@@ -26,6 +26,8 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 
 constexpr float kHadScale = 0.08838834764831845f;  // f32 bits 0x3db504f3
 
@@ -377,6 +379,14 @@ __device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                :
                : "v"(g), "s"(lds)
+               : "memory", "m0");
+}
+// The same copy from a scalar base plus the lane's 32-bit byte offset (no
+// per-lane 64-bit address).
+__device__ __forceinline__ void lds_dma16_s(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(off), "s"(base), "s"(lds)
                : "memory", "m0");
 }
 

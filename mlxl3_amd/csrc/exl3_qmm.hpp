@@ -209,6 +209,34 @@ __device__ __forceinline__ void load_slice_counted(const uint32_t* __restrict__ 
   load_words<(K < 4 ? K : 4)>(p, w + 1);
   if constexpr (K > 4) load_words<K - 4>(p + 4, w + 5);
 }
+// The same instruction count as raw buffer loads: resource `r`, the step's
+// scalar byte offset `so`, the lane's byte offsets of its words (`lo`) and of
+// the previous lane's last word (`lo_prev`).
+template <int N>
+__device__ __forceinline__ void buffer_words(__amdgpu_buffer_rsrc_t r, uint32_t lo, uint32_t so,
+                                             uint32_t* w) {
+  if constexpr (N == 1) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, lo, so, kCpolNt);
+  } else if constexpr (N == 2) {
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, lo, so, kCpolNt);
+    w[0] = v[0], w[1] = v[1];
+  } else if constexpr (N == 3) {
+    const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(r, lo, so, kCpolNt);
+    w[0] = v[0], w[1] = v[1], w[2] = v[2];
+  } else {
+    static_assert(N == 4, "1-4 words");
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, lo, so, kCpolNt);
+    w[0] = v[0], w[1] = v[1], w[2] = v[2], w[3] = v[3];
+  }
+}
+template <int K>
+__device__ __forceinline__ void buffer_slice_counted(__amdgpu_buffer_rsrc_t r, uint32_t so,
+                                                     uint32_t lo, uint32_t lo_prev,
+                                                     uint32_t (&w)[K + 1]) {
+  w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, lo_prev, so, kCpolNt);
+  buffer_words<(K < 4 ? K : 4)>(r, lo, so, w + 1);
+  if constexpr (K > 4) buffer_words<K - 4>(r, lo + 16, so, w + 5);
+}
 
 // Buffer resource over the split-K partials of (split, tile): the f32
 // accumulators of the tile's 4 consumers in fragment order, [consumer][mb][f]
@@ -301,6 +329,22 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
                          ((size_t)(4 * qa + g) * TN + cblk_l * 8 + role * 2 + hsel) * (8 * K) +
                          (size_t)j * K;
     const int prev_off = j == 0 ? 8 * K - 1 : -1;
+    // With the direct A copies the slices are raw buffer loads from the
+    // workgroup's base (its first quad and column block: uniform, held in
+    // scalar registers, bounded by the end of the member's trellis): the
+    // producer's and the lane's parts sit in the 32-bit vector offset, the
+    // step's in the scalar one, so a slice costs no vector address work.
+    const size_t wg_words = ((size_t)4 * qa * TN + cblk_l * 8) * (8 * K);
+    const size_t tensor_words = (size_t)(p.in >> 4) * TN * (8 * K);
+    const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(mm.trellis + wg_words), 0,
+        (int)(uint32_t)min((tensor_words - wg_words) * 4, (size_t)0xffffffffu), kBufferRsrcWord3);
+    const uint32_t wlo = (uint32_t)(((g * TN + role * 2 + hsel) * 8 * K + j * K) * 4);
+    const uint32_t wlo_prev = wlo + (uint32_t)(prev_off * 4);
+    const uint32_t qbytes = (uint32_t)qstride * 4u, last_off = (uint32_t)qlast * qbytes;
+    auto fetch_counted = [&](uint32_t(&w)[K + 1], int step) {
+      buffer_slice_counted<K>(wrsrc, min((uint32_t)step * qbytes, last_off), wlo, wlo_prev, w);
+    };
     uint32_t sl[PD][K + 1];
 #pragma unroll
     for (int d = 0; d < PD; ++d)
@@ -322,15 +366,25 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
 #pragma unroll
     for (int i = 0; i < 2 * MB; ++i) {
       const int row = row_base + 8 * i + ar;
-      const int chunk = kDma ? ac ^ a_swizzle(8 * i + ar) : ac;
-      ap[i] = mm.xhat + (size_t)(row < p.M ? row : 0) * p.in + (size_t)qa * 64 + chunk * 8;
+      ap[i] = mm.xhat + (size_t)(row < p.M ? row : 0) * p.in + (size_t)qa * 64 + ac * 8;
+    }
+    // direct copies: the row tile's first row and the step in the scalar
+    // base, the lane's row (rows >= M read the tile's first row) and chunk in
+    // a 32-bit byte offset
+    const int tile_row0 = mtile * 64 * MB;
+    const uint16_t* abase = mm.xhat + (size_t)tile_row0 * p.in + (size_t)qa * 64;
+    uint32_t aoff[2 * MB];
+#pragma unroll
+    for (int i = 0; i < 2 * MB; ++i) {
+      const int r = role * 16 * MB + 8 * i + ar;  // row inside the tile
+      aoff[i] = (uint32_t)(((tile_row0 + r < p.M ? r : 0) * p.in + (ac ^ a_swizzle(8 * i + ar)) * 8) * 2);
     }
     auto dma_a = [&](int step, int st) {
       const uint32_t base = __builtin_amdgcn_readfirstlane(
           lds_offset(astage(st) + role * (16 * MB * 128)));
+      const uint16_t* sb = abase + (size_t)min(step, qlast) * 64;
 #pragma unroll
-      for (int i = 0; i < 2 * MB; ++i)
-        lds_dma16(ap[i] + (size_t)min(step, qlast) * 64, base + i * 1024);
+      for (int i = 0; i < 2 * MB; ++i) lds_dma16_s(sb, aoff[i], base + i * 1024);
     };
     // A rows of steps q+2 and q+3 in flight (register sets alternate by step)
     u32x4 areg[2][kDma ? 1 : 2 * MB];
@@ -355,8 +409,8 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
       qmm_produce<K, CB>(sl[0], bstage(0) + role * 256, lane);
       qmm_produce<K, CB>(sl[1], bstage(1) + role * 256, lane);
       __builtin_amdgcn_sched_barrier(0);
-      load_slice_counted<K>(tp + (size_t)min(PD, qlast) * qstride, prev_off, sl[0]);
-      load_slice_counted<K>(tp + (size_t)min(PD + 1, qlast) * qstride, prev_off, sl[1]);
+      fetch_counted(sl[0], PD);
+      fetch_counted(sl[1], PD + 1);
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * kSliceLoads<K>));
     } else {
@@ -384,8 +438,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
         __builtin_amdgcn_sched_barrier(0);
         qmm_produce<K, CB>(sl[(P + 2) % PD], bstage(st) + role * 256, lane);
         __builtin_amdgcn_sched_barrier(0);
-        load_slice_counted<K>(tp + (size_t)min(q + 2 + PD, qlast) * qstride, prev_off,
-                              sl[(P + 2) % PD]);
+        fetch_counted(sl[(P + 2) % PD], q + 2 + PD);
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(vmcnt_only(kSliceLoads<K>));  // A of step q+2 has landed
       } else {

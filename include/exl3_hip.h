@@ -68,7 +68,10 @@ const char* exl3_version(void);
 /* Exl3Linear::new, linear.rs:577-653.  trellis: [in/16][out/16][16k] u16
  * (I16 accepted by the caller's reinterpretation); suh f16[in]; svh f16[out];
  * bias f16[out] or NULL; k in 1..8; cb an exl3_codebook.  in and out must be
- * positive multiples of 128 (linear.rs:593-596). */
+ * positive multiples of 128 (linear.rs:593-596).  A trellis of 4 GiB or more
+ * (in * out * k / 8 bytes) is rejected: the kernels address it with 32-bit
+ * offsets (no counterpart in the reference, whose largest real tensors are
+ * ~1.2 GB). */
 int exl3_linear_create(const uint16_t* trellis, int32_t in, int32_t out, int32_t k, int32_t cb,
                        const uint16_t* suh, const uint16_t* svh, const uint16_t* bias,
                        exl3_linear** out_handle);

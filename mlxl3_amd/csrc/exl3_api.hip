@@ -557,6 +557,11 @@ int exl3_linear_create(const uint16_t* trellis, int32_t in, int32_t out, int32_t
   if (in <= 0 || out <= 0) return fail(EXL3_EINVAL, "invalid trellis shape");
   if (in % 128 || out % 128)
     return fail(EXL3_EINVAL, "public EXL3 projections require 128-aligned dimensions");
+  // The kernels address a trellis with 32-bit byte offsets from a base inside it.
+  const int64_t trellis_bytes = (int64_t)in * out / 8 * k;
+  if (trellis_bytes >= ((int64_t)1 << 32))
+    return fail(EXL3_EINVAL, "EXL3 trellis of %lld bytes exceeds the 4 GiB limit",
+                (long long)trellis_bytes);
   if (!trellis || !suh || !svh) return fail(EXL3_EINVAL, "null weight pointer");
   exl3_linear* h = new (std::nothrow) exl3_linear;
   if (!h) return fail(EXL3_ENOMEM, "out of host memory");

@@ -56,6 +56,8 @@ def create(k=4, cb=0, n_in=256, n_out=256, trellis=FAKE, suh=FAKE, svh=FAKE):
         (dict(n_in=192), "128-aligned"),
         (dict(n_out=100), "128-aligned"),
         (dict(trellis=None), "null weight pointer"),
+        # 65536 x 65536 at K=8: 4 GiB of trellis, past the 32-bit kernel offsets
+        (dict(k=8, n_in=65536, n_out=65536), "exceeds the 4 GiB limit"),
     ],
 )
 def test_create_rejects_like_the_reference(kwargs, msg):

@@ -13,11 +13,12 @@
 //      K-dword load brings in 8 whole tiles (lanes 16g..16g+15 hold tile row
 //      tk0+g, tiles tn0 and tn0+1).  Lanes decode their 32 weights in
 //      registers into MFMA B fragments and v_mfma_f32_16x16x32_f16 multiplies
-//      them with up to 16 activation rows at once (rows >= M are zero), so
-//      M = 1..16 costs the same decode;
-//   3. split-K partials go to the workspace; the last workgroup to finish a
-//      128-column block sums the splits in split order (deterministic), and
-//      applies the epilogue (linear.rs:984-997): f16, H128, * svh, cast, bias.
+//      them with up to 16 activation rows at once (rows >= M repeat row M-1
+//      and are never stored), so M = 1..16 costs the same decode;
+//   3. split-K partials go to the workspace (row-major, or in fragment order
+//      from 8 rows); the last workgroup to finish a 128-column block sums the
+//      splits in split order (deterministic), and applies the epilogue
+//      (linear.rs:984-997): f16, H128, * svh, cast, bias.
 #pragma once
 
 #include "exl3_device.hpp"
@@ -63,7 +64,7 @@ __device__ __forceinline__ void load_slice_prev(const uint32_t* __restrict__ p, 
   }
 }
 
-// The same loads as raw buffer loads: the resource holds the wave-uniform
+// The same loads as raw buffer loads: the resource holds a workgroup-uniform
 // base, `soff` the slice's scalar byte offset, `loff` / `loff_prev` the lane's
 // byte offsets (its own words, the previous lane's last word), so a slice costs
 // no vector address arithmetic and every access is bounded by the resource.

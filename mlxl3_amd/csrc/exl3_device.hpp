@@ -367,22 +367,15 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-// global_load_lds_dwordx4 as inline assembly: lane l copies the 16 bytes at
-// its global address g into LDS bytes lds + 16l .. lds + 16l + 15 (lds
+// global_load_lds_dwordx4 as inline assembly, in its scalar-base form: lane
+// l copies the 16 bytes at base + off (base wave-uniform, off the lane's
+// 32-bit byte offset) into LDS bytes lds + 16l .. lds + 16l + 15 (lds
 // wave-uniform; the s_nop covers the M0 write -> LDS-DMA hazard).  The
 // compiler does not see this LDS write, so it adds no waits of its own for it
 // (it cannot tell the destination from other LDS accesses and would wait for
 // every outstanding load before them): the caller waits with s_waitcnt vmcnt
 // before the barrier that publishes the bytes.  "memory" keeps other memory
 // accesses from moving across the issue.
-__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(g), "s"(lds)
-               : "memory", "m0");
-}
-// The same copy from a scalar base plus the lane's 32-bit byte offset (no
-// per-lane 64-bit address).
 __device__ __forceinline__ void lds_dma16_s(const void* base, uint32_t off, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :

@@ -177,41 +177,14 @@ __device__ __forceinline__ void qmm_finish_chunk(const u32x4 raw, const float (&
   *(u32x4*)((uint16_t*)mm.y + yoff) = o;
 }
 
-// load_slice_prev<K> with a fixed count of load instructions, 2 for K <= 4
-// and 3 above (the previous lane's word, then the lane's K words as 1-4 word
-// loads at 4-byte alignment), which the producers' direct A copies wait
-// around.
-typedef uint32_t u32x2a __attribute__((ext_vector_type(2), aligned(4)));
-typedef uint32_t u32x3a __attribute__((ext_vector_type(3), aligned(4)));
-typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
-template <int N>
-__device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
-  if constexpr (N == 1) {
-    w[0] = __builtin_nontemporal_load(p);
-  } else if constexpr (N == 2) {
-    const u32x2a v = __builtin_nontemporal_load((const u32x2a*)p);
-    w[0] = v[0], w[1] = v[1];
-  } else if constexpr (N == 3) {
-    const u32x3a v = __builtin_nontemporal_load((const u32x3a*)p);
-    w[0] = v[0], w[1] = v[1], w[2] = v[2];
-  } else {
-    static_assert(N == 4, "1-4 words");
-    const u32x4a v = __builtin_nontemporal_load((const u32x4a*)p);
-    w[0] = v[0], w[1] = v[1], w[2] = v[2], w[3] = v[3];
-  }
-}
+// load_slice_prev<K> as raw buffer loads with a fixed count of load
+// instructions, 2 for K <= 4 and 3 above (the previous lane's word, then the
+// lane's K words as 1-4 word loads at 4-byte alignment), which the producers'
+// direct A copies wait around: resource `r`, the step's scalar byte offset
+// `so`, the lane's byte offsets of its words (`lo`) and of the previous lane's
+// last word (`lo_prev`).
 template <int K>
 constexpr int kSliceLoads = K <= 4 ? 2 : 3;
-template <int K>
-__device__ __forceinline__ void load_slice_counted(const uint32_t* __restrict__ p, int prev_off,
-                                                   uint32_t (&w)[K + 1]) {
-  w[0] = __builtin_nontemporal_load(p + prev_off);
-  load_words<(K < 4 ? K : 4)>(p, w + 1);
-  if constexpr (K > 4) load_words<K - 4>(p + 4, w + 5);
-}
-// The same instruction count as raw buffer loads: resource `r`, the step's
-// scalar byte offset `so`, the lane's byte offsets of its words (`lo`) and of
-// the previous lane's last word (`lo_prev`).
 template <int N>
 __device__ __forceinline__ void buffer_words(__amdgpu_buffer_rsrc_t r, uint32_t lo, uint32_t so,
                                              uint32_t* w) {
@@ -351,7 +324,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
       load_slice_prev<K>(tp + (size_t)min(d, qlast) * qstride, prev_off, sl[d]);
     // A: row 8i + (lane >> 3) of the consumer's 16*MB rows; the lane's slot is
     // lane & 7.  At MB >= 2 (trellis slices loaded with a known count of
-    // instructions, load_slice_counted) A goes global -> LDS directly (lds_dma16: lane l
+    // instructions, buffer_slice_counted) A goes global -> LDS directly (lds_dma16_s: lane l
     // of a load fills bytes 16l..16l+15 of its 1 KB region, 8 rows; the swizzle
     // goes to the global side: slot s of row r reads chunk s ^ a_swizzle(r)),
     // issued when the stage frees and waited for before the iteration's barrier

@@ -27,9 +27,16 @@
 namespace exl3 {
 
 
-// Slices per prefetch set of the QMV weight stream (two sets in flight).
+// Slices per prefetch set of the MoE and mapped-expert weight streams (two
+// sets in flight).
 template <int K>
 constexpr int kQmvDepth = K <= 4 ? 4 : 2;
+// Slices per prefetch set of the QMV weight loop (two sets in flight).  With
+// the loop branch-free and the slices buffer loads, shallower sets won (same
+// box, K=4: NS 14.23 -> 13.65 us with 2 instead of 4, 14.8 us with 1; K=5:
+// 24.97 -> 24.41 us with 1 instead of 2).
+template <int K>
+constexpr int kQmvLoopDepth = K <= 4 ? 2 : 1;
 
 // Split-K sums load this many splits' partials together.
 constexpr int kSplitChunk = 8;
@@ -409,7 +416,7 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   const uint32_t loff = (uint32_t)((((size_t)4 * q_lo * TN + pair * 2 + g * TN + hsel) * 8 * K +
                                     j * K) * 4);
   const uint32_t loff_prev = loff + (uint32_t)((j == 0 ? 8 * K - 1 : -1) * 4);
-  constexpr int D = kQmvDepth<K>;
+  constexpr int D = kQmvLoopDepth<K>;
   uint32_t setA[D][K + 1], setB[D][K + 1];
   const int qlast = nquads > 0 ? nquads - 1 : 0;
   const uint32_t qbytes = (uint32_t)qstride * 4u, last_off = (uint32_t)qlast * qbytes;

@@ -309,7 +309,9 @@ __attribute__((amdgpu_waves_per_eu(MB == 4 ? 2 : CB == 2 ? 3 : 4))) void moe_mm_
   // load fills bytes 16l..16l+15 of its 1 KB region, 8 rows of one
   // projection, the swizzle applied to the global address), one barrier per
   // chunk.  After the loop the same bytes hold the row-group sums.
-  constexpr int D = kQmvDepth<K>, C = D;
+  // trellis slices per set and steps per A chunk: 2 (same box, C4: 147.0 ->
+  // 144.2 us against the 4 of the weight-stream default at K <= 4)
+  constexpr int D = 2, C = D;
   constexpr int kRows = 16 * MB, kStep = NPROJ * kRows * 128, kBuf = C * kStep;
   constexpr int kRed = NPROJ * 16 * 128 * 4;
   // two separate objects, so that the compiler sees the loads into one buffer

@@ -27,8 +27,8 @@
 namespace exl3 {
 
 
-// Slices per prefetch set of the MoE and mapped-expert weight streams (two
-// sets in flight).
+// Slices per prefetch set of the mapped-expert weight stream (two sets in
+// flight).
 template <int K>
 constexpr int kQmvDepth = K <= 4 ? 4 : 2;
 // Slices per prefetch set of the QMV weight loop (two sets in flight).  With

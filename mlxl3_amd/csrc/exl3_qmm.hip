@@ -81,6 +81,8 @@ const QmmFn kQmm[3][8][3] = {EXL3_TABLE(run_qmm1), EXL3_TABLE(run_qmm2), EXL3_TA
 
 void launch_prologue(const PrologueParams& p, int members, hipStream_t s) {
   const int64_t groups = ((int64_t)p.rows * (p.in / 128) + 15) / 16;
+  // prologue_kernel indexes jobs in 32 bits: the entry points reject
+  // rows * in > INT32_MAX, so rows * blocks stays below 2^24
   uintptr_t bits = (uintptr_t)p.x;
   for (int i = 0; i < members; ++i) bits |= (uintptr_t)p.suh[i] | (uintptr_t)p.xhat[i];
   if ((bits & 15) == 0)

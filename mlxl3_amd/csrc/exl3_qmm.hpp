@@ -35,16 +35,31 @@ namespace exl3 {
 // lanes per (row, 128-block) job (prologue8).  suh_stride = in gives every
 // row its own scales (exl3_prepare128).  grid (ceil(rows * blocks / 16),
 // members), 256 threads.
+// The (row, 128-block) job of this lane's DPP row when each workgroup of 256
+// threads takes 16 consecutive jobs of a rows x nb grid; returns whether the
+// job exists.  Past-the-end jobs become the last one (all lanes of a DPP row
+// stay active) and are not stored.  The workgroup's first job is divided once,
+// uniformly and in 32 bits (rows * nb < 2^24: the entry points reject
+// rows * in > INT32_MAX); a lane's job lies at most 15 blocks further, so rows
+// advance by subtraction (at most once when a row has 16 blocks or more).
+__device__ __forceinline__ bool job16(int rows, int nb, int& row, int& b) {
+  const uint32_t n = (uint32_t)nb, j0 = blockIdx.x * 16u;
+  const uint32_t row0 = j0 / n;
+  uint32_t bu = j0 - row0 * n + (threadIdx.x >> 4), ru = row0;
+  while (bu >= n) {
+    bu -= n;
+    ++ru;
+  }
+  const bool live = ru < (uint32_t)rows;
+  row = live ? (int)ru : rows - 1;
+  b = live ? (int)bu : nb - 1;
+  return live;
+}
+
 template <bool VEC>
 __global__ __launch_bounds__(256) void prologue_kernel(PrologueParams p) {
-  const int nb = p.in >> 7;
-  const int64_t njobs = (int64_t)p.rows * nb;
-  const int64_t job = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  // past-the-end groups redo the last job (all lanes of a DPP row stay
-  // active) and store nothing
-  const bool live = job < njobs;
-  const int64_t jc = live ? job : njobs - 1;
-  const int row = (int)(jc / nb), b = (int)(jc - (int64_t)row * nb);
+  int row, b;
+  const bool live = job16(p.rows, p.in >> 7, row, b);
   const int c8 = 8 * (threadIdx.x & 15);
   const uint16_t* suh = p.suh[0];
   uint16_t* xhat = p.xhat[0];
@@ -71,12 +86,8 @@ __global__ __launch_bounds__(256) void swiglu_prepare_kernel(const uint16_t* __r
                                                              const uint16_t* __restrict__ down_suh,
                                                              int H, int rows,
                                                              uint16_t* __restrict__ xhat) {
-  const int nb = H >> 7;
-  const int64_t njobs = (int64_t)rows * nb;
-  const int64_t job = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const bool live = job < njobs;  // past-the-end groups redo the last job unstored
-  const int64_t jc = live ? job : njobs - 1;
-  const int row = (int)(jc / nb), b = (int)(jc - (int64_t)row * nb);
+  int row, b;
+  const bool live = job16(rows, H >> 7, row, b);
   const int c = b * 128 + 8 * (threadIdx.x & 15);
   const size_t e = (size_t)row * H + c;
   float a[8], sv[8];

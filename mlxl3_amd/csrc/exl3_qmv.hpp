@@ -259,11 +259,7 @@ __device__ __forceinline__ void h128_lane8(float (&v)[8], int lane) {
 // Tail of prologue8: dst[0..7] = f16(H128(f16(f16(a) * s)) / sqrt(128)) over
 // the row of 16 lanes (stored only if live).
 template <bool VEC>
-__device__ __forceinline__ void finish8(const float (&a)[8], const float (&sv)[8], uint16_t* dst,
-                                        bool live, int lane) {
-  float v[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = round_f16(round_f16(a[i]) * sv[i]);
+__device__ __forceinline__ void finish8_scaled(float (&v)[8], uint16_t* dst, bool live, int lane) {
   h128_lane8(v, lane);
   if (!live) return;
   if constexpr (VEC) {
@@ -276,6 +272,14 @@ __device__ __forceinline__ void finish8(const float (&a)[8], const float (&sv)[8
 #pragma unroll
     for (int i = 0; i < 8; ++i) dst[i] = f2h(v[i] * kHadScale);
   }
+}
+template <bool VEC>
+__device__ __forceinline__ void finish8(const float (&a)[8], const float (&sv)[8], uint16_t* dst,
+                                        bool live, int lane) {
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = round_f16(round_f16(a[i]) * sv[i]);
+  finish8_scaled<VEC>(v, dst, live, lane);
 }
 
 // The activation inputs of prologue8: a[i] = x[xe + i] (f16, bf16 or f32),
@@ -341,6 +345,26 @@ template <bool VEC>
 __device__ __forceinline__ void prologue8(const void* x, int x_dtype, size_t xe,
                                           const uint16_t* sp, uint16_t* dst, bool live,
                                           int lane) {
+  if constexpr (VEC) {
+    // f16 activations: f16(x * suh) of two f16 operands is their IEEE f16
+    // product (the f32 product of two 11-bit significands is exact and at
+    // least 2^-48, so the one rounding to f16 is the only one), two per
+    // packed multiply
+    if (x_dtype == DT_F16) {
+      const u32x4 xw = *(const u32x4*)((const uint16_t*)x + xe);
+      const u32x4 sw = *(const u32x4*)sp;
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t xi = xw[i], si = sw[i];
+        const half2v q = __builtin_bit_cast(half2v, xi) * __builtin_bit_cast(half2v, si);
+        v[2 * i] = (float)q[0];
+        v[2 * i + 1] = (float)q[1];
+      }
+      finish8_scaled<VEC>(v, dst, live, lane);
+      return;
+    }
+  }
   float a[8], sv[8];
   load8<VEC>(x, x_dtype, xe, sp, a, sv);
   finish8<VEC>(a, sv, dst, live, lane);

@@ -149,6 +149,22 @@ __device__ __forceinline__ void moe_gather_wave(const MoeGatherParams& p, int jo
   // a group past the row's end (its last run holding fewer than 4 blocks)
   // recomputes block nb - 1 without storing
   const int c0c = b0 < nb ? c0 : (nb - 1) * 128 + 8 * (lane & 15);
+  if constexpr (VEC) {
+    if (p.x_dtype == DT_F16) {  // packed f16 products (scale8_f16)
+      const uint16_t* xh = (const uint16_t*)p.x + xrow;
+      const u32x4 x0 = *(const u32x4*)(xh + c0c), x1 = *(const u32x4*)(xh + c1);
+      const uint32_t e = p.selected[slot];
+      const bool live = e < (uint32_t)p.experts;
+      const uint16_t* suh = p.gu_suh + ((size_t)(live ? e : 0u) * 2 + proj) * p.in;
+      float v0[8], v1[8];
+      scale8_f16(x0, *(const u32x4*)(suh + c0c), v0);
+      scale8_f16(x1, *(const u32x4*)(suh + c1), v1);
+      uint16_t* dst = p.xgu + ((size_t)proj * p.slots + slot) * p.in;
+      finish8_scaled<VEC>(v0, dst + c0c, live && b0 < nb, lane);
+      finish8_scaled<VEC>(v1, dst + c1, live && b1 < nb, lane);
+      return;
+    }
+  }
   float a0[8], s0[8], a1[8], s1[8];
   load8_act<VEC>(p.x, p.x_dtype, xrow + c0c, a0);
   load8_act<VEC>(p.x, p.x_dtype, xrow + c1, a1);

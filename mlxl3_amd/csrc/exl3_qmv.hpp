@@ -341,26 +341,31 @@ __device__ __forceinline__ void load8(const void* x, int x_dtype, size_t xe, con
 // 16-byte words (VEC; callers whose x, scales or output are not 16-byte
 // aligned take the element-wise loads instead).  All 16 lanes of the row
 // must be active; `live` = false computes without storing.
+// v[i] = f16(x[i] * s[i]) for 8 f16 activations and scales held as raw
+// 16-byte words, as packed f16 products.  Equal to round_f16(round_f16(a) * s)
+// of finish8: the f32 product of two f16 values is exact (11-bit
+// significands, at least 2^-48), so its one rounding to f16 is the IEEE f16
+// product.  Each element is copied to a scalar before the bit cast (this
+// hipcc casts element 0 for every v[i] of an ext-vector operand).
+__device__ __forceinline__ void scale8_f16(const u32x4 xw, const u32x4 sw, float (&v)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t xi = xw[i], si = sw[i];
+    const half2v q = __builtin_bit_cast(half2v, xi) * __builtin_bit_cast(half2v, si);
+    v[2 * i] = (float)q[0];
+    v[2 * i + 1] = (float)q[1];
+  }
+}
+
 template <bool VEC>
 __device__ __forceinline__ void prologue8(const void* x, int x_dtype, size_t xe,
                                           const uint16_t* sp, uint16_t* dst, bool live,
                                           int lane) {
   if constexpr (VEC) {
-    // f16 activations: f16(x * suh) of two f16 operands is their IEEE f16
-    // product (the f32 product of two 11-bit significands is exact and at
-    // least 2^-48, so the one rounding to f16 is the only one), two per
-    // packed multiply
+    // f16 activations: packed f16 products (scale8_f16)
     if (x_dtype == DT_F16) {
-      const u32x4 xw = *(const u32x4*)((const uint16_t*)x + xe);
-      const u32x4 sw = *(const u32x4*)sp;
       float v[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t xi = xw[i], si = sw[i];
-        const half2v q = __builtin_bit_cast(half2v, xi) * __builtin_bit_cast(half2v, si);
-        v[2 * i] = (float)q[0];
-        v[2 * i + 1] = (float)q[1];
-      }
+      scale8_f16(*(const u32x4*)((const uint16_t*)x + xe), *(const u32x4*)sp, v);
       finish8_scaled<VEC>(v, dst, live, lane);
       return;
     }

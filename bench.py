@@ -13,7 +13,10 @@ Protocol:
   windows of exactly --steps steps, each bracketed by torch.cuda.synchronize()
   and HIP events recorded on that stream behind a short device spin (so the
   events time the GPU's work, not the CPU's submission); the headline is the
-  median window (min / mean / max under "timing");
+  median window (min / mean / max under "timing"); before each leg's warmup
+  steps ~50 ms of untimed replays of the leg's own graph bring the GPU to its
+  steady state (short windows would otherwise time the ramp after the setup:
+  20-step NS windows read 15.2 us cold against 14.4 us settled on one box);
 * value = algorithmic bytes per step / time per step, bytes =
   in*out*K/8 + M*in*2 + M*out*2 + in*2 + out*2 (each tensor once);
 * roofline.valu_ceiling: the QMV's measured SQ_INSTS_VALU as an issue-bound
@@ -73,6 +76,21 @@ def make_rotation(n_in, n_out, k, cb, seed, max_copies=None):
     return lins, weights
 
 
+def settle(replay, seconds=0.05):
+    """Replay the leg's own graph (all rotated copies) for `seconds`, untimed,
+    before its warmup steps.  A GPU that has idled or run other work (the
+    CPU-side setup between legs) needs tens of milliseconds of this workload to
+    reach its steady state: 20-step NS windows read 15.2 us right after other
+    work and 14.4 us after 50 ms of the workload on one box (50 ms of dense
+    GEMMs instead left the first windows at 15.5-16 us)."""
+    import torch
+
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        replay()
+        torch.cuda.synchronize()
+
+
 def time_steps(lins, x, steps, warmup, ws, windows=1):
     """Run warmup steps, then `windows` timed windows of exactly `steps` steps
     each, as graph replays on one stream.  Each window is bracketed by HIP
@@ -108,9 +126,10 @@ def time_steps(lins, x, steps, warmup, ws, windows=1):
                 parts[count % n] = capture(count % n)[0]
             parts[count % n].replay()
 
+    if steps % n and steps % n not in parts:
+        parts[steps % n] = capture(steps % n)[0]  # the window's partial graph, captured untimed
+    settle(full.replay)
     run(max(1, warmup))
-    if steps % n:
-        run(steps % n)  # captures the window's partial graph outside the timed region
     torch.cuda.synchronize()
     per = []
     for _ in range(windows):
@@ -133,6 +152,7 @@ def windowed(replay, reps, steps_per_rep, windows):
     import torch
 
     stream = torch.cuda.current_stream()
+    settle(replay)
     per = []
     for _ in range(windows):
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -852,7 +872,9 @@ def main():
         },
         "timing": dict(window_stats(per), steps_per_window=args.steps,
                        protocol="median over windows of exactly `steps` graph-replayed steps, "
-                                "each bracketed by HIP events on the launch stream"),
+                                "each bracketed by HIP events on the launch stream, after "
+                                "~50 ms of untimed replays of the rotation graph (settle) "
+                                "and the warmup steps"),
         "roofline": {
             "bound": "hbm",
             "achieved": round(gbs, 2),

@@ -347,10 +347,15 @@ def cpu_baseline(n_in, n_out, k, cb, rows, scale=1.0):
     }
 
 
-def moe_leg(steps, warmup, windows=21):
-    """C4 expert block (hidden 2048, 128 experts x 768, top-8, 256 tokens, K=3
-    3INST): one SwitchGLU forward per step through the C ABI, graph replays
-    rotating over copies of the 226 MB bank so each step streams it from HBM."""
+def moe_leg(steps, warmup, windows=21, rows=256, experts=128):
+    """C4 expert block (hidden 2048, `experts` experts x 768, top-8, K=3
+    3INST) over `rows` tokens: one SwitchGLU forward per step through the C
+    ABI, graph replays rotating over copies of the bank so each step streams
+    the experts it routes to from HBM.  rows=256 with 128 experts is C4; 1 and 4
+    tokens are the decode shapes (rows < 64: the reference's small-row path);
+    16 experts with 256 tokens is one GPU's share of the bank split 8 ways
+    (expert parallel).  Bytes per step count each routed expert's weights and
+    scales once, plus x and y."""
     import ctypes
 
     import numpy as np
@@ -359,7 +364,7 @@ def moe_leg(steps, warmup, windows=21):
     import mlxl3_amd
     from mlxl3_amd import synth
 
-    in_f, hidden, experts, top_k, k, rows = 2048, 768, 128, 8, 3, 256
+    in_f, hidden, top_k, k = 2048, 768, 8, 3
     layer = synth.moe_layer(4, 500, in_f, hidden, experts, k)
 
     def dev(a):
@@ -376,8 +381,8 @@ def moe_leg(steps, warmup, windows=21):
     moes = [mlxl3_amd.Exl3SwitchGlu(g, bank[1], bank[2], d, bank[4], bank[5], top_k=top_k, k=k, cb=0)
             for g, d in trellises]
     x = dev(synth.activations(4, 510, rows, in_f))
-    sel, sc = synth.moe_routes(4, 520, rows, experts, top_k)
-    sel, sc = dev(sel), dev(sc)
+    sel_np, sc_np = synth.moe_routes(4, 520, rows, experts, top_k)
+    sel, sc = dev(sel_np), dev(sc_np)
     y = torch.empty_like(x)
     lib = mlxl3_amd.load_library()
     nws = int(lib.exl3_moe_workspace_bytes(moes[0]._handle, rows))
@@ -402,15 +407,18 @@ def moe_leg(steps, warmup, windows=21):
     torch.cuda.synchronize()
     reps = max(1, math.ceil(steps / len(moes)))
     ms, per = windowed(g.replay, reps, len(moes), windows)
-    nbytes = bank_bytes + rows * in_f * 2 * 2 + (experts * 2 * in_f + experts * 2 * hidden
-                                                  + experts * hidden + experts * in_f) * 2
+    routed = len(np.unique(sel_np))
+    per_expert = bank_bytes // experts + (2 * in_f + 2 * hidden + hidden + in_f) * 2
+    nbytes = routed * per_expert + rows * in_f * 2 * 2
     gbs = nbytes / (ms * 1e-3) / 1e9
+    workload = f"moe_switchglu_{in_f}x{hidden}_e{experts}_top{top_k}_rows{rows}_k{k}_3inst"
     return {
-        "workload": f"moe_switchglu_{in_f}x{hidden}_e{experts}_top{top_k}_rows{rows}_k{k}_3inst",
+        "workload": workload,
         "ms_per_step": round(ms, 6),
         "steps": reps * len(moes),
         "timing": window_stats(per),
         "bank_copies_rotated": copies,
+        "experts_routed": routed,
         "bytes_per_step": nbytes,
         "gflop_per_step": round(2.0 * rows * top_k * 3 * in_f * hidden / 1e9, 3),
         "roofline": {
@@ -419,10 +427,38 @@ def moe_leg(steps, warmup, windows=21):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(
-                f"moe_switchglu_{in_f}x{hidden}_e{experts}_top{top_k}_rows{rows}_k{k}_3inst"),
+            "traffic": measured_traffic(workload),
         },
     }
+
+
+def shares_leg(steps, warmup, windows=21):
+    """One GPU's share of the multi-GPU layouts (design only beyond one GPU):
+    the NS linear column-sharded 8 ways (4096 x 1792, each GPU owns 14 of the
+    112 column blocks; x replicated, no exchange) at batch 1, and the C4 expert
+    bank split 8 ways by experts (16 experts per GPU) with all 256 tokens x
+    top-8 routed to them (what one GPU runs after the all-to-all dispatch).
+    Same protocol as the headline and C4 legs."""
+    import torch
+
+    from mlxl3_amd import synth
+
+    lins, _w = make_rotation(4096, 1792, 4, 0, seed=2)
+    x = torch.from_numpy(synth.activations(2, 0, 1, 4096)).cuda()
+    ws = torch.zeros(lins[0].workspace_bytes(1) + 4096, dtype=torch.uint8, device="cuda")
+    ms, _, per = time_steps(lins, x, steps, warmup, ws, windows=windows)
+    nbytes = alg_bytes(4096, 1792, 4, 1)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    col = {"workload": "qmv_4096x1792_k4_3inst_m1 (NS column shard 1/8)",
+           "ms_per_step": round(ms, 6), "steps": steps, "timing": window_stats(per),
+           "bytes_per_step": nbytes,
+           "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+    del lins, _w
+    torch.cuda.empty_cache()
+    ep = moe_leg(max(8, steps // 40), max(2, warmup // 40), windows=windows, rows=256, experts=16)
+    ep["workload"] += " (C4 bank expert-parallel share 1/8)"
+    return {"ns_column_shard": col, "moe_expert_share": ep}
 
 
 def mlp_leg(steps, warmup, rows=1, windows=21):
@@ -809,6 +845,13 @@ def main():
     ap.add_argument("--no-qmm", action="store_true", help="skip the QMM M=512 leg")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE SwitchGLU leg")
     ap.add_argument("--no-mlp", action="store_true", help="skip the dense SwiGLU MLP leg")
+    ap.add_argument("--no-moe-decode", action="store_true",
+                    help="skip the MoE decode legs (1 and 4 tokens x top-8 over the C4 bank)")
+    ap.add_argument("--no-shares", action="store_true",
+                    help="skip the one-GPU-share legs (NS column shard, 16-expert bank)")
+    ap.add_argument("--no-ns", action="store_true", help="skip the headline QMV leg (tuning runs)")
+    ap.add_argument("--moe-decode-rows", default="1,4",
+                    help="token counts of the MoE decode legs (comma-separated)")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the C1/C2-sweep/C3/C5 configuration legs")
     ap.add_argument("--no-ceilings", action="store_true",
@@ -843,6 +886,18 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     n_in, n_out, k, cb, rows = args.in_features, args.out_features, args.k, args.cb, args.rows
+    decode_rows = [int(v) for v in args.moe_decode_rows.split(",") if v]
+    if args.no_ns:  # tuning runs of the other legs only (the JSON line then has no headline)
+        result = {}
+        if not args.no_moe_decode:
+            result["moe_decode"] = [moe_leg(max(32, args.steps // 10), max(8, args.warmup // 10),
+                                            rows=r) for r in decode_rows]
+        if not args.no_shares:
+            result["shares"] = shares_leg(args.steps, args.warmup)
+        if not args.no_moe:
+            result["moe"] = moe_leg(max(8, args.steps // 40), max(2, args.warmup // 40))
+        print(json.dumps(result), flush=True)
+        return
     lins, _w = make_rotation(n_in, n_out, k, cb, seed=2, max_copies=args.copies or None)
     x = torch.from_numpy(synth.activations(2, 0, rows, n_in)).cuda()
     ws = torch.zeros(max(l.workspace_bytes(max(rows, 512)) for l in lins[:1]) + 4096,
@@ -917,6 +972,11 @@ def main():
 
     if not args.no_moe:
         result["moe"] = moe_leg(max(8, args.steps // 40), max(2, args.warmup // 40))
+    if not args.no_moe_decode:
+        result["moe_decode"] = [moe_leg(max(32, args.steps // 10), max(8, args.warmup // 10), rows=r)
+                                for r in decode_rows]
+    if not args.no_shares:
+        result["shares"] = shares_leg(args.steps, args.warmup)
     if not args.no_mlp:
         result["mlp"] = mlp_leg(max(24, args.steps // 10), max(4, args.warmup // 10), rows=1)
         result["mlp_m512"] = mlp_leg(max(24, args.steps // 40), max(4, args.warmup // 40), rows=512)

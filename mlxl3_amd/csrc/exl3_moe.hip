@@ -21,7 +21,9 @@ namespace exl3 {
   template __global__ void moe_mm_kernel<K, CB, 2, 2>(MoeMmParams);                  \
   template __global__ void moe_mm_kernel<K, CB, 1, 2>(MoeMmParams);                  \
   template __global__ void moe_mm_kernel<K, CB, 2, 4>(MoeMmParams);                  \
-  template __global__ void moe_mm_kernel<K, CB, 1, 4>(MoeMmParams);
+  template __global__ void moe_mm_kernel<K, CB, 1, 4>(MoeMmParams);                  \
+  template __global__ void moe_dec_gu_kernel<K, CB>(MoeDecParams);                   \
+  template __global__ void moe_dec_down_kernel<K, CB>(MoeDecParams);
 // K = 7 is not a SwitchGLU width (switch_glu_layout rejects it).
 EXL3_INST_CB(EXL3_MOE_INST, 1)
 EXL3_INST_CB(EXL3_MOE_INST, 2)
@@ -54,6 +56,13 @@ static const MoeKernel kGateUp[3][8][3] = {EXL3_MOE_TABLE(2, 1), EXL3_MOE_TABLE(
                                            EXL3_MOE_TABLE(2, 4)};
 static const MoeKernel kDown[3][8][3] = {EXL3_MOE_TABLE(1, 1), EXL3_MOE_TABLE(1, 2),
                                          EXL3_MOE_TABLE(1, 4)};
+typedef void (*MoeDecKernel)(MoeDecParams);
+#define EXL3_DEC_ROW(F, K) {F<K, 0>, F<K, 1>, F<K, 2>}
+#define EXL3_DEC_TABLE(F)                                                                   \
+  {EXL3_DEC_ROW(F, 1), EXL3_DEC_ROW(F, 2), EXL3_DEC_ROW(F, 3), EXL3_DEC_ROW(F, 4),         \
+   EXL3_DEC_ROW(F, 5), EXL3_DEC_ROW(F, 6), {nullptr, nullptr, nullptr}, EXL3_DEC_ROW(F, 8)}
+static const MoeDecKernel kDecGateUp[8][3] = EXL3_DEC_TABLE(moe_dec_gu_kernel);
+static const MoeDecKernel kDecDown[8][3] = EXL3_DEC_TABLE(moe_dec_down_kernel);
 
 struct exl3_moe {
   const uint16_t *gu_trellis, *gu_suh, *gu_svh;
@@ -84,10 +93,41 @@ int moe_splits(const exl3_moe* h, int64_t slots, int block_rows, int k_in, int c
   return std::max(1, std::min(s, k_in / 128));
 }
 
+// The small-row path (decode): up to this many routed slots run as two
+// launches, one workgroup row per slot (moe_dec_*_kernel), where the grouped
+// path's four launches cost more than the weight reuse it offers (C4 bank,
+// top-8, same box: 1 token 29.4 -> 24.4 us, 4 tokens 46.3 -> 40.9, 8 tokens
+// 64.7 -> 60.6 with the first split rule).
+static constexpr int64_t kMoeSmallSlots = 64;
+
+// K-splits of a small-row projection, at most 30 steps of 64 inputs each (the
+// gate/up prologue holds 16 blocks of 128 inputs).  Gate/up: ranges of about
+// 8 steps; down: about 384 workgroups over slots x column blocks with at least
+// 2 steps per range.  Measured on the C4 bank, top-8, same box (us, 1 / 4
+// tokens): gate/up splits 2: 29.0 / 44.6, 4: 24.4 / 40.9, 8: 25.8 / 47.3, 16:
+// 27.8 / 59.6; down splits 1: 27.4 / 44.6, 2: 25.8 / 45.9, 4: 25.7 / 46.7, 12:
+// 30.8 / 61.7 (the down rule's picks: 3 / 1).  EXL3_MOE_SPLITS at create pins
+// both (then the small-row and grouped paths give equal outputs).
+int moe_small_splits(const exl3_moe* h, int64_t slots, int k_in, int col_blocks, bool gate_up) {
+  const int nq = k_in / 64;
+  const int lo = (nq + 29) / 30;
+  if (h->force_splits > 0) return std::max(lo, std::min(h->force_splits, nq));
+  int s;
+  if (gate_up) {
+    s = (nq + 4) / 8;
+  } else {
+    const int64_t base = std::max<int64_t>(1, slots * col_blocks);
+    s = (int)((384 + base / 2) / base);
+    s = std::min(s, std::max(1, nq / 2));
+  }
+  return std::max(std::max(s, 1), lo);
+}
+
 // Workspace layout for `slots` = rows * top_k routed slots.
 struct MoeLayout {
   size_t counts, rank, sorted, expert_count, table, counters, xgu, xd, z, partials, total;
   int max_blocks, ncounters, splits_gu, splits_down, block_rows;
+  int small, small_gu, small_down;  // small-row path and its split counts
 };
 
 bool moe_layout(const exl3_moe* h, int64_t rows, MoeLayout& L) {
@@ -105,14 +145,31 @@ bool moe_layout(const exl3_moe* h, int64_t rows, MoeLayout& L) {
     const int v = atoi(env);
     if (v == 16 || v == 32 || v == 64) L.block_rows = v;
   }
-  // each expert's last block may be partial: sum ceil(c_e/b) <= slots/b + E
-  const int64_t max_blocks = slots / L.block_rows + h->experts + 1;
+  // each routed expert's last block may be partial: sum ceil(c_e/b) <=
+  // slots/b + (experts routed) <= slots/b + min(E, slots).  The expert QMM
+  // grids are sized by this bound, so a decode call (8 slots) launches the
+  // workgroups of 9 blocks, not of E + 1 that exit at once.
+  const int64_t max_blocks = slots / L.block_rows + std::min<int64_t>(h->experts, slots) + 1;
   const int64_t ncounters = max_blocks * (std::max(h->hidden, h->in) / 128);
   if (ncounters > INT32_MAX) return false;
   L.max_blocks = (int)max_blocks;
   L.ncounters = (int)ncounters;
   L.splits_gu = moe_splits(h, slots, L.block_rows, h->in, h->hidden / 128);
   L.splits_down = moe_splits(h, slots, L.block_rows, h->hidden, h->in / 128);
+  // small-row path: its arrival counters (gate/up, down, top-k sums) must fit
+  // the workspace's counter region
+  const int64_t small_counters =
+      slots * (h->hidden / 128 + h->in / 128) + rows * (h->in / 128);
+  L.small = slots <= kMoeSmallSlots && !getenv("EXL3_MOE_GROUPED") &&
+            small_counters * 4 <= (int64_t)kWorkspaceCounterBytes;
+  L.small_gu = L.small ? moe_small_splits(h, slots, h->in, h->hidden / 128, true) : 0;
+  L.small_down = L.small ? moe_small_splits(h, slots, h->hidden, h->in / 128, false) : 0;
+  if (L.small) {  // tuning overrides of the small-row split counts
+    if (const char* env = getenv("EXL3_MOE_SMALL_GU"))
+      L.small_gu = std::max((h->in / 64 + 29) / 30, std::min(atoi(env), h->in / 64));
+    if (const char* env = getenv("EXL3_MOE_SMALL_DOWN"))
+      L.small_down = std::max((h->hidden / 64 + 29) / 30, std::min(atoi(env), h->hidden / 64));
+  }
   size_t off = kWorkspaceCounterBytes;  // the shared counter region stays untouched
   auto take = [&](size_t bytes) {
     size_t at = off;
@@ -128,13 +185,67 @@ bool moe_layout(const exl3_moe* h, int64_t rows, MoeLayout& L) {
   L.xgu = take((size_t)2 * slots * h->in * sizeof(uint16_t));
   L.xd = take((size_t)slots * h->hidden * sizeof(uint16_t));
   L.z = take((size_t)slots * h->in * sizeof(float));  // f32 for f32 / bf16 scores
-  const size_t pgu = L.splits_gu > 1 ? (size_t)L.splits_gu * 2 * slots * h->hidden : 0;
-  const size_t pdn = L.splits_down > 1 ? (size_t)L.splits_down * slots * h->in : 0;
+  const int sgu = std::max(L.splits_gu, L.small_gu), sdn = std::max(L.splits_down, L.small_down);
+  const size_t pgu = sgu > 1 ? (size_t)sgu * 2 * slots * h->hidden : 0;
+  const size_t pdn = sdn > 1 ? (size_t)sdn * slots * h->in : 0;
   L.partials = take(std::max(pgu, pdn) * sizeof(float));
   L.total = off;
   return true;
 }
 }  // namespace
+
+// The small-row path: gate/up (+ SwiGLU glue) and down (+ finish and top-k
+// sum) as two launches over the slots (moe_dec_*_kernel).
+static int moe_forward_small(const exl3_moe* h, const MoeLayout& L, const void* x, int x_type,
+                             int64_t rows, const uint32_t* selected, const void* scores,
+                             int scores_type, void* y, char* ws, hipStream_t s) {
+  const MoeDecKernel gateup = kDecGateUp[h->k - 1][h->cb], down = kDecDown[h->k - 1][h->cb];
+  if (!gateup || !down) return fail(EXL3_EUNSUPPORTED, "no SwitchGLU kernel for K=%d", h->k);
+  const int slots = (int)(rows * h->top_k);
+  MoeDecParams dp{};
+  MoeMmParams& q = dp.m;
+  q.experts = h->experts;
+  q.slots_pad = slots;
+  q.partials = (float*)(ws + L.partials);
+  q.trellis = (const uint32_t*)h->gu_trellis;
+  q.tn_total = 2 * h->experts * h->hidden / 16;
+  q.k_in = h->in;
+  q.width = h->hidden;
+  q.col_blocks = h->hidden / 128;
+  q.splits = L.small_gu;
+  q.gu_svh = h->gu_svh;
+  q.down_suh = h->down_suh;
+  q.xd = (uint16_t*)(ws + L.xd);
+  q.gelu = h->gelu;
+  q.logical_hidden = h->logical_hidden;
+  q.down_svh = h->down_svh;
+  q.scores = scores;
+  q.scores_dtype = scores_type;
+  dp.x = x;
+  dp.x_dtype = x_type;
+  dp.top_k = h->top_k;
+  dp.in = h->in;
+  dp.selected = selected;
+  dp.gu_suh = h->gu_suh;
+  dp.counters = (uint32_t*)ws;  // the workspace's counter region
+  dp.zf = (float*)(ws + L.z);
+  dp.y = y;
+  if (int rc = launch_gate("moe gate/up")) return rc;
+  gateup<<<(unsigned)(slots * q.col_blocks * q.splits), 512, 0, s>>>(dp);
+  if (int rc = check_launch("moe gate/up")) return rc;
+  MoeDecParams dd = dp;
+  dd.m.trellis = (const uint32_t*)h->down_trellis;
+  dd.m.tn_total = h->experts * h->in / 16;
+  dd.m.k_in = h->hidden;
+  dd.m.width = h->in;
+  dd.m.col_blocks = h->in / 128;
+  dd.m.splits = L.small_down;
+  dd.m.xa = q.xd;
+  dd.counters = dp.counters + (size_t)slots * q.col_blocks;
+  if (int rc = launch_gate("moe down")) return rc;
+  down<<<(unsigned)(slots * dd.m.col_blocks * dd.m.splits), 256, 0, s>>>(dd);
+  return check_launch("moe down");
+}
 
 extern "C" {
 
@@ -261,6 +372,8 @@ int exl3_moe_forward(const exl3_moe* h, const void* x, int32_t x_type, int64_t r
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
   const int slots = (int)(rows * h->top_k);
+  if (L.small && (((uintptr_t)x | (uintptr_t)h->gu_suh) & 15) == 0)
+    return moe_forward_small(h, L, x, x_type, rows, selected, scores, scores_type, y, ws, s);
 
   MoePlanParams pp;
   pp.selected = selected;

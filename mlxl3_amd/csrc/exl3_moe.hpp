@@ -236,6 +236,24 @@ __device__ __forceinline__ float weighted(float v16, float score, int scores_dty
   return scores_dtype == DT_F16 ? round_f16(v16 * score) : v16 * score;
 }
 
+// finish_and_reduce's per-slot part (moe.rs:586-609) for columns (lane,
+// lane + 64) of a 128-column block of the down projection's f32 sums (g0, g1):
+// f16(raw) -> staged Hadamard -> f16(* scale) -> f16(* svh) -> * score
+// (weighted).
+__device__ __forceinline__ void moe_down_values(const MoeMmParams& p, int e, int slot, int cblk,
+                                                float g0, float g1, int lane, float& v0,
+                                                float& v1) {
+  v0 = round_f16(g0);
+  v1 = round_f16(g1);
+  h128_wave<true>(v0, v1, lane);
+  v0 = round_f16(v0 * kHadScale);
+  v1 = round_f16(v1 * kHadScale);
+  const uint16_t* sv = p.down_svh + (size_t)e * p.width + cblk * 128;
+  const float sc = load_score(p.scores, p.scores_dtype, slot);
+  v0 = weighted(round_f16(v0 * h2f(sv[lane])), sc, p.scores_dtype);
+  v1 = weighted(round_f16(v1 * h2f(sv[lane + 64])), sc, p.scores_dtype);
+}
+
 // Epilogue of one routed row of a 128-column block: (g0, g1) and (u0, u1) are
 // the f32 sums of columns (lane, lane+64) of the first and last projection.
 template <bool GLU>
@@ -284,17 +302,10 @@ __device__ __forceinline__ void moe_finish_row(const MoeMmParams& p, int e, int 
     dst[lane] = f2h(d0 * kHadScale);
     dst[lane + 64] = f2h(d1 * kHadScale);
   } else {
-    // f16(raw) -> staged Hadamard -> f16(* scale) -> f16(* svh) -> f16(* score)
     (void)u0, (void)u1;
     const int slot = p.sorted_slot[pos];
-    float v0 = round_f16(g0), v1 = round_f16(g1);
-    h128_wave<true>(v0, v1, lane);
-    v0 = round_f16(v0 * kHadScale);
-    v1 = round_f16(v1 * kHadScale);
-    const uint16_t* sv = p.down_svh + (size_t)e * p.width + col0;
-    const float sc = load_score(p.scores, p.scores_dtype, slot);
-    v0 = weighted(round_f16(v0 * h2f(sv[lane])), sc, p.scores_dtype);
-    v1 = weighted(round_f16(v1 * h2f(sv[lane + 64])), sc, p.scores_dtype);
+    float v0, v1;
+    moe_down_values(p, e, slot, cblk, g0, g1, lane, v0, v1);
     const size_t at = (size_t)slot * p.width + col0 + lane;
     if (p.scores_dtype == DT_F16) {
       ((uint16_t*)p.z)[at] = f2h(v0);
@@ -657,6 +668,303 @@ __global__ __launch_bounds__(256) void moe_reduce_kernel(const void* __restrict_
     *(float4v*)((float*)y + o) = float4v{acc[0], acc[1], acc[2], acc[3]};
     *(float4v*)((float*)y + o + 4) = float4v{acc[4], acc[5], acc[6], acc[7]};
   }
+}
+
+// ---------------------------------------------------------------------------
+// Small-row path (decode): one slot per workgroup row
+// ---------------------------------------------------------------------------
+// For a handful of routed slots (the reference runs rows < 64 through its
+// small-row path, moe.rs:925-970) the forward is two launches with no route
+// plan and no gather:
+//   moe_dec_gu_kernel: per (slot, 128 hidden columns, K-range) a workgroup of
+//     8 waves computes the slot's gate and up inputs for its K-range (the
+//     gather's prologue8 on x and gu_suh[e]) into LDS, decodes expert e's gate
+//     (waves 0-3) and up (waves 4-7) tiles and multiplies them with that one
+//     row; the K-ranges meet in the last arriving workgroup, which runs
+//     glu_down_input and writes the down projection's xhat of the slot;
+//   moe_dec_down_kernel: per (slot, 128 output columns, K-range) 4 waves over
+//     the down bank with the slot's xhat read from L2; the last arriver of the
+//     K-ranges computes the slot's weighted values (finish_and_reduce's
+//     per-slot part), and the last of a token's valid slots to finish a
+//     column block sums them in top-k order into y.
+// The K-ranges, the MFMA order of every step and the epilogues are those of
+// moe_mm_kernel, so with the same split count every output equals the grouped
+// path's bit for bit.  Arrival counters sit in the workspace's counter region
+// (zero between calls, reset by each last arriver).  Slots routed to an
+// expert id >= experts contribute nothing.
+struct MoeDecParams {
+  MoeMmParams m;             // bank, widths, epilogue scales, scores
+  const void* x;             // [rows][in] activations
+  int x_dtype, top_k, in;
+  const uint32_t* selected;  // [slots]
+  const uint16_t* gu_suh;    // [E][2][in]
+  uint32_t* counters;        // gate/up: [slots][hidden/128]; down: [slots][in/128]
+                             // then the top-k sums' [rows][in/128]
+  float* zf;                 // [slots][in] weighted slot outputs (f32)
+  void* y;                   // [rows][in] f16 (f16 scores) or f32
+};
+
+// Gate/up: grid slots * (hidden / 128) * splits, 512 threads.
+template <int K, int CB>
+__global__ __launch_bounds__(512) void moe_dec_gu_kernel(MoeDecParams dp) {
+  const MoeMmParams& p = dp.m;
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][16 * 128];  // xhat of the K-range
+  __shared__ float red[2][128];
+  __shared__ int s_last;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int proj = wave >> 2, pair = wave & 3;
+  const int per_slot = p.col_blocks * p.splits;
+  const int slot = blockIdx.x / per_slot, rem = blockIdx.x - slot * per_slot;
+  const int cblk = rem / p.splits, split = rem - cblk * p.splits;
+  const uint32_t eu = dp.selected[slot];
+  if (eu >= (uint32_t)p.experts) return;  // uniform: a slot outside the bank adds nothing
+  const int e = (int)eu, row = slot / dp.top_k;
+  const int nq_all = p.k_in >> 6;
+  const int qa = split * nq_all / p.splits, nq = (split + 1) * nq_all / p.splits - qa;
+  // the K-range's 128-blocks [bq0, bq0 + nbk): wave w of a projection takes
+  // blocks w, w + 4, w + 8, w + 12 (16 lanes each)
+  const int bq0 = qa >> 1, nbk = ((qa + nq + 1) >> 1) - bq0;
+  const int pblk = pair + 4 * (lane >> 4);
+  const bool pwave = pair < nbk;  // uniform
+  Pro8In pin;
+  if (pwave) {
+    const size_t off = (size_t)(bq0 + min(pblk, nbk - 1)) * 128 + (lane & 15) * 8;
+    pin = pro8_load(dp.x, dp.x_dtype, (size_t)row * dp.in + off,
+                    dp.gu_suh + ((size_t)e * 2 + proj) * dp.in + off);
+  }
+  const int g = lane >> 4, hsel = (lane >> 3) & 1, j = lane & 7;
+  const int tpe = p.width / 16;
+  const size_t qstride = (size_t)4 * p.tn_total * 8 * K;
+  const int tcol = (proj * p.experts + e) * tpe + cblk * 8 + 2 * pair + hsel;
+  const uint32_t* tp =
+      p.trellis + ((size_t)(4 * qa + g) * p.tn_total + tcol) * (8 * K) + (size_t)j * K;
+  const int prev_off = j == 0 ? 8 * K - 1 : -1;
+  constexpr int D = 2;
+  uint32_t setA[D][K + 1], setB[D][K + 1];
+  const int qlast = nq - 1;
+  auto fetch = [&](uint32_t(&set)[D][K + 1], int qbase) {
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      load_slice_prev<K>(tp + (size_t)min(qbase + d, qlast) * qstride, prev_off, set[d]);
+  };
+  fetch(setA, 0);
+  if (pwave) pro8_finish(pin, dp.x_dtype, xs[proj] + pblk * 128 + (lane & 15) * 8, pblk < nbk, lane);
+  __syncthreads();
+  const _Float16* xrow = (const _Float16*)xs[proj] + (qa - 2 * bq0) * 64 + 16 * g;
+  float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](uint32_t(&set)[D][K + 1], int qbase) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int q = qbase + d;
+      if (q < nq) {  // uniform
+        const half8 a0 = *(const half8*)(xrow + q * 64);
+        const half8 a1 = *(const half8*)(xrow + q * 64 + 8);
+        qmv_step_prev<K, CB>(set[d], a0, a1, acc0, acc1);
+      }
+    }
+  };
+  for (int q0 = 0; q0 < nq; q0 += 2 * D) {
+    fetch(setB, q0 + D);
+    compute(setA, q0);
+    fetch(setA, q0 + 2 * D);
+    compute(setB, q0 + D);
+  }
+  // accumulator lane l < 16 holds row 0 at column 32*pair + 16*(l/8) + l%8 (+8: acc1)
+  const int col = 32 * pair + 16 * (lane >> 3) + (lane & 7);
+  if (p.splits == 1) {
+    if (g == 0) {
+      red[proj][col] = acc0[0];
+      red[proj][col + 8] = acc1[0];
+    }
+    __syncthreads();
+    if (wave == 0)
+      moe_finish_row<true>(p, e, slot, cblk, red[0][lane], red[0][lane + 64], red[1][lane],
+                           red[1][lane + 64], lane);
+    return;
+  }
+  float* part = p.partials + ((size_t)split * 2 + proj) * p.slots_pad * p.width;
+  if (g == 0) {
+    float* dst = part + (size_t)slot * p.width + cblk * 128 + col;
+    store_coherent(dst, acc0[0]);
+    store_coherent(dst + 8, acc1[0]);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  uint32_t* counter = dp.counters + (size_t)slot * p.col_blocks + cblk;
+  if (threadIdx.x == 0) {
+    const uint32_t old =
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = old == (uint32_t)(p.splits - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;  // uniform
+  if (threadIdx.x == 0)
+    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (wave != 0) return;
+  // split sums in split order (as moe_mm_kernel's last arriver)
+  constexpr int kChunk = kSplitChunk / 2;
+  float v[2][2] = {};
+  for (int s0 = 0; s0 < p.splits; s0 += kChunk) {
+    float t[kChunk][2][2];
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      const int s = min(s0 + c, p.splits - 1);  // clamped: always a written split
+#pragma unroll
+      for (int pj = 0; pj < 2; ++pj) {
+        const float* src =
+            p.partials + ((size_t)(s * 2 + pj) * p.slots_pad + slot) * p.width + cblk * 128;
+        t[c][pj][0] = load_coherent(src + lane);
+        t[c][pj][1] = load_coherent(src + lane + 64);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c)
+      if (s0 + c < p.splits)
+#pragma unroll
+        for (int pj = 0; pj < 2; ++pj) {
+          v[pj][0] += t[c][pj][0];
+          v[pj][1] += t[c][pj][1];
+        }
+  }
+  moe_finish_row<true>(p, e, slot, cblk, v[0][0], v[0][1], v[1][0], v[1][1], lane);
+}
+
+// Down + weighted top-k sum: grid slots * (in / 128) * splits, 256 threads.
+template <int K, int CB>
+__global__ __launch_bounds__(256) void moe_dec_down_kernel(MoeDecParams dp) {
+  const MoeMmParams& p = dp.m;
+  __shared__ float red[128];
+  __shared__ int s_last;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int pair = wave;
+  const int per_slot = p.col_blocks * p.splits;
+  const int slot = blockIdx.x / per_slot, rem = blockIdx.x - slot * per_slot;
+  const int cblk = rem / p.splits, split = rem - cblk * p.splits;
+  const uint32_t eu = dp.selected[slot];
+  if (eu >= (uint32_t)p.experts) return;  // uniform
+  const int e = (int)eu, row = slot / dp.top_k;
+  const int nq_all = p.k_in >> 6;
+  const int qa = split * nq_all / p.splits, nq = (split + 1) * nq_all / p.splits - qa;
+  const int g = lane >> 4, hsel = (lane >> 3) & 1, j = lane & 7;
+  const int tpe = p.width / 16;
+  const size_t qstride = (size_t)4 * p.tn_total * 8 * K;
+  const int tcol = e * tpe + cblk * 8 + 2 * pair + hsel;
+  const uint32_t* tp =
+      p.trellis + ((size_t)(4 * qa + g) * p.tn_total + tcol) * (8 * K) + (size_t)j * K;
+  const int prev_off = j == 0 ? 8 * K - 1 : -1;
+  const _Float16* xrow = (const _Float16*)p.xa + (size_t)slot * p.k_in + qa * 64 + 16 * g;
+  constexpr int D = 2;
+  uint32_t setA[D][K + 1], setB[D][K + 1];
+  const int qlast = nq - 1;
+  auto fetch = [&](uint32_t(&set)[D][K + 1], int qbase) {
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      load_slice_prev<K>(tp + (size_t)min(qbase + d, qlast) * qstride, prev_off, set[d]);
+  };
+  float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](uint32_t(&set)[D][K + 1], int qbase) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int q = qbase + d;
+      if (q < nq) {  // uniform
+        const half8 a0 = *(const half8*)(xrow + q * 64);
+        const half8 a1 = *(const half8*)(xrow + q * 64 + 8);
+        qmv_step_prev<K, CB>(set[d], a0, a1, acc0, acc1);
+      }
+    }
+  };
+  fetch(setA, 0);
+  for (int q0 = 0; q0 < nq; q0 += 2 * D) {
+    fetch(setB, q0 + D);
+    compute(setA, q0);
+    fetch(setA, q0 + 2 * D);
+    compute(setB, q0 + D);
+  }
+  const int col = 32 * pair + 16 * (lane >> 3) + (lane & 7);
+  float s0v, s1v;  // the slot's column sums (wave 0 of the finishing workgroup)
+  if (p.splits == 1) {
+    if (g == 0) {
+      red[col] = acc0[0];
+      red[col + 8] = acc1[0];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    s0v = red[lane];
+    s1v = red[lane + 64];
+  } else {
+    float* part = p.partials + (size_t)split * p.slots_pad * p.width;
+    if (g == 0) {
+      float* dst = part + (size_t)slot * p.width + cblk * 128 + col;
+      store_coherent(dst, acc0[0]);
+      store_coherent(dst + 8, acc1[0]);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    uint32_t* counter = dp.counters + (size_t)slot * p.col_blocks + cblk;
+    if (threadIdx.x == 0) {
+      const uint32_t old =
+          __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = old == (uint32_t)(p.splits - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;  // uniform
+    if (threadIdx.x == 0)
+      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (wave != 0) return;
+    float v0 = 0.f, v1 = 0.f;
+    for (int c0 = 0; c0 < p.splits; c0 += kSplitChunk) {
+      float a[kSplitChunk], b[kSplitChunk];
+#pragma unroll
+      for (int c = 0; c < kSplitChunk; ++c) {
+        const int s = min(c0 + c, p.splits - 1);  // clamped: always a written split
+        const float* src =
+            p.partials + ((size_t)s * p.slots_pad + slot) * p.width + cblk * 128;
+        a[c] = load_coherent(src + lane);
+        b[c] = load_coherent(src + lane + 64);
+      }
+#pragma unroll
+      for (int c = 0; c < kSplitChunk; ++c)
+        if (c0 + c < p.splits) {
+          v0 += a[c];
+          v1 += b[c];
+        }
+    }
+    s0v = v0;
+    s1v = v1;
+  }
+  // wave 0 of the slot's finishing workgroup: its weighted values, then the
+  // token's top-k sum by the last of its valid slots
+  float z0, z1;
+  moe_down_values(p, e, slot, cblk, s0v, s1v, lane, z0, z1);
+  float* zrow = dp.zf + (size_t)slot * p.width + cblk * 128;
+  store_coherent(zrow + lane, z0);
+  store_coherent(zrow + lane + 64, z1);
+  __builtin_amdgcn_s_waitcnt(0);  // the stores are acknowledged before the arrival
+  uint32_t* rcounter =
+      dp.counters + (size_t)p.slots_pad * p.col_blocks + (size_t)row * p.col_blocks + cblk;
+  int valid = 0;
+  for (int t = 0; t < dp.top_k; ++t)
+    valid += dp.selected[(size_t)row * dp.top_k + t] < (uint32_t)p.experts ? 1 : 0;
+  uint32_t old = 0;
+  if (lane == 0) {
+    old = __hip_atomic_fetch_add(rcounter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == (uint32_t)(valid - 1))
+      __hip_atomic_store(rcounter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (__builtin_amdgcn_readfirstlane(old) != (uint32_t)(valid - 1)) return;
+  // y = sum over the token's valid slots in top-k order (moe_reduce_kernel's
+  // order and f32 adds), stored as f16 or f32
+  float y0 = 0.f, y1 = 0.f;
+  for (int t = 0; t < dp.top_k; ++t) {
+    const size_t ts = (size_t)row * dp.top_k + t;
+    if (dp.selected[ts] >= (uint32_t)p.experts) continue;
+    const float* zr = dp.zf + ts * p.width + cblk * 128;
+    y0 += load_coherent(zr + lane);
+    y1 += load_coherent(zr + lane + 64);
+  }
+  const size_t o = (size_t)row * p.width + cblk * 128 + lane;
+  store_reduced(dp.y, p.scores_dtype, o, y0);
+  store_reduced(dp.y, p.scores_dtype, o + 64, y1);
 }
 
 }  // namespace exl3

@@ -375,6 +375,60 @@ __device__ __forceinline__ void prologue8(const void* x, int x_dtype, size_t xe,
   finish8<VEC>(a, sv, dst, live, lane);
 }
 
+// prologue8 split into its loads and its arithmetic, for 16-byte aligned x and
+// scales: the loads of a lane's 8 activations (one 16-byte load, two for f32)
+// and 8 scales are issued early and consumed by pro8_finish, which stores the
+// lane's 8 xhat values as one 16-byte write when `live`.  The results equal
+// prologue8's.  All 16 lanes of the DPP row must be active.
+struct Pro8In {
+  u32x4 x0, x1, s;  // x1: the high 16 bytes of f32 activations
+};
+__device__ __forceinline__ Pro8In pro8_load(const void* x, int x_dtype, size_t xe,
+                                            const uint16_t* sp) {
+  Pro8In in;
+  if (x_dtype == DT_F32) {
+    const u32x4* xp = (const u32x4*)((const float*)x + xe);
+    in.x0 = xp[0];
+    in.x1 = xp[1];
+  } else {
+    in.x0 = *(const u32x4*)((const uint16_t*)x + xe);
+    in.x1 = in.x0;
+  }
+  in.s = *(const u32x4*)sp;
+  return in;
+}
+__device__ __forceinline__ void pro8_finish(const Pro8In& in, int x_dtype, uint16_t* dst,
+                                            bool live, int lane) {
+  float v[8];
+  if (x_dtype == DT_F16) {
+    scale8_f16(in.x0, in.s, v);
+  } else {
+    float sv[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t si = in.s[i];
+      sv[2 * i] = h2f((uint16_t)si);
+      sv[2 * i + 1] = h2f((uint16_t)(si >> 16));
+    }
+    if (x_dtype == DT_F32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = in.x0[i], hi = in.x1[i];
+        v[i] = round_f16(round_f16(__builtin_bit_cast(float, lo)) * sv[i]);
+        v[i + 4] = round_f16(round_f16(__builtin_bit_cast(float, hi)) * sv[i + 4]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t xi = in.x0[i];
+        v[2 * i] = round_f16(round_f16(bf2f((uint16_t)xi)) * sv[2 * i]);
+        v[2 * i + 1] = round_f16(round_f16(bf2f((uint16_t)(xi >> 16))) * sv[2 * i + 1]);
+      }
+    }
+  }
+  finish8_scaled<true>(v, dst, live, lane);
+}
+
 // KW waves share each column pair and split the workgroup's K-range between
 // them (reduced through LDS in a fixed order), so a workgroup of 4*KW waves
 // amortises one prologue over KW times more weight stream.

@@ -104,9 +104,18 @@ def test_moe_and_expert_mapped_fail_when_armed(lib):
     y = np.full((rows, n_in), 0x7E01, np.uint16)
     ws = np.zeros(int(lib.exl3_moe_workspace_bytes(h, rows)), np.uint8)
     lib.exl3_debug_fail_launch(b"moe")
+    # 6 routed slots take the small-row path: gate/up is its first launch
     expect_forced(lib, lib.exl3_moe_forward(h, ptr(x), F16, rows, ptr(sel), ptr(scores), F16,
-                                            ptr(y), ptr(ws), ws.size, None), "moe plan")
+                                            ptr(y), ptr(ws), ws.size, None), "moe gate/up")
     assert (y == 0x7E01).all() and not ws.any()
+    # 66 slots take the grouped path: the route plan is its first launch
+    big = 33
+    xb, yb = ones(big, n_in), np.full((big, n_in), 0x7E01, np.uint16)
+    selb, scb = np.tile(sel, (11, 1)), ones(big, top_k)
+    wsb = np.zeros(int(lib.exl3_moe_workspace_bytes(h, big)), np.uint8)
+    expect_forced(lib, lib.exl3_moe_forward(h, ptr(xb), F16, big, ptr(selb), ptr(scb), F16,
+                                            ptr(yb), ptr(wsb), wsb.size, None), "moe plan")
+    assert (yb == 0x7E01).all() and not wsb.any()
     lib.exl3_moe_destroy(h)
     # the mapped expert QMV
     bank = np.zeros((n_in // 16, E * 8, 16 * k), np.uint16)

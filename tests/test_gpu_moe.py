@@ -144,6 +144,43 @@ def test_moe_c4_full_shape():
     check(y[pick], ref, "moe C4")
 
 
+@pytest.mark.parametrize("rows", [1, 4, 8, 9])
+def test_moe_c4_decode_rows_small_path(rows, monkeypatch):
+    """Up to 64 routed slots (8 tokens x top-8) run the small-row path (two
+    launches, one workgroup row per slot); 9 tokens run the grouped path.  Both
+    vs the oracle on the C4 bank; with the split count pinned the two paths give
+    the same bits (same K-ranges, MFMA order and epilogues), and a token's
+    output does not depend on the other tokens of the call."""
+    print(f"moe C4 decode rows={rows}", flush=True)
+    layer, x, sel, sc = case(2048, 768, 128, 8, rows, 3, 17 + rows)
+    moe = make_moe(layer, 8, 3, 0)
+    y = run(moe, x, sel, sc)
+    check(y, oracle.moe_forward(x, sel, sc, *layer, 3, 0), f"moe C4 decode rows={rows}")
+    monkeypatch.setenv("EXL3_MOE_SPLITS", "3")
+    moe = make_moe(layer, 8, 3, 0)  # the pinned split count is read at create
+    small = run(moe, x, sel, sc)
+    monkeypatch.setenv("EXL3_MOE_GROUPED", "1")
+    grouped = run(moe, x, sel, sc)
+    np.testing.assert_array_equal(small, grouped)
+    monkeypatch.delenv("EXL3_MOE_GROUPED")
+    np.testing.assert_array_equal(run(moe, x[-1:], sel[-1:], sc[-1:]), small[-1:])
+
+
+def test_moe_small_path_invalid_expert_ids():
+    """A slot routed outside the bank adds nothing on the small-row path, as on
+    the grouped one (the reference reads out of its bank)."""
+    layer, x, sel, sc = case(512, 256, 16, 4, 3, 3, 93)
+    sel = sel.copy()
+    sel[1, 2] = 16
+    sel[2, 0] = 1000
+    moe = make_moe(layer, 4, 3, 0)
+    y = run(moe, x, sel, sc)
+    keep = sel < 16
+    ref = oracle.moe_forward(x, np.where(keep, sel, 0).astype(np.uint32),
+                             np.where(keep, sc, 0).astype(sc.dtype), *layer, 3, 0)
+    check(y, ref, "moe small path, ids outside the bank")
+
+
 def _bf16_bits(v):
     b = np.asarray(v, np.float32).view(np.uint32).astype(np.uint64)
     return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)

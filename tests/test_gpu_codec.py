@@ -9,7 +9,10 @@
   per output), 205 lines in all;
 * unpack / codebook against the oracle on the reference's quantizer vectors and
   on every state; mlx-linear / mlx-group / metal-swiglu against the Python
-  mirror's results and the oracle, bit for bit.
+  mirror's results and the oracle, bit for bit;
+* metal-prepare128 and metal-prepare-view on seeded rows, edge values and
+  strided views (the case lists are in the docstrings below), bit for bit
+  against the oracle's prologue and the library's prepare128.
 """
 
 import json
@@ -118,24 +121,44 @@ def test_linear_group_swiglu_ops():
     assert rows[2] == {"data": bits(oracle.swiglu(g, u))}
 
 
+PREP_SEED = 6221
+
+
 def prepare128_cases():
-    """The cases of the reference's tests/physical_prepare128.py (its f16 ones):
-    the 128 basis rows with unit scales, normal rows of widths 128/640/2560 with
-    column or element scales, and subnormal / signed-zero rows."""
-    rng = np.random.default_rng(75)
-    cases = [("all-128-basis-rows", np.eye(128, dtype=np.float16),
-              np.ones((1, 128), dtype=np.float16))]
-    for rows in (1, 3, 20):
-        for width in (128, 640, 2560):
-            x = rng.normal(0, 1.125, (rows, width)).astype(np.float16)
-            for scale_rows in sorted({1, rows}):
-                s = rng.normal(0, 0.75, (scale_rows, width)).astype(np.float16)
-                cases.append((f"mixed-{rows}x{width}-scale-rows-{scale_rows}", x, s))
-    bits = np.array([0x0000, 0x8000, 1, 0x8001, 0x3C00, 0xBC00, 0x0400, 0x8400], dtype=np.uint16)
-    special = np.resize(bits, (3, 128)).view(np.float16)
-    special[1] = np.float16(-0.0)
-    special[2] = np.resize(bits[::-1], 128).view(np.float16)
-    cases.append(("subnormal-signed-zero", special, np.ones_like(special)))
+    """f16 prepare128 cases (input x scale, one f16 product, then the staged
+    H128 of every 128-wide block):
+
+    * the 128 unit rows with unit scales, whose outputs are the normalised
+      Sylvester rows;
+    * rows in (1, 2, 7, 33) x widths (256, 896, 4096) of N(0, 1) inputs with
+      1% outlier channels scaled by 20, with column scales (one row) when
+      rows + width / 128 is even, element scales (one per input) when it is
+      odd, and both for 7 rows; scales +-U(0.5, 1.5);
+    * edge rows: all negative zeros, the smallest subnormals between signed
+      zeros, the largest subnormal beside the smallest normal, and signed
+      ones mixed with subnormals, under unit scales and, by element, under
+      scales of -1 and 2**-10 (which push the products into the subnormals).
+    """
+    cases = [("unit-rows", np.eye(128, dtype=np.float16), np.ones((1, 128), dtype=np.float16))]
+    tid = 0
+    for rows in (1, 2, 7, 33):
+        for width in (256, 896, 4096):
+            x = synth.activations(PREP_SEED, tid, rows, width, outlier_frac=0.01)
+            kinds = (1, rows) if rows == 7 else ((1,) if (rows + width // 128) % 2 == 0 else (rows,))
+            for scale_rows in kinds:
+                s = synth.signs_scales(PREP_SEED, tid + 1 + scale_rows, scale_rows * width)
+                cases.append((f"normal-{rows}x{width}-scales-{scale_rows}", x,
+                              s.reshape(scale_rows, width)))
+            tid += 64
+    edge = np.zeros((4, 256), np.uint16)
+    edge[0] = 0x8000
+    edge[1, 0::4], edge[1, 1::4], edge[1, 2::4], edge[1, 3::4] = 0x0001, 0x8000, 0x8001, 0x0000
+    edge[2, 0::2], edge[2, 1::2] = 0x03FF, 0x8400
+    edge[3] = np.resize(np.array([0x3C00, 0x8002, 0xBC00, 0x0200, 0x83FF], np.uint16), 256)
+    x = edge.view(np.float16)
+    cases.append(("edge-unit-scales", x, np.ones((1, 256), np.float16)))
+    flip = np.resize(np.array([-1.0, 2.0 ** -10, 1.0], np.float16), (4, 256))
+    cases.append(("edge-element-scales", x, np.ascontiguousarray(flip)))
     return cases
 
 
@@ -170,39 +193,86 @@ def test_prepare128_codec_and_abi_match_the_oracle():
     assert np.all(np.abs(np.abs(basis) - 2 ** -3.5) < 2 ** -14)
 
 
-def test_prepare_view_strided_views_match_the_oracle():
-    """The view cases of the reference's physical_prepare128.py: transposed,
-    reversed, negative-stride and broadcast views of f16 and f32 storage with
-    guard words around each backing array, against the oracle on the gathered
-    rows (element scales)."""
-    rng = np.random.default_rng(75)
-    reqs, wants, names = [], [], []
-    for width in (128, 640, 2560):
-        rows = 3
-        for dtype in (np.float16, np.float32):
-            base = rng.normal(0, 0.5, (2 * width + 2, rows + 2)).astype(dtype)
-            scales = rng.normal(0, 0.75, (rows + 2, width + 2)).astype(np.float16)
-            for name, x, sv in (
-                ("transpose-reverse", base[1:-1:2, -2:0:-1].T, scales[1:-1, -2:0:-1]),
-                ("negative-row-col", base[-2:0:-2, -2:0:-1].T, scales[-2:0:-1, 1:-1]),
-                ("row-broadcast", np.broadcast_to(base[1:-1:2, 1], (rows, width)), scales[1:-1, 1:-1]),
-                ("column-broadcast", np.broadcast_to(base[1, 1:-1, None], (rows, width)),
-                 np.broadcast_to(scales[1, 1:-1], (rows, width))),
-            ):
-                def layout(view, backing):
-                    return {"shape": list(view.shape),
-                            "strides": [v // view.itemsize for v in view.strides],
-                            "offset": (view.ctypes.data - backing.ctypes.data) // view.itemsize}
+def off_by_a_little(v16):
+    """float32 values one f32 step away from each non-zero f16 value (away from
+    zero), which a round-to-nearest cast takes back to the f16 value; zeros
+    keep their sign."""
+    v = np.asarray(v16, np.float16).astype(np.float32)
+    return np.where(v == 0, v, np.nextafter(v, np.copysign(np.float32(np.inf), v)))
 
-                field = "x" if dtype == np.float16 else "x_f32"
-                raw = base.view(np.uint16) if dtype == np.float16 else base
-                reqs.append({"op": "metal-prepare-view", field: raw.ravel().tolist(),
-                             "x_layout": layout(x, base), "scale_layout": layout(sv, scales),
-                             "data": scales.view(np.uint16).ravel().tolist()})
-                xs = np.ascontiguousarray(x).astype(np.float16)
+
+def view_layout(view, backing):
+    """Element shape, strides and offset of a numpy view into `backing`."""
+    item = backing.itemsize
+    return {"shape": list(view.shape), "strides": [b // item for b in view.strides],
+            "offset": (view.__array_interface__["data"][0]
+                       - backing.__array_interface__["data"][0]) // item}
+
+
+def test_prepare_view_strided_views_match_the_oracle():
+    """metal-prepare-view on views of f16 and f32 storage (the f32 values one
+    f32 step off f16 values, so the cast rounds them back): widths (256, 1152,
+    3072) with 2, 3 and 5 rows, each input view paired with a scale view of
+    the same shape:
+
+    * column-major input (a transposed backing) with element scales read
+      backwards along each row;
+    * rows taken bottom-up from every second backing row, columns right to
+      left, with column-major scales;
+    * one backing row repeated for every row (row stride 0) with scales of
+      one row repeated the same way;
+    * one backing column repeated along the row (column stride 0) with every
+      other element of a scale row.
+
+    Every backing has guard elements around the viewed region; the outputs are
+    compared bit for bit with the oracle on the gathered rows.
+    """
+    reqs, wants, names = [], [], []
+    tid = 0
+    for width, rows in ((256, 2), (1152, 3), (3072, 5)):
+        for dtype in (np.float16, np.float32):
+            base16 = (synth.normal(PREP_SEED, 500 + tid, (2 * rows + 3) * (width + 4)) * 0.75
+                      ).astype(np.float16).reshape(2 * rows + 3, width + 4)
+            tall16 = (synth.normal(PREP_SEED, 600 + tid, (width + 4) * (rows + 3))
+                      .astype(np.float16).reshape(width + 4, rows + 3))
+            scales = synth.signs_scales(PREP_SEED, 700 + tid, (2 * width + 5) * (rows + 2)).reshape(
+                rows + 2, 2 * width + 5)
+            tscales = np.ascontiguousarray(scales[:, :width + 3].T)  # [width + 3, rows + 2]
+            tid += 1
+            for kind in range(4):
+                if kind == 0:
+                    backing, x = tall16, tall16[2:2 + width, 1:1 + rows].T
+                    sb, sv = scales, scales[1:1 + rows, width + 1:1:-1]
+                elif kind == 1:
+                    backing, x = base16, base16[2 * rows - 1:0:-2, width + 2:2:-1]
+                    sb, sv = tscales, tscales[2:2 + width, 1:1 + rows].T
+                elif kind == 2:
+                    backing = base16
+                    x = np.broadcast_to(base16[rows, 3:3 + width], (rows, width))
+                    sb, sv = scales, np.broadcast_to(scales[rows, 4:4 + width], (rows, width))
+                else:
+                    backing = tall16
+                    x = np.broadcast_to(tall16[1:1 + rows, 2, None], (rows, width))
+                    sb, sv = scales, np.broadcast_to(scales[0, 3:3 + 2 * width:2], (rows, width))
+                assert x.shape == sv.shape == (rows, width)
+                layout = view_layout(x, backing)
+                if dtype == np.float32:
+                    store = off_by_a_little(backing).ravel()
+                    idx = (layout["offset"] + np.arange(rows)[:, None] * layout["strides"][0]
+                           + np.arange(width)[None, :] * layout["strides"][1])
+                    assert np.array_equal(store[idx].astype(np.float16).view(np.uint16),
+                                          np.ascontiguousarray(x).view(np.uint16))
+                    field, raw = "x_f32", store.tolist()
+                else:
+                    field, raw = "x", backing.view(np.uint16).ravel().tolist()
+                reqs.append({"op": "metal-prepare-view", field: raw, "x_layout": layout,
+                             "scale_layout": view_layout(sv, sb),
+                             "data": sb.view(np.uint16).ravel().tolist()})
+                xs = np.ascontiguousarray(x)
                 ss = np.ascontiguousarray(sv)
-                wants.append(np.concatenate([oracle.prologue(xs[r:r + 1], ss[r]) for r in range(rows)]))
-                names.append(f"{name}-{width}-{dtype.__name__}")
+                wants.append(np.concatenate([oracle.prologue(xs[r:r + 1], ss[r])
+                                             for r in range(rows)]))
+                names.append(f"kind{kind}-{rows}x{width}-{np.dtype(dtype).name}")
     rows_out = run(reqs)
     for name, want, row in zip(names, wants, rows_out):
         got = np.array(row["data"], np.uint16)

@@ -641,11 +641,13 @@ def _rotated_time(n_in, n_out, k, cb, rows, steps, warmup, gen, x=None):
     return ms, reps * copies
 
 
-def configs_leg(steps, warmup):
+def configs_leg(steps, warmup, which=("c1", "c2", "c3", "c5"), c2_k=(3, 4, 5),
+                c2_m=(16, 128, 512, 2048), c5_k=(2, 4), c5_m=(4, 8, 16)):
     """The remaining configurations of the measurement plan at one GPU:
     C1 (QMV 4096x4096), the C2 QMM sweep ({4096->14336, 14336->4096} x K{3,4,5}
     x M{16,128,512,2048}, 1 % x20 outlier channels), C3 (32 chained dense
-    decoder layers at batch 1) and C5 (27B-class verify block, MCG)."""
+    decoder layers at batch 1) and C5 (27B-class verify block, MCG).  `which`
+    and the K / M lists pick a subset (profiling runs)."""
     import torch
 
     import mlxl3_amd
@@ -653,16 +655,16 @@ def configs_leg(steps, warmup):
 
     gen = torch.Generator(device="cuda").manual_seed(3)
     out = {}
-    # C1
-    ms, n = _rotated_time(4096, 4096, 4, 0, 1, steps, warmup, gen)
-    b = alg_bytes(4096, 4096, 4, 1)
-    out["c1"] = {"workload": "qmv_4096x4096_k4_3inst_m1", "ms_per_step": round(ms, 6), "steps": n,
-                 "gbs": round(b / ms / 1e6, 1), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)}
-    # C2
+    if "c1" in which:
+        ms, n = _rotated_time(4096, 4096, 4, 0, 1, steps, warmup, gen)
+        b = alg_bytes(4096, 4096, 4, 1)
+        out["c1"] = {"workload": "qmv_4096x4096_k4_3inst_m1", "ms_per_step": round(ms, 6),
+                     "steps": n, "gbs": round(b / ms / 1e6, 1),
+                     "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)}
     sweep = []
-    for n_in, n_out in ((4096, 14336), (14336, 4096)):
-        for k in (3, 4, 5):
-            for m in (16, 128, 512, 2048):
+    for n_in, n_out in ((4096, 14336), (14336, 4096)) if "c2" in which else ():
+        for k in c2_k:
+            for m in c2_m:
                 x = torch.from_numpy(synth.activations(2, m, m, n_in, outlier_frac=0.01)).cuda()
                 st = max(20, steps // (4 if m <= 128 else 40 if m == 512 else 160))
                 ms, n = _rotated_time(n_in, n_out, k, 0, m, st, max(4, warmup // 10), gen, x=x)
@@ -674,9 +676,12 @@ def configs_leg(steps, warmup):
                 if m == 16:
                     entry["frac_hbm"] = round(b / ms / 1e6 / HBM_PEAK_GBS, 4)
                 sweep.append(entry)
-    out["c2"] = sweep
-    out["c3"] = _c3_chain(gen, max(3, steps // 200), 2)
-    out["c5"] = _c5_layers(gen, max(10, steps // 40), max(2, warmup // 40))
+    if sweep:
+        out["c2"] = sweep
+    if "c3" in which:
+        out["c3"] = _c3_chain(gen, max(3, steps // 200), 2)
+    if "c5" in which:
+        out["c5"] = _c5_layers(gen, max(10, steps // 40), max(2, warmup // 40), c5_k, c5_m)
     return out
 
 
@@ -741,7 +746,7 @@ def _c3_chain(gen, steps, warmup):
             "out_rms": round(float(y.pow(2).mean().sqrt()), 3)}
 
 
-def _c5_layers(gen, steps, warmup):
+def _c5_layers(gen, steps, warmup, ks=(2, 4), m_values=(4, 8, 16)):
     """C5: one 27B-class layer of 7 linears (q/k/v as one group, o, gate/up as
     one group, down) at M in {4, 8, 16}, K in {2, 4}, MCG, rotating over layer
     copies."""
@@ -751,7 +756,7 @@ def _c5_layers(gen, steps, warmup):
 
     hid, inter, kv = 5120, 27648, 1024
     res = []
-    for k in (2, 4):
+    for k in ks:
         per = (hid * (hid + 2 * kv) + hid * hid + 2 * hid * inter + inter * hid) * k // 8
         copies = max(2, math.ceil(ROTATE_BYTES / per))
         layers = []
@@ -760,7 +765,7 @@ def _c5_layers(gen, steps, warmup):
             g, u, d = _dev_linear(hid, inter, k, 1, gen), _dev_linear(hid, inter, k, 1, gen), \
                 _dev_linear(inter, hid, k, 1, gen)
             layers.append((mlxl3_amd.Exl3Group([q, kk, v]), o, mlxl3_amd.Exl3Group([g, u]), d))
-        for m in (4, 8, 16):
+        for m in m_values:
             xh = torch.randn(m, hid, device="cuda", generator=gen).half()
             xi = torch.randn(m, inter, device="cuda", generator=gen).half()
 
@@ -854,6 +859,13 @@ def main():
                     help="token counts of the MoE decode legs (comma-separated)")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the C1/C2-sweep/C3/C5 configuration legs")
+    ap.add_argument("--configs-only", default="",
+                    help="run only these configuration legs (comma list of c1, c2, c3, c5) and "
+                         "print their JSON (profiling runs; no headline)")
+    ap.add_argument("--c2-k", default="3,4,5", help="C2 sweep K values (with --configs-only)")
+    ap.add_argument("--c2-m", default="16,128,512,2048", help="C2 sweep M values")
+    ap.add_argument("--c5-k", default="2,4", help="C5 K values")
+    ap.add_argument("--c5-m", default="4,8,16", help="C5 block sizes")
     ap.add_argument("--no-ceilings", action="store_true",
                     help="skip the measured stream-read / fp16 GEMM / GEMV reference ceilings")
     ap.add_argument("--k", type=int, default=4)
@@ -887,6 +899,13 @@ def main():
         del src, dst
     n_in, n_out, k, cb, rows = args.in_features, args.out_features, args.k, args.cb, args.rows
     decode_rows = [int(v) for v in args.moe_decode_rows.split(",") if v]
+    if args.configs_only:  # profiling runs of configuration legs only
+        ints = lambda v: tuple(int(t) for t in v.split(",") if t)  # noqa: E731
+        print(json.dumps({"configs": configs_leg(
+            args.steps, args.warmup, which=tuple(args.configs_only.split(",")),
+            c2_k=ints(args.c2_k), c2_m=ints(args.c2_m), c5_k=ints(args.c5_k),
+            c5_m=ints(args.c5_m))}), flush=True)
+        return
     if args.no_ns:  # tuning runs of the other legs only (the JSON line then has no headline)
         result = {}
         if not args.no_moe_decode:

@@ -4,6 +4,9 @@ Each kernel family is its own translation unit; they compile in parallel and
 link into one shared object that exports the C ABI of include/exl3_hip.h.
 
     python -m mlxl3_amd.build            # build (always recompiles)
+
+build(defines=..., lib=...) makes a variant of the library (the phase-probe
+build of mlxl3_amd/phases.py) without touching the default one.
 """
 
 from __future__ import annotations
@@ -55,8 +58,8 @@ def hipcc() -> str:
     return path
 
 
-def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, obj: Path, defines=()) -> None:
+    cmd = [hipcc(), *HIPCC_FLAGS, *(f"-D{d}" for d in defines), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(line for line in res.stderr.splitlines() if noise not in line)
@@ -66,21 +69,29 @@ def _compile(src: Path, obj: Path) -> None:
         print(err, file=sys.stderr)
 
 
-def build(verbose: bool = True) -> Path:
-    """Compile every translation unit and link LIB; returns its path."""
+def build(verbose: bool = True, defines=(), lib: Path = LIB) -> Path:
+    """Compile every translation unit and link `lib` (LIB and the codec driver
+    by default; a variant library alone when `lib` is another path); returns
+    the library's path."""
     srcs = [CSRC / s for s in SOURCES]
+    lib = Path(lib)
     with tempfile.TemporaryDirectory(prefix="exl3_build_") as tmp:
         objs = [Path(tmp) / (s.stem + ".o") for s in srcs]
         jobs = min(len(srcs), max(1, os.cpu_count() or 1))
         with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
-            list(pool.map(_compile, srcs, objs))
+            list(pool.map(lambda so: _compile(*so, defines), zip(srcs, objs)))
         tmp_lib = Path(tmp) / LIB.name
         cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp_lib)]
         cmd += [str(o) for o in objs]
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             raise RuntimeError(f"link failed:\n{res.stderr}")
-        shutil.copy2(tmp_lib, LIB)
+        lib.parent.mkdir(parents=True, exist_ok=True)
+        shutil.copy2(tmp_lib, lib)
+        if lib != LIB:
+            if verbose:
+                print(f"built {lib}")
+            return lib
         # the codec driver: host code against the library just built
         tmp_codec = Path(tmp) / CODEC.name
         cmd = [hipcc(), "-O2", "-std=c++17", "-Wall", str(CSRC / "exl3_codec.cpp"), "-o",

@@ -132,3 +132,14 @@ const DecodeFn kDecode[8][3] = EXL3_TABLE(run_decode);
 #endif
 
 }  // namespace exl3
+
+#ifdef EXL3_QMV_PHASES
+// The phase-probe build's stamp buffer for the single-row QMV (a device
+// pointer with room for kPhaseWords words per wave of a launch, or NULL to
+// stop recording).  Not part of the library's ABI: only this build has it.
+extern "C" int exl3_debug_phase_buffer(void* dev) {
+  return hipMemcpyToSymbol(HIP_SYMBOL(exl3::qmv_phase_out), &dev, sizeof(dev)) == hipSuccess ? 0
+                                                                                             : -2;
+}
+#endif
+

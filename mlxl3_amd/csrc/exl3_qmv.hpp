@@ -26,6 +26,20 @@
 
 namespace exl3 {
 
+// Phase stamps of the single-row QMV, compiled only into the phase-probe build
+// of the library (-DEXL3_QMV_PHASES; mlxl3_amd/phases.py drives it).  While
+// qmv_phase_out is set, every wave of a single-row launch writes kPhaseWords
+// words at qmv_phase_out[(workgroup * waves + wave) * kPhaseWords]: the
+// 100 MHz realtime counter at entry, at the loop start and end, at its
+// counter arrival and at the end of the epilogue (last arrivers), the shader
+// clock at the loop start and end, and HW_ID | XCC_ID << 32 | last << 48.
+#ifdef EXL3_QMV_PHASES
+static __device__ unsigned long long* qmv_phase_out;
+constexpr int kPhaseWords = 8;
+#define EXL3_PHASE(stmt) stmt
+#else
+#define EXL3_PHASE(stmt)
+#endif
 
 // Slices per prefetch set of the mapped-expert weight stream (two sets in
 // flight).
@@ -429,6 +443,25 @@ __device__ __forceinline__ void pro8_finish(const Pro8In& in, int x_dtype, uint1
   finish8_scaled<true>(v, dst, live, lane);
 }
 
+#ifdef EXL3_QMV_PHASES
+// Lane 0 of each wave writes its stamps (words 0..6; word 7, the end of the
+// epilogue, follows for last arrivers).
+__device__ __forceinline__ void phase_record(unsigned long long (&ph)[kPhaseWords], int last,
+                                             int lane, int wave, int kw) {
+  ph[3] = __builtin_amdgcn_s_memrealtime();
+  // HW_ID (wave, SIMD, CU, SH, SE) and XCC_ID, read with s_getreg_b32
+  const unsigned long long hw = (uint32_t)__builtin_amdgcn_s_getreg((31 << 11) | 4);
+  const unsigned long long xcc = (uint32_t)__builtin_amdgcn_s_getreg((31 << 11) | 20) & 0xffu;
+  ph[6] = hw | xcc << 32 | (unsigned long long)(last != 0) << 48;
+  if (qmv_phase_out && lane == 0) {
+    unsigned long long* o =
+        qmv_phase_out + ((size_t)(blockIdx.y * gridDim.x + blockIdx.x) * 4 * kw + wave) * kPhaseWords;
+#pragma unroll
+    for (int i = 0; i < 7; ++i) o[i] = ph[i];
+  }
+}
+#endif
+
 // KW waves share each column pair and split the workgroup's K-range between
 // them (reduced through LDS in a fixed order), so a workgroup of 4*KW waves
 // amortises one prologue over KW times more weight stream.
@@ -456,6 +489,8 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   const int q_hi = KW == 1 ? nq_wg : (kpart + 1) * nq_wg / KW;
   const int nquads = q_hi - q_lo;
   const int M = p.M;
+  EXL3_PHASE(unsigned long long ph[kPhaseWords] = {};
+             ph[0] = __builtin_amdgcn_s_memrealtime();)
   // Issue priority falls with progress (3 -> 0 over the K-range): the SIMD's
   // arbiter otherwise favours the oldest wave, which starves later waves until
   // it finishes and leaves them to run alone at single-wave efficiency.
@@ -483,7 +518,6 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   __builtin_amdgcn_sched_barrier(0);
 
   const int g = lane >> 4, hsel = (lane >> 3) & 1, j = lane & 7;
-  const int tn0 = cblk_l * 8 + pair * 2;
   const size_t qstride = (size_t)4 * TN * 8 * K;  // words per quad of tile rows
   // The weight loads are buffer loads from the workgroup's base (its first
   // tile row and column block: uniform, so the resource sits in scalar
@@ -571,6 +605,7 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
     }
   }
   __syncthreads();
+  EXL3_PHASE(ph[1] = __builtin_amdgcn_s_memrealtime(); ph[4] = __builtin_amdgcn_s_memtime();)
 
   // main loop: two sets of D slices in ping-pong; the D loads of one set are
   // issued together, then the other set (already in flight for D steps) is
@@ -621,6 +656,7 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
     compute(setB, q0 + D, false);
   }
 
+  EXL3_PHASE(ph[2] = __builtin_amdgcn_s_memrealtime(); ph[5] = __builtin_amdgcn_s_memtime();)
   // K-parts of a pair meet in LDS; part 0 adds them in part order
   if constexpr (KW > 1) {
     if (kpart > 0) {
@@ -639,6 +675,7 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   const bool writer = kpart == 0;
 
   // accumulator lane l: rows 4*(l/16)+r, column 16*(tn0 + n/8) + n%8 + 8*cg
+  // (tn0 = cblk_l*8 + 2*pair, the pair's first tile)
   // of the member; partials are laid out by global column
   const int n = lane & 15;
   const int col = 128 * cblk + 16 * (pair * 2 + (n >> 3)) + (n & 7);
@@ -689,12 +726,18 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
       s_last = (old == (uint32_t)(arrivals - 1));
     }
     __syncthreads();
+#ifdef EXL3_QMV_PHASES
+    if (!MULTI) phase_record(ph, s_last, lane, wave, KW);
+#endif
     if (!s_last) return;  // uniform across the workgroup
     if (threadIdx.x == 0)
       __hip_atomic_store(&p.counters[cidx], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+#ifdef EXL3_QMV_PHASES
+    if (!MULTI) phase_record(ph, 1, lane, wave, KW);
+#endif
   }
   const int colb_l = cblk_l * 128;
   // Split sums: the loads of kSplitChunk splits go out together (one round
@@ -750,6 +793,12 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
       finish_row128(v0, v1, lane, colb_l, mm.svh, mm.bias, mm.y, mm.y_dtype, p.x_dtype,
                     (size_t)m * mm.out);
     }
+#ifdef EXL3_QMV_PHASES
+    __builtin_amdgcn_s_waitcnt(0);  // the output stores have landed
+    if (qmv_phase_out && lane == 0)
+      qmv_phase_out[((size_t)(blockIdx.y * gridDim.x + blockIdx.x) * 4 * KW + wave) * kPhaseWords +
+                    7] = __builtin_amdgcn_s_memrealtime();
+#endif
   } else if constexpr (!FRAG) {
     // rows of the block from row-major partials (the split loads of a batch go
     // out together, each row adding its splits in split order)

@@ -279,11 +279,21 @@ static void group_qmv_shape(const Group& g, int* splits, int* kw) {
 // prologue jobs, a few hundred cycles each); once that reaches 64 jobs per
 // workgroup, one separate prologue launch (~3.5 us) is cheaper.  Measured on
 // MI355X: 4096x14336 M=8 22.5 vs 24.1 us, M=4 21.2 vs 19.8 us; 4096x4096 M=16
-// 20.7 vs 19.2 us.
+// 20.7 vs 19.2 us.  Every column block repeats the jobs of its K-range, so a
+// launch computes rows x blocks x column blocks of them in all: multi-row
+// launches past kProloguePerLaunch jobs also take the separate launch (the
+// 4-row gate/up of a 5120 -> 2 x 27648 group repeats 69 k jobs, ~10 us of VALU
+// issue).  EXL3_QMV_PROLOGUE_JOBS overrides that total (0: off; tuning).
+static constexpr int64_t kProloguePerLaunch = 20480;
 static bool qmv_separate_prologue(const Group& g, int64_t rows, int splits) {
+  static const int64_t per_launch = [] {
+    const char* env = getenv("EXL3_QMV_PROLOGUE_JOBS");
+    return env ? (int64_t)atoll(env) : kProloguePerLaunch;
+  }();
   const int nb = g.in / 128;
   const int blocks = (nb + splits - 1) / splits;  // the largest K-range of a split
-  return rows * blocks >= 64;
+  if (rows * blocks >= 64) return true;
+  return rows > 1 && per_launch > 0 && rows * nb * (int64_t)(g.total_out / 128) >= per_launch;
 }
 
 // Multi-row QMVs of at least this many rows (one K-part per column pair)

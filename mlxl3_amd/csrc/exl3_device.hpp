@@ -277,6 +277,19 @@ __device__ __forceinline__ half8 decode_fragment(const uint32_t (&src)[32]) {
   return __builtin_bit_cast(half8, d);
 }
 
+// Two B fragments written by the decode's inline assembly, passed through one
+// `s_nop 1` on their way to the MFMAs.  A VALU write of a VGPR needs 2 wait
+// states before an MFMA reads that VGPR; the compiler inserts them only for
+// writes it can see, and the decode's SDWA adds are inline assembly to it.
+// Without this some schedules left 1 wait state between the last half-write of
+// a fragment and its MFMA, which then read the register's previous value
+// (wrong, run-to-run varying partial sums of the second tile of a pair).
+// The statement is volatile: as a plain asm statement the scheduler was free to
+// move it, and the schedules it chose were slower (NS QMV 14.06 -> 15.85 us).
+__device__ __forceinline__ void mfma_operand_fence(half8& b0, half8& b1) {
+  asm volatile("s_nop 1" : "+v"(b0), "+v"(b1));
+}
+
 __device__ __forceinline__ float4v mfma16(half8 a, half8 b, float4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

@@ -443,10 +443,12 @@ __attribute__((amdgpu_waves_per_eu(MB == 4 ? 2 : CB == 2 ? 3 : 4))) void moe_mm_
       if (q < nq) {  // uniform
         uint32_t src[32];
         extract_states<K>(cur[d], src);
-        const half8 b00 = decode_fragment<CB, K, 0, 0>(src);
-        const half8 b01 = decode_fragment<CB, K, 0, 1>(src);
-        const half8 b10 = decode_fragment<CB, K, 1, 0>(src);
-        const half8 b11 = decode_fragment<CB, K, 1, 1>(src);
+        half8 b00 = decode_fragment<CB, K, 0, 0>(src);
+        half8 b01 = decode_fragment<CB, K, 0, 1>(src);
+        half8 b10 = decode_fragment<CB, K, 1, 0>(src);
+        half8 b11 = decode_fragment<CB, K, 1, 1>(src);
+        mfma_operand_fence(b00, b01);
+        mfma_operand_fence(b10, b11);
         const uint8_t* st = (b ? abuf1 : abuf0) + d * kStep;
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)

@@ -63,6 +63,43 @@ __device__ __forceinline__ float load_coherent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// v0 += sum over splits s of col[s * stride + lane], v1 likewise at lane + 64,
+// added in split order.  Coherent loads are served one after another (~50 ns
+// each, measured), so exactly `splits` of them are issued per column, up to
+// kSplitChunk splits in flight at a time.
+template <int C>
+__device__ __forceinline__ void sum_split_chunk(const float* col, size_t stride, int s0, int lane,
+                                                float& v0, float& v1) {
+  float a[C], b[C];
+#pragma unroll
+  for (int i = 0; i < C; ++i) {
+    const float* ps = col + (size_t)(s0 + i) * stride;
+    a[i] = load_coherent(ps + lane);
+    b[i] = load_coherent(ps + lane + 64);
+  }
+#pragma unroll
+  for (int i = 0; i < C; ++i) {
+    v0 += a[i];
+    v1 += b[i];
+  }
+}
+__device__ __forceinline__ void sum_split_columns(const float* col, size_t stride, int splits,
+                                                  int lane, float& v0, float& v1) {
+  int s0 = 0;
+  for (; s0 + kSplitChunk <= splits; s0 += kSplitChunk)
+    sum_split_chunk<kSplitChunk>(col, stride, s0, lane, v0, v1);
+  switch (splits - s0) {
+    case 7: sum_split_chunk<7>(col, stride, s0, lane, v0, v1); break;
+    case 6: sum_split_chunk<6>(col, stride, s0, lane, v0, v1); break;
+    case 5: sum_split_chunk<5>(col, stride, s0, lane, v0, v1); break;
+    case 4: sum_split_chunk<4>(col, stride, s0, lane, v0, v1); break;
+    case 3: sum_split_chunk<3>(col, stride, s0, lane, v0, v1); break;
+    case 2: sum_split_chunk<2>(col, stride, s0, lane, v0, v1); break;
+    case 1: sum_split_chunk<1>(col, stride, s0, lane, v0, v1); break;
+    default: break;
+  }
+}
+
 // Load the previous lane's last word of the same tile (word j*K-1, wrapping to
 // the tile's last word for j == 0) and then the K words of this lane's slice
 // of a tile: w[0] = previous word, w[1..K] = own words.  `p` points at the
@@ -116,10 +153,12 @@ __device__ __forceinline__ void qmv_step_prev(const uint32_t (&B)[K + 1], half8 
   extract_states<K>(B, src);
   half8 b00 = decode_fragment<CB, K, 0, 0>(src);
   half8 b01 = decode_fragment<CB, K, 0, 1>(src);
+  mfma_operand_fence(b00, b01);
   acc0 = mfma16(a0, b00, acc0);
   acc1 = mfma16(a0, b01, acc1);
   half8 b10 = decode_fragment<CB, K, 1, 0>(src);
   half8 b11 = decode_fragment<CB, K, 1, 1>(src);
+  mfma_operand_fence(b10, b11);
   acc0 = mfma16(a1, b10, acc0);
   acc1 = mfma16(a1, b11, acc1);
 }
@@ -746,22 +785,7 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   auto sum_row = [&](int m, int colg, float& v0, float& v1) {
     v0 = 0.f;
     v1 = 0.f;
-    for (int s0 = 0; s0 < p.splits; s0 += kSplitChunk) {
-      float a[kSplitChunk], b[kSplitChunk];
-#pragma unroll
-      for (int i = 0; i < kSplitChunk; ++i) {
-        const int s = min(s0 + i, p.splits - 1);  // clamped: always a written split
-        const float* ps = p.partials + ((size_t)s * M + m) * TO + colg;
-        a[i] = load_coherent(ps + lane);
-        b[i] = load_coherent(ps + lane + 64);
-      }
-#pragma unroll
-      for (int i = 0; i < kSplitChunk; ++i)
-        if (s0 + i < p.splits) {
-          v0 += a[i];
-          v1 += b[i];
-        }
-    }
+    sum_split_columns(p.partials + (size_t)m * TO + colg, (size_t)M * TO, p.splits, lane, v0, v1);
   };
   // a (gate, up) row of the block: staged H128, *svh, +bias, f16 SwiGLU and,
   // for the fused MLP, the down projection's prologue

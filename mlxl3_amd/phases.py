@@ -100,6 +100,7 @@ def run(n_in: int, n_out: int, k: int, cb: int, reps: int, seed: int) -> None:
 
     phase = {name: [] for name in ("start", "prologue", "loop", "exchange", "epilogue", "end")}
     clocks, spans = [], []
+    by_xcc = {}  # per XCD: (loop end from the launch's first entry, loop time)
     placement = None
     for rep in range(reps):
         buf.zero_()
@@ -129,6 +130,7 @@ def run(n_in: int, n_out: int, k: int, cb: int, reps: int, seed: int) -> None:
             if t[2] > t[1]:
                 clocks.append((t[5] - t[4]) / ((t[2] - t[1]) * 10.0))
             hw, xcc = t[6] & 0xFFFFFFFF, (t[6] >> 32) & 0xFF
+            by_xcc.setdefault(xcc, []).append(((t[2] - t00) * 10, (t[2] - t[1]) * 10))
             cu = (xcc, (hw >> 13) & 7, (hw >> 12) & 1, (hw >> 8) & 15)
             simd_waves[cu + ((hw >> 4) & 3,)] += 1
             cu_waves[cu] += 1
@@ -155,6 +157,14 @@ def run(n_in: int, n_out: int, k: int, cb: int, reps: int, seed: int) -> None:
         q = quantiles(v)
         if q:
             print(f"| {name} | " + " | ".join(f"{int(round(a))}" for a in q) + " |")
+    print()
+    print("| XCD | waves | loop median (ns) | loop max | loop end median | loop end max |")
+    print("|---|---|---|---|---|---|")
+    for xcc in sorted(by_xcc):
+        ends = sorted(e for e, _ in by_xcc[xcc])
+        loops = sorted(d for _, d in by_xcc[xcc])
+        print(f"| {xcc} | {len(ends) // reps} | {loops[len(loops) // 2]} | {loops[-1]} | "
+              f"{ends[len(ends) // 2]} | {ends[-1]} |")
 
 
 def main() -> None:

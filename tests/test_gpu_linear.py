@@ -327,3 +327,24 @@ def test_invalid_input_raises_without_launch():
         lin.forward(torch.zeros(1, 128, dtype=torch.float16, device="cuda"))
     with pytest.raises(mlxl3_amd.Exl3Error):
         lin.forward(torch.zeros(0, 256, dtype=torch.float16, device="cuda"))
+
+
+@pytest.mark.parametrize("n_in,n_out,rows,k,cb", [
+    (4096, 14336, 1, 4, 0), (4096, 14336, 4, 4, 0), (14336, 4096, 1, 4, 0),
+    (4096, 4096, 1, 3, 0), (4096, 4096, 1, 5, 1), (2048, 6144, 2, 2, 2),
+])
+def test_repeat_calls_bit_identical(n_in, n_out, rows, k, cb):
+    """Regression: the decode writes the MFMA B fragments with inline assembly,
+    which the compiler's hazard recognizer does not see, so a schedule with one
+    wait state between the last half-write of a fragment and its MFMA fed the
+    MFMA the register's previous value.  That showed as outputs that changed
+    from call to call (the second tile of each column pair) while staying close
+    to the oracle.  Five calls of one input must agree bit for bit, and the
+    first must match the oracle."""
+    lin, (tr, suh, svh, _) = make_layer(31 + k, n_in, n_out, k, cb)
+    x = synth.activations(5, rows, rows, n_in)
+    ys = [run(lin, x).cpu().numpy() for _ in range(5)]
+    for i, y in enumerate(ys[1:], 1):
+        assert np.array_equal(ys[0].view(np.uint16), y.view(np.uint16)), i
+    check(ys[0], oracle.forward(x, tr, suh, svh, k, cb, mode=1), TOL_MODE1_REL, TOL_MODE1_ULP,
+          f"{n_in}x{n_out} rows{rows} K{k} cb{cb} repeat")

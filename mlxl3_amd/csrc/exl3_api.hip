@@ -144,10 +144,15 @@ static size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // QMV launch shape.  Workgroups: out/128 column blocks x `splits` K-ranges
 // (global split-K, reduced by the last workgroup of a column block); inside a
 // workgroup KW waves per column pair split the K-range again (LDS reduction).
-// Target: about two workgroups of 4*KW waves per CU, at least 4 and at most
-// 8 Hadamard blocks (512-1024 rows) per K-range (the upper bound keeps xhat
-// of 16 rows in 32 KB of LDS).  EXL3_QMV_SPLITS and
-// EXL3_QMV_KW override (tuning).
+// Target: about 896 workgroups of 4 waves (3.5 per SIMD), with K-ranges of at
+// least 2 Hadamard blocks, at most 8 splits (the last arriver loads every
+// split's partials) and at most 8 blocks per range (xhat of 16 rows in 32 KB
+// of LDS, which outranks the other two).  Measured on MI355X (us, M = 1 / 4,
+// same box): 4096x14336 4 splits 14.10 / 17.68, 8 13.72 / 17.41; 2048x1536
+// 4: 7.57 / 9.98, 8: 6.59 / 8.50, 16: 7.32 / 9.83; 4096x6144 4: 11.41, 8:
+// 9.41, 16: 11.05; 4096x4096 8: 8.63, 16: 9.62; 14336x4096 14: 14.97, 20:
+// 15.28, 28: 16.25; 5120x7168 8: 11.24 / 14.26, 10: 11.35 / 15.56.
+// EXL3_QMV_SPLITS and EXL3_QMV_KW override (tuning).
 static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
   const int nb = in / 128, col_blocks = out / 128;
   const int min_splits = (nb + 7) / 8;
@@ -156,12 +161,9 @@ static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
     int v = atoi(env);
     if (v == 1 || v == 2 || v == 4) kw = v;
   }
-  const int target_wgs = 448;
+  const int target_wgs = 896;
   int s = (target_wgs + col_blocks - 1) / col_blocks;
-  // K-ranges of at least 4 blocks: shorter ones cost more in the split-K
-  // exchange than they add in parallelism (4096x4096: 8 splits 11.7 us, 14
-  // splits 13.9 us)
-  s = std::min(s, std::max(1, nb / 4));
+  s = std::min(s, std::max(1, std::min(8, nb / 2)));
   s = std::max(s, min_splits);
   if (const char* env = getenv("EXL3_QMV_SPLITS")) {  // tuning: any split count that
     int v = atoi(env);                                 // keeps xhat within its LDS bound

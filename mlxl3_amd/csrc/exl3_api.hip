@@ -351,6 +351,21 @@ static Member member_of(const exl3_linear* h, void* y, int cblk0, int x_type) {
   return m;
 }
 
+// SIMDs of the current device (4 per CU), cached per device.
+static int simd_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1024;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cached[dev] = 4 * cus;
+  }
+  return cached[dev];
+}
+
 // One QMV launch (rows <= 16) over the group; `glu` for a (gate, up) pair.
 static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows,
                          void* const* ys, uint32_t* counters, char* scratch, const Glu& glu,
@@ -389,6 +404,8 @@ static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows
   p.M = (int)rows;
   p.x_dtype = x_type;
   p.glu = glu;
+  const int64_t waves = (int64_t)(g.total_out / 128) * p.splits * 4 * kw;
+  p.prio_ramp = waves > simd_count();
   const int nb = g.in / 128;
   int max_blocks = 0;
   for (int s = 0; s < p.splits; ++s)
@@ -400,7 +417,12 @@ static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows
   // the fragment exchange sums a column block's rows (f32, both members of a
   // SwiGLU pair) in the activation buffer's LDS
   if (frag) lds = std::max(lds, sizeof(float) * 128 * (size_t)rows * (glu.on ? 2 : 1));
-  const QmvFn fn = single ? kQmvSingle[g.k - 1][g.cb]
+  static const int shallow_env = [] {  // EXL3_QMV_SHALLOW=0/1 overrides (tuning)
+    const char* env = getenv("EXL3_QMV_SHALLOW");
+    return env ? atoi(env) : -1;
+  }();
+  const bool shallow = shallow_env >= 0 ? shallow_env > 0 : waves >= 3 * (int64_t)simd_count();
+  const QmvFn fn = single ? (shallow ? kQmvSingleShallow : kQmvSingle)[g.k - 1][g.cb]
                    : frag ? kQmvFrag[g.k - 1][g.cb]
                           : kQmv[kwi][g.k - 1][g.cb];
   fn(p, dim3(g.total_out / 128, p.splits), lds, stream);

@@ -41,6 +41,7 @@ struct QmvParams {
   uint32_t* counters;  // [total_out/128] (GLU: [out/128]), zero between calls
   int in, total_out, M, splits;
   int x_dtype;
+  int prio_ramp;  // lower the waves' issue priority with progress (> 1 wave per SIMD)
   Glu glu;
 };
 

@@ -6,6 +6,7 @@ namespace exl3 {
 
 #define EXL3_QMV_INST(K, CB)                                                \
   template __global__ void qmv_kernel<K, CB, 1, false, false>(QmvParams); \
+  template __global__ void qmv_kernel<K, CB, 1, false, false, true>(QmvParams); \
   template __global__ void qmv_kernel<K, CB, 1, true, false>(QmvParams);  \
   template __global__ void qmv_kernel<K, CB, 1, true, true>(QmvParams);   \
   template __global__ void qmv_kernel<K, CB, 2, true, false>(QmvParams);  \
@@ -82,6 +83,10 @@ static void run_qmv1s(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) 
   hipLaunchKernelGGL((qmv_kernel<K, CB, 1, false, false>), grid, dim3(256), lds, s, p);
 }
 template <int K, int CB>
+static void run_qmv1s_shallow(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) {
+  hipLaunchKernelGGL((qmv_kernel<K, CB, 1, false, false, true>), grid, dim3(256), lds, s, p);
+}
+template <int K, int CB>
 static void run_qmv1(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) {
   hipLaunchKernelGGL((qmv_kernel<K, CB, 1, true, false>), grid, dim3(256), lds, s, p);
 }
@@ -126,6 +131,7 @@ void launch_qmv_inner(const uint16_t* values, const uint16_t* x, int rows, int c
 
 const QmvFn kQmv[3][8][3] = {EXL3_TABLE(run_qmv1), EXL3_TABLE(run_qmv2), EXL3_TABLE(run_qmv4)};
 const QmvFn kQmvSingle[8][3] = EXL3_TABLE(run_qmv1s);
+const QmvFn kQmvSingleShallow[8][3] = EXL3_TABLE(run_qmv1s_shallow);
 const QmvFn kQmvFrag[8][3] = EXL3_TABLE(run_qmv1f);
 const DecodeFn kDecode[8][3] = EXL3_TABLE(run_decode);
 

@@ -507,8 +507,11 @@ __device__ __forceinline__ void phase_record(unsigned long long (&ph)[kPhaseWord
 // MULTI = false is the single-row variant of a plain launch (the batch-1
 // decode): no batched prologue or epilogue code, no separate prologue and no
 // SwiGLU edge.  FRAG (multi-row only) exchanges the split-K partials in
-// fragment order instead of row-major.
-template <int K, int CB, int KW, bool MULTI, bool FRAG>
+// fragment order instead of row-major.  SHALLOW keeps one slice per prefetch
+// set: with 3 or more waves per SIMD each wave's step takes that much longer,
+// so shallower prefetch still covers the memory latency (4096x14336 at 3.5
+// waves per SIMD: 13.85 -> 13.64 us; at 1 or 1.75 waves per SIMD it is slower).
+template <int K, int CB, int KW, bool MULTI, bool FRAG, bool SHALLOW = false>
 __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   static_assert(MULTI || !FRAG, "the fragment exchange is a multi-row form");
   extern __shared__ __attribute__((aligned(16))) _Float16 xs[];  // [M][rows of split]
@@ -572,7 +575,7 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   const uint32_t loff = (uint32_t)((((size_t)4 * q_lo * TN + pair * 2 + g * TN + hsel) * 8 * K +
                                     j * K) * 4);
   const uint32_t loff_prev = loff + (uint32_t)((j == 0 ? 8 * K - 1 : -1) * 4);
-  constexpr int D = kQmvLoopDepth<K>;
+  constexpr int D = SHALLOW ? 1 : kQmvLoopDepth<K>;
   uint32_t setA[D][K + 1], setB[D][K + 1];
   const int qlast = nquads > 0 ? nquads - 1 : 0;
   const uint32_t qbytes = (uint32_t)qstride * 4u, last_off = (uint32_t)qlast * qbytes;
@@ -655,7 +658,9 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   const _Float16* xrow = xs + (size_t)am * nrows + 64 * q_lo + g * 16;
   float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   // issue priority falls at the quarters of the K-range (steps t1, t2, t3),
-  // set after each set of D steps
+  // set after each set of D steps, when the launch puts more than one wave on
+  // a SIMD (p.prio_ramp): a lone wave gains nothing from it and loses the
+  // setprio issue slots (4096x4096, one wave per SIMD: 8.54 -> 8.17 us without)
   const int t1 = (nquads + 3) / 4, t2 = (2 * nquads + 3) / 4, t3 = (3 * nquads + 3) / 4;
   auto lower_priority = [&](int done) {
     if (done >= t3) __builtin_amdgcn_s_setprio(0);
@@ -674,7 +679,7 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
         qmv_step_prev<K, CB>(set[d], a0, a1, acc0, acc1);
       }
     }
-    lower_priority(qbase + D);
+    if (p.prio_ramp) lower_priority(qbase + D);
   };
   // Unconditional loads (past-the-end quads re-read the last one) keep the
   // load count static, so the waits before each decode can be partial.

@@ -239,21 +239,24 @@ struct PrologueIn {
   uint32_t x0lo, x0hi, x1lo, x1hi;  // raw 16-bit halves of the two activations
   uint32_t s0, s1;                  // raw suh bits (f16)
 };
-// Raw 16-bit loads only (two per element, the second one covers the high half
-// of an f32; for 16-bit types it re-reads the element): no dtype branch, so
-// the loads stay in flight until prologue_finish consumes them.
+// Raw 16-bit loads only (the high half of an f32 is a second load, issued
+// for f32 activations only, under a uniform branch); the loads stay in flight
+// until prologue_finish consumes them.
 __device__ __forceinline__ PrologueIn prologue_load(const void* x, int x_dtype, size_t off,
                                                     const uint16_t* __restrict__ suh, int e0,
                                                     int lane) {
   const uint16_t* xb = (const uint16_t*)x;
-  const size_t esz = x_dtype == DT_F32 ? 2 : 1;  // u16 words per element
-  const size_t hi = esz - 1;
+  const bool f32 = x_dtype == DT_F32;
+  const size_t esz = f32 ? 2 : 1;  // u16 words per element
   const size_t i0 = (off + lane) * esz, i1 = (off + lane + 64) * esz;
   PrologueIn in;
   in.x0lo = xb[i0];
-  in.x0hi = xb[i0 + hi];
   in.x1lo = xb[i1];
-  in.x1hi = xb[i1 + hi];
+  in.x0hi = in.x1hi = 0u;
+  if (f32) {
+    in.x0hi = xb[i0 + 1];
+    in.x1hi = xb[i1 + 1];
+  }
   in.s0 = suh[e0 + lane];
   in.s1 = suh[e0 + lane + 64];
   return in;
@@ -551,10 +554,13 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   if (!pre) {
 #pragma unroll
     for (int t = 0; t < kPrologueEarly; ++t) {
-      const int job = min(wave + t * 4 * KW, njobs - 1);  // clamped: always a valid job
-      const int m = job / nb, b = job - m * nb;
-      first[t] = prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128, mm.suh,
-                               row0 + b * 128, lane);
+      // a second early job only where the workgroup has one (uniform)
+      if (t == 0 || njobs > 4 * KW) {
+        const int job = min(wave + t * 4 * KW, njobs - 1);  // clamped: always a valid job
+        const int m = job / nb, b = job - m * nb;
+        first[t] = prologue_load(p.x, p.x_dtype, (size_t)m * p.in + row0 + b * 128, mm.suh,
+                                 row0 + b * 128, lane);
+      }
     }
   }
   __builtin_amdgcn_sched_barrier(0);

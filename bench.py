@@ -687,13 +687,12 @@ def configs_leg(steps, warmup, which=("c1", "c2", "c3", "c5"), c2_k=(3, 4, 5),
 
 def _c3_chain(gen, steps, warmup):
     """C3: 32 dense decoder layers at batch 1, K=4 3INST, chained as
-    a=rms(x); q,k,v=W a; h=x+W_o rms(q); b=rms(h); u=swiglu(W_g b, W_u b);
-    x'=h+W_d rms(u) (residual f32; rms = f16(v / sqrt(mean v^2 + 1e-6))), one
-    graph per 32-layer step; also the same 224 linears without the glue.  The
-    gate/up output scales carry 1/sqrt(4096): with unit-scale outputs of std ~85
-    the product g*u would overflow f16."""
-    import ctypes
-
+    a=rms(x); q,k,v=W a; h=x+W_o rms(q); x'=h+mlp(rms(h)) with mlp the fused
+    SwiGLU MLP (Exl3Mlp: gate/up with the SwiGLU edge, then down; residual f32,
+    rms = f16(v / sqrt(mean v^2 + 1e-6)) in torch), one graph per 32-layer step;
+    also the same linears without the glue (frac_hbm_linears_only: the library's
+    share of the step).  The gate/up output scales carry 1/sqrt(4096):
+    with unit-scale outputs of std ~85 the product g*u would overflow f16."""
     import torch
 
     import mlxl3_amd
@@ -704,7 +703,7 @@ def _c3_chain(gen, steps, warmup):
         q, kk, v, o = (_dev_linear(hid, n, 4, 0, gen) for n in (hid, kv, kv, hid))
         g, u = (_dev_linear(hid, inter, 4, 0, gen, out_scale=1 / 64) for _ in range(2))
         d = _dev_linear(inter, hid, 4, 0, gen)
-        layers.append((mlxl3_amd.Exl3Group([q, kk, v]), o, mlxl3_amd.Exl3Group([g, u]), d))
+        layers.append((mlxl3_amd.Exl3Group([q, kk, v]), o, mlxl3_amd.Exl3Mlp(g, u, d)))
     x0 = torch.randn(1, hid, device="cuda", generator=gen)
 
     def rms(v):
@@ -715,22 +714,19 @@ def _c3_chain(gen, steps, warmup):
 
     def chain():
         x = x0.clone()
-        for qkv, o, gu, d in layers:
+        for qkv, o, mlp in layers:
             qq, _, _ = qkv(rms(x))
             h = x + o(rms(qq)).float()
-            gg, uu = gu(rms(h))
-            x = h + d(rms(mlxl3_amd.swiglu(gg, uu))).float()
+            x = h + mlp(rms(h)).float()
         state["y"] = x
 
-    xs = torch.randn(1, inter, device="cuda", generator=gen).half()
-    xh = xs[:, :hid].contiguous()
+    xh = torch.randn(1, hid, device="cuda", generator=gen).half()
 
     def linears_only():
-        for qkv, o, gu, d in layers:
+        for qkv, o, mlp in layers:
             qkv(xh)
             o(xh)
-            gu(xh)
-            d(xs)
+            mlp(xh)
 
     ms = _graph_time(chain, steps, warmup)
     ms_lin = _graph_time(linears_only, steps, warmup)
@@ -743,6 +739,7 @@ def _c3_chain(gen, steps, warmup):
             "ms_linears_only": round(ms_lin, 5), "bytes_per_step": b,
             "gbs": round(b / ms / 1e6, 1), "gbs_linears_only": round(b / ms_lin / 1e6, 1),
             "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4),
+            "frac_hbm_linears_only": round(b / ms_lin / 1e6 / HBM_PEAK_GBS, 4),
             "out_rms": round(float(y.pow(2).mean().sqrt()), 3)}
 
 

@@ -111,7 +111,7 @@ def test_c3_two_chained_layers():
         g, hg = layer(seed, 5, hid, inter, 4, 0, out_scale=1 / 64)
         u, hu = layer(seed, 6, hid, inter, 4, 0, out_scale=1 / 64)
         d, hd = layer(seed, 7, inter, hid, 4, 0)
-        layers.append((mlxl3_amd.Exl3Group([q, kk, v]), o, mlxl3_amd.Exl3Group([g, u]), d))
+        layers.append((mlxl3_amd.Exl3Group([q, kk, v]), o, mlxl3_amd.Exl3Mlp(g, u, d)))
         host.append((hq, ho, hg, hu, hd))
     x0 = synth.activations(3, 0, 1, hid).astype(np.float32)
 
@@ -120,11 +120,10 @@ def test_c3_two_chained_layers():
         return (t / torch.sqrt(t.pow(2).mean(-1, keepdim=True) + 1e-6)).half()
 
     x = torch.from_numpy(x0).cuda()
-    for qkv, o, gu, d in layers:
+    for qkv, o, mlp in layers:
         qq, _, _ = qkv(rms_t(x))
         h = x + o(rms_t(qq)).float()
-        gg, uu = gu(rms_t(h))
-        x = h + d(rms_t(mlxl3_amd.swiglu(gg, uu))).float()
+        x = h + mlp(rms_t(h)).float()
     torch.cuda.synchronize()
     y = x.cpu().numpy()
 
@@ -136,7 +135,7 @@ def test_c3_two_chained_layers():
         qq = lin(rms_np(xr), hq)
         h = xr + lin(rms_np(qq), ho).astype(np.float32)
         b = rms_np(h)
-        xr = h + lin(rms_np(oracle.swiglu(lin(b, hg), lin(b, hu))), hd).astype(np.float32)
+        xr = h + lin(oracle.swiglu(lin(b, hg), lin(b, hu)), hd).astype(np.float32)
     rel = np.linalg.norm(y - xr) / np.linalg.norm(xr)
     mx = np.abs(y - xr).max() / np.sqrt(np.mean(xr ** 2))
     print(f"C3 2-layer chain: rel_l2={rel:.3e} max_abs/rms={mx:.3e}", flush=True)

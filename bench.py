@@ -744,9 +744,10 @@ def _c3_chain(gen, steps, warmup):
 
 
 def _c5_layers(gen, steps, warmup, ks=(2, 4), m_values=(4, 8, 16)):
-    """C5: one 27B-class layer of 7 linears (q/k/v as one group, o, gate/up as
-    one group, down) at M in {4, 8, 16}, K in {2, 4}, MCG, rotating over layer
-    copies."""
+    """C5: one 27B-class layer of 7 linears (q/k/v as one group, o, and the
+    fused SwiGLU MLP: gate/up as one group whose epilogue applies the SwiGLU and
+    the down projection's prologue, then down) at M in {4, 8, 16}, K in {2, 4},
+    MCG, rotating over layer copies."""
     import torch
 
     import mlxl3_amd
@@ -761,17 +762,15 @@ def _c5_layers(gen, steps, warmup, ks=(2, 4), m_values=(4, 8, 16)):
             q, kk, v, o = (_dev_linear(hid, n, k, 1, gen) for n in (hid, kv, kv, hid))
             g, u, d = _dev_linear(hid, inter, k, 1, gen), _dev_linear(hid, inter, k, 1, gen), \
                 _dev_linear(inter, hid, k, 1, gen)
-            layers.append((mlxl3_amd.Exl3Group([q, kk, v]), o, mlxl3_amd.Exl3Group([g, u]), d))
+            layers.append((mlxl3_amd.Exl3Group([q, kk, v]), o, mlxl3_amd.Exl3Mlp(g, u, d)))
         for m in m_values:
             xh = torch.randn(m, hid, device="cuda", generator=gen).half()
-            xi = torch.randn(m, inter, device="cuda", generator=gen).half()
 
             def step():
-                for qkv, o, gu, d in layers:
+                for qkv, o, mlp in layers:
                     qkv(xh)
                     o(xh)
-                    gu(xh)
-                    d(xi)
+                    mlp(xh)
 
             reps = max(1, math.ceil(steps / copies))
             ms = _graph_time(step, reps, max(1, warmup)) / copies

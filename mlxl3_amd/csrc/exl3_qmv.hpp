@@ -163,6 +163,27 @@ __device__ __forceinline__ void qmv_step_prev(const uint32_t (&B)[K + 1], half8 
   acc1 = mfma16(a1, b11, acc1);
 }
 
+// qmv_step_prev in two halves: the decode of a step's 4 B fragments, and
+// their 4 MFMAs (in the same order).
+template <int K, int CB>
+__device__ __forceinline__ void decode_step(const uint32_t (&B)[K + 1], half8 (&b)[4]) {
+  uint32_t src[32];
+  extract_states<K>(B, src);
+  b[0] = decode_fragment<CB, K, 0, 0>(src);
+  b[1] = decode_fragment<CB, K, 0, 1>(src);
+  b[2] = decode_fragment<CB, K, 1, 0>(src);
+  b[3] = decode_fragment<CB, K, 1, 1>(src);
+  mfma_operand_fence(b[0], b[1]);
+  mfma_operand_fence(b[2], b[3]);
+}
+__device__ __forceinline__ void mma_step(half8 a0, half8 a1, const half8 (&b)[4], float4v& acc0,
+                                         float4v& acc1) {
+  acc0 = mfma16(a0, b[0], acc0);
+  acc1 = mfma16(a0, b[1], acc1);
+  acc0 = mfma16(a1, b[2], acc0);
+  acc1 = mfma16(a1, b[3], acc1);
+}
+
 // Epilogue for one row of a 128-column block held as (v0, v1) = columns
 // (lane, lane+64): f16(sum) -> staged H128 -> f16(*1/sqrt128) -> f16(*svh)
 // (finish_vals128), then cast (+bias) and store (finish_row128).
@@ -513,7 +534,8 @@ __device__ __forceinline__ void phase_record(unsigned long long (&ph)[kPhaseWord
 // fragment order instead of row-major.  SHALLOW keeps one slice per prefetch
 // set: with 3 or more waves per SIMD each wave's step takes that much longer,
 // so shallower prefetch still covers the memory latency (4096x14336 at 3.5
-// waves per SIMD: 13.85 -> 13.64 us; at 1 or 1.75 waves per SIMD it is slower).
+// waves per SIMD: 13.85 -> 13.64 us; at 1 or 1.75 waves per SIMD it is slower),
+// and decodes its first step before the prologue's barrier (PEEL).
 template <int K, int CB, int KW, bool MULTI, bool FRAG, bool SHALLOW = false>
 __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   static_assert(MULTI || !FRAG, "the fragment exchange is a multi-row form");
@@ -592,8 +614,24 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
     else
       load_slice_prev_b<K>(wrsrc, 0, loff + o, loff_prev + o, set);
   };
+  // Single-row at 3+ waves per SIMD: the first set's B fragments are decoded
+  // before the barrier that publishes xhat (the decode needs no activations),
+  // with the second set's loads already out: issued here, before the
+  // prologue's Hadamards, where K's states need a window each (16 % K != 0:
+  // one load per word and a costlier decode), after them otherwise.  Same-box
+  // A/B at 4096x14336 M=1 (us), before -> after them / here: K=2 13.22 ->
+  // 13.03 / 13.06, K=3 15.26 -> 15.18 / 14.69, K=4 13.35 -> 13.06 / 13.28,
+  // K=5 24.30 -> 24.28 / 23.28, K=6 26.83 -> 26.82 / 25.50, K=8 22.03 ->
+  // 22.02 / 22.13; bit-identical.  With D = 2 (one wave per SIMD, 4096x4096)
+  // the early decode cost 2 % (8.44 -> 8.61 us), so it stays off there.
+  constexpr bool PEEL = !MULTI && SHALLOW;
+  constexpr bool kEarlySecond = PEEL && 16 % K != 0;
 #pragma unroll
   for (int d = 0; d < D; ++d) fetch_slice(setA[d], d);
+  if constexpr (kEarlySecond) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) fetch_slice(setB[d], D + d);
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // prologue into LDS
@@ -652,6 +690,15 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
       xs[m * nrows + b * 128 + lane + 64] = (_Float16)v1;
     }
   }
+  half8 first_b[PEEL ? D : 1][4];  // the first set's fragments (PEEL)
+  if constexpr (PEEL) {
+    if constexpr (!kEarlySecond) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) fetch_slice(setB[d], D + d);
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) decode_step<K, CB>(setA[d], first_b[d]);
+  }
   __syncthreads();
   EXL3_PHASE(ph[1] = __builtin_amdgcn_s_memrealtime(); ph[4] = __builtin_amdgcn_s_memtime();)
 
@@ -694,6 +741,17 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
     for (int d = 0; d < D; ++d) fetch_slice(set[d], qbase + d);
   };
   int q0 = 0;
+  if constexpr (PEEL) {  // the first set was decoded before the barrier; setB is in flight
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (d < nquads)
+        mma_step(*(const half8*)(xrow + d * 64), *(const half8*)(xrow + d * 64 + 8), first_b[d],
+                 acc0, acc1);
+    if (p.prio_ramp) lower_priority(D);
+    fetch(setA, 2 * D);
+    compute(setB, D, false);
+    q0 = 2 * D;
+  }
   for (; q0 + 2 * D <= nquads; q0 += 2 * D) {
     fetch(setB, q0 + D);
     compute(setA, q0, true);

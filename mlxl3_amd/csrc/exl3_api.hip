@@ -421,10 +421,20 @@ static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows
     const char* env = getenv("EXL3_QMV_SHALLOW");
     return env ? atoi(env) : -1;
   }();
-  const bool shallow = shallow_env >= 0 ? shallow_env > 0 : waves >= 3 * (int64_t)simd_count();
+  // One slice per prefetch set (and the first step decoded under the
+  // prologue) from 3 waves per SIMD; multi-row launches only with K-ranges of
+  // up to 4 blocks (same box, us, two-deep -> shallow: 4096x14336 M=2/4/8/16
+  // 15.28/17.11/19.47/20.71 -> 15.09/16.90/18.74/20.45, 4096x28672 M=4 26.27
+  // -> 25.51, 2048x12288 M=4 11.32 -> 11.21; 8-block ranges lose: 5120x27648
+  // M=4 31.98 -> 32.43, 5120x55296 M=4 49.28 -> 49.74, 27648x5120 M=4 36.04 ->
+  // 36.69, while one row gains there too: 5120x27648 25.95 -> 25.72).
+  const bool shallow =
+      shallow_env >= 0 ? shallow_env > 0
+                       : waves >= 3 * (int64_t)simd_count() && (single || max_blocks <= 4);
   const QmvFn fn = single ? (shallow ? kQmvSingleShallow : kQmvSingle)[g.k - 1][g.cb]
-                   : frag ? kQmvFrag[g.k - 1][g.cb]
-                          : kQmv[kwi][g.k - 1][g.cb];
+                   : frag ? (shallow ? kQmvFragShallow : kQmvFrag)[g.k - 1][g.cb]
+                   : kw == 1 && shallow ? kQmvShallow[g.k - 1][g.cb]
+                                        : kQmv[kwi][g.k - 1][g.cb];
   fn(p, dim3(g.total_out / 128, p.splits), lds, stream);
   return check_launch("EXL3 QMV launch");
 }

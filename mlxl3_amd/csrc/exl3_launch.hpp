@@ -26,6 +26,8 @@ extern const QmvFn kQmv[3][8][3];  // [log2 KW]: 1, 2 or 4 K-parts per column pa
 extern const QmvFn kQmvSingle[8][3];  // one row, one K-part per column pair
 extern const QmvFn kQmvSingleShallow[8][3];  // the same with one slice per prefetch set
 extern const QmvFn kQmvFrag[8][3];    // one K-part per column pair, fragment-order partials
+extern const QmvFn kQmvShallow[8][3];      // kQmv[0] with one slice per prefetch set
+extern const QmvFn kQmvFragShallow[8][3];  // kQmvFrag with one slice per prefetch set
 extern const DecodeFn kDecode[8][3];
 extern const QmmFn kQmm[3][8][3];  // [log2 MB]: 64, 128 or 256 rows per workgroup
 

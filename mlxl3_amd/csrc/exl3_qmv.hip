@@ -9,6 +9,8 @@ namespace exl3 {
   template __global__ void qmv_kernel<K, CB, 1, false, false, true>(QmvParams); \
   template __global__ void qmv_kernel<K, CB, 1, true, false>(QmvParams);  \
   template __global__ void qmv_kernel<K, CB, 1, true, true>(QmvParams);   \
+  template __global__ void qmv_kernel<K, CB, 1, true, false, true>(QmvParams); \
+  template __global__ void qmv_kernel<K, CB, 1, true, true, true>(QmvParams); \
   template __global__ void qmv_kernel<K, CB, 2, true, false>(QmvParams);  \
   template __global__ void qmv_kernel<K, CB, 4, true, false>(QmvParams);
 #define EXL3_DEC_INST(K, CB)                                                             \
@@ -95,6 +97,14 @@ static void run_qmv1f(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) 
   hipLaunchKernelGGL((qmv_kernel<K, CB, 1, true, true>), grid, dim3(256), lds, s, p);
 }
 template <int K, int CB>
+static void run_qmv1_shallow(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) {
+  hipLaunchKernelGGL((qmv_kernel<K, CB, 1, true, false, true>), grid, dim3(256), lds, s, p);
+}
+template <int K, int CB>
+static void run_qmv1f_shallow(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) {
+  hipLaunchKernelGGL((qmv_kernel<K, CB, 1, true, true, true>), grid, dim3(256), lds, s, p);
+}
+template <int K, int CB>
 static void run_qmv2(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) {
   hipLaunchKernelGGL((qmv_kernel<K, CB, 2, true, false>), grid, dim3(512), lds, s, p);
 }
@@ -133,6 +143,8 @@ const QmvFn kQmv[3][8][3] = {EXL3_TABLE(run_qmv1), EXL3_TABLE(run_qmv2), EXL3_TA
 const QmvFn kQmvSingle[8][3] = EXL3_TABLE(run_qmv1s);
 const QmvFn kQmvSingleShallow[8][3] = EXL3_TABLE(run_qmv1s_shallow);
 const QmvFn kQmvFrag[8][3] = EXL3_TABLE(run_qmv1f);
+const QmvFn kQmvShallow[8][3] = EXL3_TABLE(run_qmv1_shallow);
+const QmvFn kQmvFragShallow[8][3] = EXL3_TABLE(run_qmv1f_shallow);
 const DecodeFn kDecode[8][3] = EXL3_TABLE(run_decode);
 
 #endif

@@ -531,11 +531,12 @@ __device__ __forceinline__ void phase_record(unsigned long long (&ph)[kPhaseWord
 // MULTI = false is the single-row variant of a plain launch (the batch-1
 // decode): no batched prologue or epilogue code, no separate prologue and no
 // SwiGLU edge.  FRAG (multi-row only) exchanges the split-K partials in
-// fragment order instead of row-major.  SHALLOW keeps one slice per prefetch
-// set: with 3 or more waves per SIMD each wave's step takes that much longer,
-// so shallower prefetch still covers the memory latency (4096x14336 at 3.5
-// waves per SIMD: 13.85 -> 13.64 us; at 1 or 1.75 waves per SIMD it is slower),
-// and decodes its first step before the prologue's barrier (PEEL).
+// fragment order instead of row-major.  SHALLOW (KW = 1; chosen by the host
+// from 3 waves per SIMD) keeps one slice per prefetch set: each wave's step
+// then takes that much longer, so shallower prefetch still covers the memory
+// latency (4096x14336 at 3.5 waves per SIMD: 13.85 -> 13.64 us; at 1 or 1.75
+// waves per SIMD it is slower), and decodes its first step before the
+// prologue's barrier (PEEL).
 template <int K, int CB, int KW, bool MULTI, bool FRAG, bool SHALLOW = false>
 __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   static_assert(MULTI || !FRAG, "the fragment exchange is a multi-row form");
@@ -614,7 +615,7 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
     else
       load_slice_prev_b<K>(wrsrc, 0, loff + o, loff_prev + o, set);
   };
-  // Single-row at 3+ waves per SIMD: the first set's B fragments are decoded
+  // SHALLOW launches (3+ waves per SIMD): the first set's B fragments are decoded
   // before the barrier that publishes xhat (the decode needs no activations),
   // with the second set's loads already out: issued here, before the
   // prologue's Hadamards, where K's states need a window each (16 % K != 0:
@@ -624,7 +625,7 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   // K=5 24.30 -> 24.28 / 23.28, K=6 26.83 -> 26.82 / 25.50, K=8 22.03 ->
   // 22.02 / 22.13; bit-identical.  With D = 2 (one wave per SIMD, 4096x4096)
   // the early decode cost 2 % (8.44 -> 8.61 us), so it stays off there.
-  constexpr bool PEEL = !MULTI && SHALLOW;
+  constexpr bool PEEL = SHALLOW;
   constexpr bool kEarlySecond = PEEL && 16 % K != 0;
 #pragma unroll
   for (int d = 0; d < D; ++d) fetch_slice(setA[d], d);

@@ -152,11 +152,21 @@ static size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // 4: 7.57 / 9.98, 8: 6.59 / 8.50, 16: 7.32 / 9.83; 4096x6144 4: 11.41, 8:
 // 9.41, 16: 11.05; 4096x4096 8: 8.63, 16: 9.62; 14336x4096 14: 14.97, 20:
 // 15.28, 28: 16.25; 5120x7168 8: 11.24 / 14.26, 10: 11.35 / 15.56.
+// Launches that would hold at most 1.25 waves per SIMD take 2 K-parts per
+// column pair instead (two waves per pair meet in LDS: the same splits, twice
+// the waves).  Same box, us, KW 1 -> 2 (M = 1 / 2 / 4 / 16): 4096x4096 (1024
+// waves) 8.42 / 10.04 / 11.32 / 15.35 -> 8.21 / 9.64 / 10.16 / 14.27;
+// 4096x1792 8.12 / 9.77 / 11.20 / 14.73 -> 7.89 / 9.32 / 9.98 / 13.53;
+// 5120x5120 (1280) 10.45 / 12.58 / 13.58 / 17.8 -> 10.26 / 11.98 / 13.47 /
+// 16.9; 2048x1536 6.50 -> 6.51; above the bound it loses at M = 1: 4096x6144
+// (1536) 9.32 -> 9.62, 4096x10240 11.25 -> 12.43, 2048x12288 9.24 -> 9.56
+// (but 5120x7168, 1792 waves, 11.43 -> 11.18).
 // EXL3_QMV_SPLITS and EXL3_QMV_KW override (tuning).
+static int simd_count();
 static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
   const int nb = in / 128, col_blocks = out / 128;
   const int min_splits = (nb + 7) / 8;
-  int kw = 1;
+  int kw = 0;
   if (const char* env = getenv("EXL3_QMV_KW")) {
     int v = atoi(env);
     if (v == 1 || v == 2 || v == 4) kw = v;
@@ -170,6 +180,7 @@ static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
     if (v >= 1) s = std::max(v, min_splits);
   }
   s = std::max(1, std::min(s, nb));
+  if (kw == 0) kw = (int64_t)col_blocks * s * 4 * 4 <= (int64_t)simd_count() * 5 ? 2 : 1;
   *splits_out = s;
   *kw_out = kw;
 }
@@ -431,7 +442,10 @@ static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows
   const bool shallow =
       shallow_env >= 0 ? shallow_env > 0
                        : waves >= 3 * (int64_t)simd_count() && (single || max_blocks <= 4);
-  const QmvFn fn = single ? (shallow ? kQmvSingleShallow : kQmvSingle)[g.k - 1][g.cb]
+  // one row, 2 K-parts per pair: the single-row kernel in its shallow form
+  const bool single2 = rows == 1 && kw == 2 && !glu.on && !p.mem[0].xhat;
+  const QmvFn fn = single2 ? kQmvSingle2[g.k - 1][g.cb]
+                   : single ? (shallow ? kQmvSingleShallow : kQmvSingle)[g.k - 1][g.cb]
                    : frag ? (shallow ? kQmvFragShallow : kQmvFrag)[g.k - 1][g.cb]
                    : kw == 1 && shallow ? kQmvShallow[g.k - 1][g.cb]
                                         : kQmv[kwi][g.k - 1][g.cb];

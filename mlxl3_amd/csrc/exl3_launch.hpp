@@ -25,6 +25,7 @@ constexpr size_t kWorkspaceCounterBytes = 65536;
 extern const QmvFn kQmv[3][8][3];  // [log2 KW]: 1, 2 or 4 K-parts per column pair
 extern const QmvFn kQmvSingle[8][3];  // one row, one K-part per column pair
 extern const QmvFn kQmvSingleShallow[8][3];  // the same with one slice per prefetch set
+extern const QmvFn kQmvSingle2[8][3];  // one row, 2 K-parts per pair, shallow
 extern const QmvFn kQmvFrag[8][3];    // one K-part per column pair, fragment-order partials
 extern const QmvFn kQmvShallow[8][3];      // kQmv[0] with one slice per prefetch set
 extern const QmvFn kQmvFragShallow[8][3];  // kQmvFrag with one slice per prefetch set

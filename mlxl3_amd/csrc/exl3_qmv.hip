@@ -7,6 +7,7 @@ namespace exl3 {
 #define EXL3_QMV_INST(K, CB)                                                \
   template __global__ void qmv_kernel<K, CB, 1, false, false>(QmvParams); \
   template __global__ void qmv_kernel<K, CB, 1, false, false, true>(QmvParams); \
+  template __global__ void qmv_kernel<K, CB, 2, false, false, true>(QmvParams); \
   template __global__ void qmv_kernel<K, CB, 1, true, false>(QmvParams);  \
   template __global__ void qmv_kernel<K, CB, 1, true, true>(QmvParams);   \
   template __global__ void qmv_kernel<K, CB, 1, true, false, true>(QmvParams); \
@@ -89,6 +90,10 @@ static void run_qmv1s_shallow(const QmvParams& p, dim3 grid, size_t lds, hipStre
   hipLaunchKernelGGL((qmv_kernel<K, CB, 1, false, false, true>), grid, dim3(256), lds, s, p);
 }
 template <int K, int CB>
+static void run_qmv2s_shallow(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) {
+  hipLaunchKernelGGL((qmv_kernel<K, CB, 2, false, false, true>), grid, dim3(512), lds, s, p);
+}
+template <int K, int CB>
 static void run_qmv1(const QmvParams& p, dim3 grid, size_t lds, hipStream_t s) {
   hipLaunchKernelGGL((qmv_kernel<K, CB, 1, true, false>), grid, dim3(256), lds, s, p);
 }
@@ -142,6 +147,7 @@ void launch_qmv_inner(const uint16_t* values, const uint16_t* x, int rows, int c
 const QmvFn kQmv[3][8][3] = {EXL3_TABLE(run_qmv1), EXL3_TABLE(run_qmv2), EXL3_TABLE(run_qmv4)};
 const QmvFn kQmvSingle[8][3] = EXL3_TABLE(run_qmv1s);
 const QmvFn kQmvSingleShallow[8][3] = EXL3_TABLE(run_qmv1s_shallow);
+const QmvFn kQmvSingle2[8][3] = EXL3_TABLE(run_qmv2s_shallow);
 const QmvFn kQmvFrag[8][3] = EXL3_TABLE(run_qmv1f);
 const QmvFn kQmvShallow[8][3] = EXL3_TABLE(run_qmv1_shallow);
 const QmvFn kQmvFragShallow[8][3] = EXL3_TABLE(run_qmv1f_shallow);

@@ -84,8 +84,8 @@ def run(n_in: int, n_out: int, k: int, cb: int, reps: int, seed: int) -> None:
         for lin in lins:
             lin.forward(x, workspace=ws)
     # one record per wave of the largest single-row grid (col blocks x in/128
-    # splits, 4 waves per workgroup)
-    slots = (n_out // 128) * (n_in // 128) * 4
+    # splits, up to 8 waves per workgroup)
+    slots = (n_out // 128) * (n_in // 128) * 8
     buf = torch.zeros(slots * WORDS, dtype=torch.int64, device=dev)
     for _ in range(20):  # steady state (clocks, caches) before anything is read
         graph.replay()

@@ -558,21 +558,42 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
   }
   if (p.splits > 1) {
     // the last part to arrive: every fragment summed over the parts in split
-    // order (coherent 16-byte loads, all 8 waves, 4*MB fragments each), its
-    // four rows rounded to f16 into the tile's rows in LDS
+    // order (coherent 16-byte loads, all 8 waves, 4*MB fragments each, the
+    // loads of kSumFrags fragments x kSumParts parts in flight together: one
+    // round trip to the coherence point per group, not per load), its four
+    // rows rounded to f16 into the tile's rows in LDS
+    constexpr int kSumFrags = 4, kSumParts = 4;
     const int col = 16 * (n >> 3) + (n & 7);
-    for (int i = 0; i < 4 * MB; ++i) {
-      const int slot = wave * 4 * MB + i;  // (consumer, mb, f)
-      const int cr = slot / (8 * MB), mb = (slot / 8) % MB, f = slot % 8;
-      float4v sum = {0.f, 0.f, 0.f, 0.f};
-      for (int sp = 0; sp < p.splits; ++sp)
-        sum += __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(
-                                               qmm_slab(p, sp, tile, MB), slot * 1024 + lane * 16,
-                                               0, kCpolSc1));
-      uint16_t* y = ys + (cr * 16 * MB + 16 * mb + 4 * g) * kYStride + 32 * (f >> 1) +
-                    8 * (f & 1) + col;
+    for (int i0 = 0; i0 < 4 * MB; i0 += kSumFrags) {
+      float4v sum[kSumFrags];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) y[r * kYStride] = f2h(sum[r]);
+      for (int i = 0; i < kSumFrags; ++i) sum[i] = float4v{0.f, 0.f, 0.f, 0.f};
+      for (int s0 = 0; s0 < p.splits; s0 += kSumParts) {
+        u32x4 t[kSumParts][kSumFrags];
+#pragma unroll
+        for (int c = 0; c < kSumParts; ++c) {
+          // clamped: always a written part (the extra loads are not added)
+          const __amdgpu_buffer_rsrc_t src = qmm_slab(p, min(s0 + c, p.splits - 1), tile, MB);
+#pragma unroll
+          for (int i = 0; i < kSumFrags; ++i)
+            t[c][i] = __builtin_amdgcn_raw_buffer_load_b128(
+                src, (wave * 4 * MB + i0 + i) * 1024 + lane * 16, 0, kCpolSc1);
+        }
+#pragma unroll
+        for (int c = 0; c < kSumParts; ++c)
+          if (s0 + c < p.splits)
+#pragma unroll
+            for (int i = 0; i < kSumFrags; ++i) sum[i] += __builtin_bit_cast(float4v, t[c][i]);
+      }
+#pragma unroll
+      for (int i = 0; i < kSumFrags; ++i) {
+        const int slot = wave * 4 * MB + i0 + i;  // (consumer, mb, f)
+        const int cr = slot / (8 * MB), mb = (slot / 8) % MB, f = slot % 8;
+        uint16_t* y = ys + (cr * 16 * MB + 16 * mb + 4 * g) * kYStride + 32 * (f >> 1) +
+                      8 * (f & 1) + col;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r * kYStride] = f2h(sum[i][r]);
+      }
     }
   }
   __syncthreads();

@@ -191,12 +191,16 @@ static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
 // fitted on MI355X with every CU busy: MB=1 660 ns, MB=2 750 ns, MB=4 1250 ns
 // (per 64 input rows); a split adds its f32 partials (64*MB rows x 128 columns
 // per tile, padded), written and read back through 16-byte coherent accesses
-// at ~1.0 ns per KB.  Splits are only used while the output tiles alone fill
+// at ~0.7 ns per KB.  Splits are only used while the output tiles alone fill
 // at most 256 workgroups, so at most 256 tile counters are ever needed.
 // Fitted to a sweep of MB {1,2,4} x splits {1,2,3,4,6,8} over 4096x14336 M
 // {128, 512}, 14336x4096 M {128, 256, 512, 2048}, 27648x5120 and 5120x27648
-// at M=128 and 4096x4096 at M=512: the chosen shape is the fastest measured at
-// every point but 14336x4096 M=128 (55 us against 51 for MB=1, 4 splits).
+// at M=128 and 4096x4096 at M=512; the partials' price refitted (1.0 -> 0.7 ns
+// per KB) after the last arriver's loads went out 16 at a time, when a second
+// sweep (14336x4096 M {128, 256, 512}, 27648x5120, 4096x14336 and 5120x27648
+// at M=128, 4096x4096 at M=512) found the chosen shape fastest everywhere but
+// 14336x4096 M=512 (MB=2, 2 splits 99.5 us against 93.7 for MB=4, 4 splits),
+// which every price from 0.5 to 0.8 picks.
 // EXL3_QMM_MB and EXL3_QMM_SPLITS override.
 static constexpr int kTileCounters = 256;
 
@@ -225,7 +229,7 @@ static QmmShape choose_qmm_shape(int in, int out, int64_t rows) {
       if (s > 1 && base > kTileCounters) s = 1;
       const int64_t rounds = (base * s + 255) / 256;
       double cost = (double)rounds * ((nq + s - 1) / s) * step_ns;
-      if (s > 1) cost += 1.0 / 1024 * 4.0 * (double)s * mt * 64 * mb * out;
+      if (s > 1) cost += 0.7 / 1024 * 4.0 * (double)s * mt * 64 * mb * out;
       if (cost < best_cost) {
         best_cost = cost;
         best = QmmShape{mb, (int)mt, s};

@@ -944,9 +944,19 @@ __global__ __launch_bounds__(256) void moe_dec_down_kernel(MoeDecParams dp) {
   __builtin_amdgcn_s_waitcnt(0);  // the stores are acknowledged before the arrival
   uint32_t* rcounter =
       dp.counters + (size_t)p.slots_pad * p.col_blocks + (size_t)row * p.col_blocks + cblk;
+  // the token's expert ids (and below its slots' values) are loaded a chunk
+  // of kTopChunk slots at a time, not one dependent round trip per slot
+  constexpr int kTopChunk = 8;
   int valid = 0;
-  for (int t = 0; t < dp.top_k; ++t)
-    valid += dp.selected[(size_t)row * dp.top_k + t] < (uint32_t)p.experts ? 1 : 0;
+  for (int t0 = 0; t0 < dp.top_k; t0 += kTopChunk) {
+    uint32_t ids[kTopChunk];
+#pragma unroll
+    for (int c = 0; c < kTopChunk; ++c)
+      ids[c] = dp.selected[(size_t)row * dp.top_k + min(t0 + c, dp.top_k - 1)];
+#pragma unroll
+    for (int c = 0; c < kTopChunk; ++c)
+      valid += t0 + c < dp.top_k && ids[c] < (uint32_t)p.experts ? 1 : 0;
+  }
   uint32_t old = 0;
   if (lane == 0) {
     old = __hip_atomic_fetch_add(rcounter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -956,13 +966,25 @@ __global__ __launch_bounds__(256) void moe_dec_down_kernel(MoeDecParams dp) {
   if (__builtin_amdgcn_readfirstlane(old) != (uint32_t)(valid - 1)) return;
   // y = sum over the token's valid slots in top-k order (moe_reduce_kernel's
   // order and f32 adds), stored as f16 or f32
+  // (the rows of slots outside the bank were never written: loaded, not added)
   float y0 = 0.f, y1 = 0.f;
-  for (int t = 0; t < dp.top_k; ++t) {
-    const size_t ts = (size_t)row * dp.top_k + t;
-    if (dp.selected[ts] >= (uint32_t)p.experts) continue;
-    const float* zr = dp.zf + ts * p.width + cblk * 128;
-    y0 += load_coherent(zr + lane);
-    y1 += load_coherent(zr + lane + 64);
+  for (int t0 = 0; t0 < dp.top_k; t0 += kTopChunk) {
+    uint32_t ids[kTopChunk];
+    float a[kTopChunk], b[kTopChunk];
+#pragma unroll
+    for (int c = 0; c < kTopChunk; ++c) {
+      const size_t ts = (size_t)row * dp.top_k + min(t0 + c, dp.top_k - 1);
+      ids[c] = dp.selected[ts];
+      const float* zr = dp.zf + ts * p.width + cblk * 128;
+      a[c] = load_coherent(zr + lane);
+      b[c] = load_coherent(zr + lane + 64);
+    }
+#pragma unroll
+    for (int c = 0; c < kTopChunk; ++c)
+      if (t0 + c < dp.top_k && ids[c] < (uint32_t)p.experts) {
+        y0 += a[c];
+        y1 += b[c];
+      }
   }
   const size_t o = (size_t)row * p.width + cblk * 128 + lane;
   store_reduced(dp.y, p.scores_dtype, o, y0);

@@ -43,6 +43,19 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(std::make_integer_sequence<int, N>{}, f);
 }
 
+// acc + v where `live`, else acc, as a select.  Sums over a chunk of values
+// loaded together (split-K partials, top-k slots) add them with this: behind a
+// conditional add the compiler sinks each load into its branch, and the chunk's
+// loads then go out one round trip at a time.
+__device__ __forceinline__ float add_if(bool live, float acc, float v) {
+  const float s = acc + v;
+  return live ? s : acc;
+}
+__device__ __forceinline__ float4v add_if(bool live, float4v acc, float4v v) {
+  const float4v s = acc + v;
+  return live ? s : acc;
+}
+
 // ---------------------------------------------------------------------------
 // f16 helpers
 // ---------------------------------------------------------------------------

@@ -69,9 +69,18 @@ __device__ __forceinline__ void moe_plan_block(const MoePlanParams& p) {
   for (int i = tid; i < p.ncounters; i += NT) p.counters[i] = 0u;
   for (int e = tid; e < p.experts; e += NT) cnt[e] = 0;
   __syncthreads();
-  for (int s = tid; s < p.slots; s += NT) {
-    const uint32_t e = p.selected[s];
-    p.rank[s] = e < (uint32_t)p.experts ? atomicAdd(&cnt[e], 1) : -1;
+  // each thread's expert ids are loaded kPlanBatch at a time (clamped: always
+  // a valid slot), not one dependent round trip per slot
+  constexpr int kPlanBatch = 8;
+  for (int s0 = tid; s0 < p.slots; s0 += kPlanBatch * NT) {
+    uint32_t e[kPlanBatch];
+#pragma unroll
+    for (int u = 0; u < kPlanBatch; ++u) e[u] = p.selected[min(s0 + u * NT, p.slots - 1)];
+#pragma unroll
+    for (int u = 0; u < kPlanBatch; ++u) {
+      const int s = s0 + u * NT;
+      if (s < p.slots) p.rank[s] = e[u] < (uint32_t)p.experts ? atomicAdd(&cnt[e[u]], 1) : -1;
+    }
   }
   __syncthreads();
   // exclusive scans of the counts and block counts: each thread sums a run of
@@ -108,9 +117,20 @@ __device__ __forceinline__ void moe_plan_block(const MoePlanParams& p) {
     p.counts[1] = rc;
   }
   __syncthreads();
-  for (int s = tid; s < p.slots; s += NT) {
-    const int r = p.rank[s];
-    if (r >= 0) p.sorted_slot[off[p.selected[s]] + r] = s;
+  for (int s0 = tid; s0 < p.slots; s0 += kPlanBatch * NT) {
+    int r[kPlanBatch];
+    uint32_t e[kPlanBatch];
+#pragma unroll
+    for (int u = 0; u < kPlanBatch; ++u) {
+      const int s = min(s0 + u * NT, p.slots - 1);
+      r[u] = p.rank[s];
+      e[u] = p.selected[s];
+    }
+#pragma unroll
+    for (int u = 0; u < kPlanBatch; ++u) {
+      const int s = s0 + u * NT;
+      if (s < p.slots && r[u] >= 0) p.sorted_slot[off[e[u]] + r[u]] = s;
+    }
   }
   for (int e = tid; e < p.experts; e += NT) {
     p.expert_count[e] = cnt[e];
@@ -545,12 +565,11 @@ __attribute__((amdgpu_waves_per_eu(MB == 4 ? 2 : CB == 2 ? 3 : 4))) void moe_mm_
       }
 #pragma unroll
       for (int c = 0; c < kChunk; ++c)
-        if (s0 + c < p.splits)
 #pragma unroll
-          for (int pj = 0; pj < NPROJ; ++pj) {
-            v[pj][0] += t[c][pj][0];
-            v[pj][1] += t[c][pj][1];
-          }
+        for (int pj = 0; pj < NPROJ; ++pj) {
+          v[pj][0] = add_if(s0 + c < p.splits, v[pj][0], t[c][pj][0]);
+          v[pj][1] = add_if(s0 + c < p.splits, v[pj][1], t[c][pj][1]);
+        }
     }
     moe_finish_row<GLU>(p, e, pos0 + m, cblk, v[0][0], v[0][1], v[NPROJ - 1][0],
                         v[NPROJ - 1][1], lane);
@@ -652,9 +671,8 @@ __global__ __launch_bounds__(256) void moe_reduce_kernel(const void* __restrict_
     }
 #pragma unroll
     for (int c = 0; c < 8; ++c)
-      if (ok[c])
 #pragma unroll
-        for (int k = 0; k < 8; ++k) acc[k] += v[c][k];
+      for (int k = 0; k < 8; ++k) acc[k] = add_if(ok[c], acc[k], v[c][k]);
   }
   const size_t o = (size_t)row * width + i;
   if (!VEC) {
@@ -821,12 +839,11 @@ __global__ __launch_bounds__(512) void moe_dec_gu_kernel(MoeDecParams dp) {
     }
 #pragma unroll
     for (int c = 0; c < kChunk; ++c)
-      if (s0 + c < p.splits)
 #pragma unroll
-        for (int pj = 0; pj < 2; ++pj) {
-          v[pj][0] += t[c][pj][0];
-          v[pj][1] += t[c][pj][1];
-        }
+      for (int pj = 0; pj < 2; ++pj) {
+        v[pj][0] = add_if(s0 + c < p.splits, v[pj][0], t[c][pj][0]);
+        v[pj][1] = add_if(s0 + c < p.splits, v[pj][1], t[c][pj][1]);
+      }
   }
   moe_finish_row<true>(p, e, slot, cblk, v[0][0], v[0][1], v[1][0], v[1][1], lane);
 }
@@ -925,11 +942,10 @@ __global__ __launch_bounds__(256) void moe_dec_down_kernel(MoeDecParams dp) {
         b[c] = load_coherent(src + lane + 64);
       }
 #pragma unroll
-      for (int c = 0; c < kSplitChunk; ++c)
-        if (c0 + c < p.splits) {
-          v0 += a[c];
-          v1 += b[c];
-        }
+      for (int c = 0; c < kSplitChunk; ++c) {
+        v0 = add_if(c0 + c < p.splits, v0, a[c]);
+        v1 = add_if(c0 + c < p.splits, v1, b[c]);
+      }
     }
     s0v = v0;
     s1v = v1;
@@ -980,11 +996,11 @@ __global__ __launch_bounds__(256) void moe_dec_down_kernel(MoeDecParams dp) {
       b[c] = load_coherent(zr + lane + 64);
     }
 #pragma unroll
-    for (int c = 0; c < kTopChunk; ++c)
-      if (t0 + c < dp.top_k && ids[c] < (uint32_t)p.experts) {
-        y0 += a[c];
-        y1 += b[c];
-      }
+    for (int c = 0; c < kTopChunk; ++c) {
+      const bool live = t0 + c < dp.top_k && ids[c] < (uint32_t)p.experts;
+      y0 = add_if(live, y0, a[c]);
+      y1 = add_if(live, y1, b[c]);
+    }
   }
   const size_t o = (size_t)row * p.width + cblk * 128 + lane;
   store_reduced(dp.y, p.scores_dtype, o, y0);

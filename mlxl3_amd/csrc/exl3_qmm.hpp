@@ -581,9 +581,9 @@ __global__ __launch_bounds__(512) void qmm_kernel(QmmParams p) {
         }
 #pragma unroll
         for (int c = 0; c < kSumParts; ++c)
-          if (s0 + c < p.splits)
 #pragma unroll
-            for (int i = 0; i < kSumFrags; ++i) sum[i] += __builtin_bit_cast(float4v, t[c][i]);
+          for (int i = 0; i < kSumFrags; ++i)
+            sum[i] = add_if(s0 + c < p.splits, sum[i], __builtin_bit_cast(float4v, t[c][i]));
       }
 #pragma unroll
       for (int i = 0; i < kSumFrags; ++i) {

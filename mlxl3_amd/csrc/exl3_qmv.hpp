@@ -637,11 +637,40 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
 
   // prologue into LDS
   if (pre) {
-    const int chunks = nrows >> 3;  // 16-byte chunks per row
-    for (int i = threadIdx.x; i < M * chunks; i += 256 * KW) {
-      const int m = i / chunks, c = i - m * chunks;
-      *(u32x4*)(xs + m * nrows + c * 8) =
-          *(const u32x4*)(mm.xhat + (size_t)m * p.in + row0 + c * 8);
+    const int chunks = nrows >> 3, total = M * chunks;  // 16-byte chunks per row
+    if constexpr (FRAG) {
+      // 8+ rows: kCopyBatch of a thread's chunks in flight together, as buffer
+      // loads (the compiler re-rolls plain ones into one load per iteration),
+      // clamped to a valid chunk and stored only where real.  Not in the
+      // row-major kernels: the same code there cost 4 % at M = 4 (5120x5120
+      // 13.16 -> 13.72 us) although that path never runs at those rows.
+      constexpr int kCopyBatch = 4;
+      const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(mm.xhat + row0), 0, (int)min((size_t)M * p.in * 2, (size_t)0x7fffffff),
+          kBufferRsrcWord3);
+      for (int i0 = threadIdx.x; i0 < total; i0 += kCopyBatch * 256 * KW) {
+        u32x4 v[kCopyBatch];
+#pragma unroll
+        for (int u = 0; u < kCopyBatch; ++u) {
+          const int i = min(i0 + u * 256 * KW, total - 1);
+          const int m = i / chunks, c = i - m * chunks;
+          v[u] = __builtin_amdgcn_raw_buffer_load_b128(xr, (uint32_t)(m * p.in + c * 8) * 2u, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < kCopyBatch; ++u) {
+          const int i = i0 + u * 256 * KW;
+          if (i < total) {
+            const int m = i / chunks, c = i - m * chunks;
+            *(u32x4*)(xs + m * nrows + c * 8) = v[u];
+          }
+        }
+      }
+    } else {
+      for (int i = threadIdx.x; i < total; i += 256 * KW) {
+        const int m = i / chunks, c = i - m * chunks;
+        *(u32x4*)(xs + m * nrows + c * 8) =
+            *(const u32x4*)(mm.xhat + (size_t)m * p.in + row0 + c * 8);
+      }
     }
   }
 #pragma unroll
@@ -946,7 +975,7 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
   } else {
     // Multi-row: the split sums in fragment space -- pair wave w (K-part 0)
     // loads its two accumulators of every split (16-byte coherent loads, up to
-    // kSplitChunk splits in flight) and adds them in split order -- then the
+    // kSplitChunk / 2 splits in flight) and adds them in split order -- then the
     // block's rows through LDS to the row-wise finishing.  The rows (M per
     // member, f32) take the activation buffer's place: every wave is past
     // the K loop (the barrier above).
@@ -954,10 +983,13 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
     auto gather_block = [&](int gcb, float(*dst)[128]) {
       if (writer) {
         float4v s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-        for (int c0 = 0; c0 < p.splits; c0 += kSplitChunk) {
-          float4v a[kSplitChunk], b[kSplitChunk];
+        // kFragChunk splits' two fragments in flight (16 bytes each: 8 splits
+        // would hold 64 more registers and cost the kernel a wave per SIMD)
+        constexpr int kFragChunk = kSplitChunk / 2;
+        for (int c0 = 0; c0 < p.splits; c0 += kFragChunk) {
+          float4v a[kFragChunk], b[kFragChunk];
 #pragma unroll
-          for (int i = 0; i < kSplitChunk; ++i) {
+          for (int i = 0; i < kFragChunk; ++i) {
             const __amdgpu_buffer_rsrc_t src = frag_slab(min(c0 + i, p.splits - 1), gcb);
             a[i] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(
                                                    src, ((pair * 2) * 64 + lane) * 16, 0, kCpolSc1));
@@ -966,11 +998,10 @@ __global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
                                                    kCpolSc1));
           }
 #pragma unroll
-          for (int i = 0; i < kSplitChunk; ++i)
-            if (c0 + i < p.splits) {
-              s0 += a[i];
-              s1 += b[i];
-            }
+          for (int i = 0; i < kFragChunk; ++i) {
+            s0 = add_if(c0 + i < p.splits, s0, a[i]);
+            s1 = add_if(c0 + i < p.splits, s1, b[i]);
+          }
         }
         const int c = 16 * (pair * 2 + (n >> 3)) + (n & 7);
 #pragma unroll

@@ -536,9 +536,15 @@ __device__ __forceinline__ void phase_record(unsigned long long (&ph)[kPhaseWord
 // then takes that much longer, so shallower prefetch still covers the memory
 // latency (4096x14336 at 3.5 waves per SIMD: 13.85 -> 13.64 us; at 1 or 1.75
 // waves per SIMD it is slower), and decodes its first step before the
-// prologue's barrier (PEEL).
+// prologue's barrier (PEEL).  The row-major multi-row kernel (MULTI, !FRAG)
+// asks for 5 waves per SIMD: left alone its epilogue took it to 104 registers
+// and 4 waves, which launches of more than 4 waves per SIMD felt (27648x5120
+// M=4, 4320 waves: 36.2 -> 32.5 us; C5 layer M=4 K2/K4 117.1/124.7 ->
+// 111.8/116.6 us; 90 registers, no scratch).
 template <int K, int CB, int KW, bool MULTI, bool FRAG, bool SHALLOW = false>
-__global__ __launch_bounds__(256 * KW) void qmv_kernel(QmvParams p) {
+__global__ __launch_bounds__(256 * KW)
+__attribute__((amdgpu_waves_per_eu(MULTI && !FRAG && KW == 1 ? 5 : 1))) void qmv_kernel(
+    QmvParams p) {
   static_assert(MULTI || !FRAG, "the fragment exchange is a multi-row form");
   extern __shared__ __attribute__((aligned(16))) _Float16 xs[];  // [M][rows of split]
   __shared__ int s_last;

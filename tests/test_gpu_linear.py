@@ -243,11 +243,14 @@ def test_north_star_shape_qmv():
     check(y, oracle.forward(x, tr, suh, svh, 4, 0, mode=0), TOL_MODE0_REL, TOL_MODE0_ULP, "NS mode0")
 
 
-@pytest.mark.parametrize("rows", [8, 16])
+@pytest.mark.parametrize("rows", [2, 4, 8, 16])
 def test_north_star_shape_multirow_separate_prologue(rows):
-    """4096 x 14336 at M = 8, 16: rows x blocks per K-range >= 64, so xhat comes
-    from the separate prologue launch.  Every row must equal the same row run
-    alone (fused prologue, M = 1) bit for bit, and the batch the oracle."""
+    """4096 x 14336 at M = 2, 4 (row-major exchange, fused prologue) and 8, 16
+    (fragment exchange; xhat from the separate prologue launch): all of them
+    launches of 3.5 waves per SIMD, so the one-slice prefetch kernels with the
+    first step decoded under the prologue.  Every row must equal the same row
+    run alone (the single-row kernel, M = 1) bit for bit, and the batch the
+    oracle."""
     torch = torch_mod()
     lin, (tr, suh, svh, _) = make_layer(2, 4096, 14336, 4, 0)
     x = synth.activations(7, rows, rows, 4096)

@@ -274,6 +274,49 @@ __device__ __forceinline__ void moe_down_values(const MoeMmParams& p, int e, int
   v1 = weighted(round_f16(v1 * h2f(sv[lane + 64])), sc, p.scores_dtype);
 }
 
+// Stores one reduced output value: f16 for f16 scores, f32 otherwise (the
+// dtype MLX's promotion gives the weighted sum).
+__device__ __forceinline__ void store_reduced(void* y, int scores_dtype, size_t i, float v) {
+  if (scores_dtype == DT_F16)
+    ((uint16_t*)y)[i] = f2h(v);
+  else
+    ((float*)y)[i] = v;
+}
+
+// The token `row`'s output columns (lane, lane + 64) of 128-column block
+// `cblk`: the sum over its valid slots in top-k order of their weighted values
+// (f32 z rows, f32 adds, as moe_reduce_kernel), stored as f16 or f32; the
+// slots' ids and values load kTopChunk slots at a time (rows of slots outside
+// the bank are loaded, never added).
+__device__ __forceinline__ void moe_token_sum(const MoeMmParams& p, const uint32_t* selected,
+                                              int top_k,
+                                              const float* zf, void* y, int row, int cblk,
+                                              int lane) {
+  constexpr int kTopChunk = 8;
+  float y0 = 0.f, y1 = 0.f;
+  for (int t0 = 0; t0 < top_k; t0 += kTopChunk) {
+    uint32_t ids[kTopChunk];
+    float a[kTopChunk], b[kTopChunk];
+#pragma unroll
+    for (int c = 0; c < kTopChunk; ++c) {
+      const size_t ts = (size_t)row * top_k + min(t0 + c, top_k - 1);
+      ids[c] = selected[ts];
+      const float* zr = zf + ts * p.width + cblk * 128;
+      a[c] = load_coherent(zr + lane);
+      b[c] = load_coherent(zr + lane + 64);
+    }
+#pragma unroll
+    for (int c = 0; c < kTopChunk; ++c) {
+      const bool live = t0 + c < top_k && ids[c] < (uint32_t)p.experts;
+      y0 = add_if(live, y0, a[c]);
+      y1 = add_if(live, y1, b[c]);
+    }
+  }
+  const size_t o = (size_t)row * p.width + cblk * 128 + lane;
+  store_reduced(y, p.scores_dtype, o, y0);
+  store_reduced(y, p.scores_dtype, o + 64, y1);
+}
+
 // Epilogue of one routed row of a 128-column block: (g0, g1) and (u0, u1) are
 // the f32 sums of columns (lane, lane+64) of the first and last projection.
 template <bool GLU>
@@ -595,15 +638,6 @@ __global__ __launch_bounds__(64) void swiglu_down_input_kernel(MoeMmParams p,
                        gate_up[off + p.width + lane], gate_up[off + p.width + lane + 64], lane);
 }
 
-// Stores one reduced output value: f16 for f16 scores, f32 otherwise (the
-// dtype MLX's promotion gives the weighted sum).
-__device__ __forceinline__ void store_reduced(void* y, int scores_dtype, size_t i, float v) {
-  if (scores_dtype == DT_F16)
-    ((uint16_t*)y)[i] = f2h(v);
-  else
-    ((float*)y)[i] = v;
-}
-
 // finish_and_reduce (moe.rs:586-609) as an op: y[row] = sum_t of
 // weighted(f16(H(f16(raw)) * svh), score) over slots row*top_k + t in t order
 // (f32 adds), rounded to f16 for f16 scores; H the staged Hadamard with
@@ -860,7 +894,22 @@ __global__ __launch_bounds__(256) void moe_dec_down_kernel(MoeDecParams dp) {
   const int slot = blockIdx.x / per_slot, rem = blockIdx.x - slot * per_slot;
   const int cblk = rem / p.splits, split = rem - cblk * p.splits;
   const uint32_t eu = dp.selected[slot];
-  if (eu >= (uint32_t)p.experts) return;  // uniform
+  if (eu >= (uint32_t)p.experts) {  // uniform: the slot adds nothing
+    // ... and when none of its token's slots is in the bank, the token's first
+    // slot (split 0) writes the zeros no top-k sum will
+    const int row = slot / dp.top_k;
+    if (slot == row * dp.top_k && split == 0 && wave == 0) {
+      bool any = false;
+      for (int t = 0; t < dp.top_k; ++t)
+        any = any || dp.selected[(size_t)row * dp.top_k + t] < (uint32_t)p.experts;
+      if (!any) {
+        const size_t o = (size_t)row * p.width + cblk * 128 + lane;
+        store_reduced(dp.y, p.scores_dtype, o, 0.f);
+        store_reduced(dp.y, p.scores_dtype, o + 64, 0.f);
+      }
+    }
+    return;
+  }
   const int e = (int)eu, row = slot / dp.top_k;
   const int nq_all = p.k_in >> 6;
   const int qa = split * nq_all / p.splits, nq = (split + 1) * nq_all / p.splits - qa;
@@ -982,29 +1031,7 @@ __global__ __launch_bounds__(256) void moe_dec_down_kernel(MoeDecParams dp) {
   if (__builtin_amdgcn_readfirstlane(old) != (uint32_t)(valid - 1)) return;
   // y = sum over the token's valid slots in top-k order (moe_reduce_kernel's
   // order and f32 adds), stored as f16 or f32
-  // (the rows of slots outside the bank were never written: loaded, not added)
-  float y0 = 0.f, y1 = 0.f;
-  for (int t0 = 0; t0 < dp.top_k; t0 += kTopChunk) {
-    uint32_t ids[kTopChunk];
-    float a[kTopChunk], b[kTopChunk];
-#pragma unroll
-    for (int c = 0; c < kTopChunk; ++c) {
-      const size_t ts = (size_t)row * dp.top_k + min(t0 + c, dp.top_k - 1);
-      ids[c] = dp.selected[ts];
-      const float* zr = dp.zf + ts * p.width + cblk * 128;
-      a[c] = load_coherent(zr + lane);
-      b[c] = load_coherent(zr + lane + 64);
-    }
-#pragma unroll
-    for (int c = 0; c < kTopChunk; ++c) {
-      const bool live = t0 + c < dp.top_k && ids[c] < (uint32_t)p.experts;
-      y0 = add_if(live, y0, a[c]);
-      y1 = add_if(live, y1, b[c]);
-    }
-  }
-  const size_t o = (size_t)row * p.width + cblk * 128 + lane;
-  store_reduced(dp.y, p.scores_dtype, o, y0);
-  store_reduced(dp.y, p.scores_dtype, o + 64, y1);
+  moe_token_sum(p, dp.selected, dp.top_k, dp.zf, dp.y, row, cblk, lane);
 }
 
 }  // namespace exl3

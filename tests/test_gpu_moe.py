@@ -181,6 +181,42 @@ def test_moe_small_path_invalid_expert_ids():
     check(y, ref, "moe small path, ids outside the bank")
 
 
+@pytest.mark.parametrize("grouped", [False, True])
+def test_moe_token_without_slots_in_bank(grouped, monkeypatch):
+    """A token none of whose top-k slots is in the bank gets a zero row (no
+    top-k sum writes it; the route plan or the token's first slot does): the
+    output buffer starts as NaN and must come back 0 in that row and match the
+    oracle in the others, on the small-row and the grouped path."""
+    import mlxl3_amd
+
+    torch = torch_mod()
+    if grouped:
+        monkeypatch.setenv("EXL3_MOE_GROUPED", "1")
+    layer, x, sel, sc = case(512, 256, 16, 4, 3, 3, 95)
+    sel = sel.copy()
+    sel[1, :] = 16  # every slot of token 1 outside the bank
+    moe = make_moe(layer, 4, 3, 0)
+    xd, sd, scd = dev(x), dev(sel).to(torch.int32).contiguous(), dev(sc)
+    y = torch.full((3, 512), float("nan"), dtype=mlxl3_amd.scores_result_dtype(scd.dtype),
+                   device="cuda")
+    lib = mlxl3_amd.load_library()
+    ws = torch.zeros(int(lib.exl3_moe_workspace_bytes(moe._handle, 3)), dtype=torch.uint8,
+                     device="cuda")
+    rc = lib.exl3_moe_forward(moe._handle, mlxl3_amd._ptr(xd), mlxl3_amd._dtype_code(xd.dtype), 3,
+                              mlxl3_amd._ptr(sd), mlxl3_amd._ptr(scd),
+                              mlxl3_amd._dtype_code(scd.dtype), mlxl3_amd._ptr(y),
+                              mlxl3_amd._ptr(ws), ws.numel(), mlxl3_amd._stream_ptr(xd.device))
+    torch.cuda.synchronize()
+    assert rc == 0
+    got = y.float().cpu().numpy()
+    assert (got[1] == 0).all(), got[1][:8]
+    keep = sel < 16
+    ref = oracle.moe_forward(x, np.where(keep, sel, 0).astype(np.uint32),
+                             np.where(keep, sc, 0).astype(sc.dtype), *layer, 3, 0)
+    check(got[[0, 2]].astype(ref.dtype), ref[[0, 2]],
+          f"moe {'grouped' if grouped else 'small'} path, a token without slots in the bank")
+
+
 def _bf16_bits(v):
     b = np.asarray(v, np.float32).view(np.uint32).astype(np.uint64)
     return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)

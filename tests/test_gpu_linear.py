@@ -351,3 +351,29 @@ def test_repeat_calls_bit_identical(n_in, n_out, rows, k, cb):
         assert np.array_equal(ys[0].view(np.uint16), y.view(np.uint16)), i
     check(ys[0], oracle.forward(x, tr, suh, svh, k, cb, mode=1), TOL_MODE1_REL, TOL_MODE1_ULP,
           f"{n_in}x{n_out} rows{rows} K{k} cb{cb} repeat")
+
+
+@pytest.mark.parametrize("n_in,n_out,rows", [
+    (4096, 14336, 1), (4096, 14336, 4), (4096, 14336, 16), (14336, 4096, 1),
+    (4096, 4096, 2), (14336, 4096, 512),
+])
+def test_split_exchange_alternating_inputs(n_in, n_out, rows):
+    """The split-K exchange (partials through coherent stores, an arrival
+    counter, the last arriver's coherent loads) relies on acknowledged stores
+    being visible before the counter increment.  A partial read before its
+    store landed would be the previous call's, so calls alternate between two
+    inputs on one workspace (the previous call's partials always differ): 60
+    calls, each bit-identical to its input's first result.  Shapes: the
+    single-row, row-major, fragment-order and QMM (4 K-splits) exchanges."""
+    torch = torch_mod()
+    lin, _ = make_layer(4100 + rows, n_in, n_out, 4, 0)
+    xs = [torch.from_numpy(synth.activations(60 + i, rows, rows, n_in)).cuda() for i in range(2)]
+    ws = torch.zeros(lin.workspace_bytes(rows), dtype=torch.uint8, device="cuda")
+    want = [lin.forward(x, workspace=ws).clone() for x in xs]
+    torch.cuda.synchronize()
+    assert not torch.equal(want[0], want[1])
+    outs = [lin.forward(xs[i % 2], workspace=ws) for i in range(60)]
+    torch.cuda.synchronize()
+    for i, y in enumerate(outs):
+        assert torch.equal(y.view(torch.int16), want[i % 2].view(torch.int16)), i
+

@@ -423,3 +423,29 @@ def test_glue_codec_ops():
     assert np.mean(got == want.view(np.uint16).ravel()) >= 0.99
     assert rows[1]["data"] == u16(oracle.finish_and_reduce(raw, svh, sc))
     assert rows[2]["data"] == [0] * 128
+
+
+@pytest.mark.parametrize("rows", [1, 4, 64])
+def test_moe_exchanges_alternating_inputs(rows, monkeypatch):
+    """The MoE split-K and top-k exchanges (small-row path at 1 and 4 tokens,
+    grouped path with 2 K-splits pinned at 64) on one workspace, calls
+    alternating between two inputs and routings: 30 calls, each bit-identical
+    to its input's first result (a partial or slot value read before its store
+    landed would be the other call's)."""
+    torch = torch_mod()
+    layer, x0, sel0, sc0 = case(512, 256, 16, 4, rows, 3, 97)
+    _, x1, sel1, sc1 = case(512, 256, 16, 4, rows, 3, 98)
+    if rows == 64:  # read at create: both grouped expert QMMs with 2 K-splits
+        monkeypatch.setenv("EXL3_MOE_SPLITS", "2")
+    moe = make_moe(layer, 4, 3, 0)
+    ins = [(dev(x0), dev(sel0).to(torch.int32), dev(sc0)),
+           (dev(x1), dev(sel1).to(torch.int32), dev(sc1))]
+    want = [moe.forward(*a).clone() for a in ins]
+    torch.cuda.synchronize()
+    assert not torch.equal(want[0], want[1])
+    outs = [moe.forward(*ins[i % 2]) for i in range(30)]
+    torch.cuda.synchronize()
+    as_int = torch.int16 if want[0].element_size() == 2 else torch.int32
+    for i, y in enumerate(outs):
+        assert torch.equal(y.view(as_int), want[i % 2].view(as_int)), i
+

@@ -382,9 +382,10 @@ static int simd_count() {
 }
 
 // One QMV launch (rows <= 16) over the group; `glu` for a (gate, up) pair.
+// `given_xhat`: the single member's xhat, already computed (no prologue here).
 static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows,
                          void* const* ys, uint32_t* counters, char* scratch, const Glu& glu,
-                         hipStream_t stream) {
+                         hipStream_t stream, const uint16_t* given_xhat = nullptr) {
   if (int rc = launch_gate("EXL3 QMV launch")) return rc;
   QmvParams p{};
   int cblk0 = 0;
@@ -394,7 +395,9 @@ static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows
   }
   int kw;
   group_qmv_shape(g, &p.splits, &kw);
-  if (qmv_separate_prologue(g, rows, p.splits)) {
+  if (given_xhat) {
+    p.mem[0].xhat = given_xhat;
+  } else if (qmv_separate_prologue(g, rows, p.splits)) {
     const size_t xbytes = align_up(sizeof(uint16_t) * (size_t)rows * g.in);
     PrologueParams pp{};
     pp.x = x;
@@ -584,10 +587,19 @@ static int mlp_forward(const exl3_linear* gate, const exl3_linear* up, const exl
     Glu glu{};
     glu.on = 1;
     glu.out = act;
+    // Where the down projection would run its prologue as a launch of its
+    // own, the gate/up epilogue applies it to each finished 128-block instead
+    // (f16(a * suh), the staged H128, f16(* 1/sqrt(128))) and down reads that
+    // xhat: one launch fewer per MLP.
+    int dsplits, dkw;
+    group_qmv_shape(d, &dsplits, &dkw);
+    const bool down_xhat = qmv_separate_prologue(d, rows, dsplits);
+    if (down_xhat) glu.down_suh = down->suh;
     void* gu_y[2] = {nullptr, nullptr};  // not written: the edge consumes the partials
     if (int rc = run_group_qmv(g, x, EXL3_F16, rows, gu_y, counters, base + act_bytes, glu, stream))
       return rc;
-    return run_group_qmv(d, act, EXL3_F16, rows, dy, counters, base + act_bytes, Glu{}, stream);
+    return run_group_qmv(d, act, EXL3_F16, rows, dy, counters, base + act_bytes, Glu{}, stream,
+                         down_xhat ? act : nullptr);
   }
   void* gu_y[2] = {base + act_bytes, base + 2 * act_bytes};
   char* scratch = base + 3 * act_bytes;

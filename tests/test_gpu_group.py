@@ -8,7 +8,9 @@ the GPU, through the C ABI.
 * exl3_swiglu (Array::swiglu, native/ffi/mlx_bridge.cpp:745-749) against the
   oracle's f16-staged restatement: bit-exact for every finite f16 gate value;
 * exl3_mlp_forward (qwen35.rs:303-307; rows <= 16: SwiGLU in the gate/up QMV
-  epilogue; rows > 16: one SwiGLU + down-prologue kernel between the QMMs)
+  epilogue, which also applies the down projection's prologue where down would
+  otherwise launch it separately; rows > 16: one SwiGLU + down-prologue kernel
+  between the QMMs)
   against the unfused composition
   exl3_group_forward -> exl3_swiglu -> exl3_linear_forward: bit-exact; and
   against the oracle composition (oracle.mlp_forward) within the linear's
@@ -154,12 +156,17 @@ def test_mlp_fused_equals_unfused_and_oracle(k, cb, rows):
         check_tol(y.cpu().numpy(), oracle.mlp_forward(x_np, *host), f"mlp k={k} cb={cb} rows={rows}")
 
 
-def test_mlp_separate_prologue_rows():
-    """4096 -> 8192 -> 4096 at M = 16: the gate/up QMV and the down QMV both
-    take xhat from the separate prologue launch; fused == unfused bit-exact."""
+@pytest.mark.parametrize("hidden, rows", [(8192, 16), (20480, 4)])
+def test_mlp_separate_prologue_rows(hidden, rows):
+    """4096 -> hidden -> 4096 where the down projection would take its xhat
+    from a prologue launch of its own (16 rows x 4-block K-ranges; 4 rows x 160
+    blocks x 32 column blocks = 20 480 repeated jobs): the fused MLP's gate/up
+    epilogue writes down's xhat instead, and the unfused path runs the
+    prologue launch; fused == unfused bit-exact."""
     torch = torch_mod()
-    mlp, parts, _ = mlp_case(4096, 8192, 4, 0, seed=9)
-    x = torch.from_numpy(synth.activations(3, 16, 16, 4096)).cuda()
+    print(f"mlp separate prologue hidden={hidden} rows={rows}", flush=True)
+    mlp, parts, _ = mlp_case(4096, hidden, 4, 0, seed=9)
+    x = torch.from_numpy(synth.activations(3, rows, rows, 4096)).cuda()
     y = mlp.forward(x)
     y_ref = unfused(parts, x)
     torch.cuda.synchronize()

@@ -396,6 +396,7 @@ static int run_group_qmv(const Group& g, const void* x, int x_type, int64_t rows
   int kw;
   group_qmv_shape(g, &p.splits, &kw);
   if (given_xhat) {
+    if (g.count != 1) return fail(EXL3_EINVAL, "a precomputed xhat serves one projection");
     p.mem[0].xhat = given_xhat;
   } else if (qmv_separate_prologue(g, rows, p.splits)) {
     const size_t xbytes = align_up(sizeof(uint16_t) * (size_t)rows * g.in);

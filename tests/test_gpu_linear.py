@@ -263,6 +263,41 @@ def test_north_star_shape_multirow_separate_prologue(rows):
     del torch
 
 
+@pytest.mark.parametrize("n_in, n_out", [(4096, 14336), (14336, 4096)])
+@pytest.mark.parametrize("k", range(1, 9))
+@pytest.mark.parametrize("cb", [0, 1, 2])
+def test_full_shape_every_k_and_codebook(n_in, n_out, k, cb):
+    """Both NS-sized shapes for every K x codebook at 1, 4 and 16 rows
+    (single-row, row-major and fragment-order exchanges; 16 rows take xhat
+    from the prologue launch).  4096 x 14336 puts 3.5 waves on a SIMD, so it
+    runs the one-slice prefetch kernels with the first step decoded under the
+    prologue (for 16 % K != 0 the second set's loads issued before it);
+    14336 x 4096 (1.75 waves) the two-slice ones.  Basis rows bit-exact
+    against the oracle, random rows within the stated tolerance, and rows of
+    a batch equal to the same rows run alone."""
+    import mlxl3_amd
+
+    torch = torch_mod()
+    print(f"full shape {n_in}x{n_out} k={k} cb={cb}", flush=True)
+    tr, _, svh, _ = synth.linear_layer(11000 + 10 * k + cb, 10, n_in, n_out, k)
+    suh = np.ones(n_in, np.float16)
+    dev = lambda a: torch.from_numpy(a.view(np.int16) if a.dtype == np.uint16 else a).cuda()
+    lin = mlxl3_amd.Exl3Linear(dev(tr), dev(suh), dev(svh), None, k, cb)
+    for rows in (1, 4, 16):
+        x, _ = basis_inputs(rows, n_in, 100 * k + 10 * cb + rows)
+        y = run(lin, x).cpu().numpy()
+        ref = oracle.forward(x, tr, suh, svh, k, cb, mode=1)
+        assert np.array_equal(y.view(np.uint16), ref.view(np.uint16)), \
+            (k, cb, rows, float(np.mean(y == ref)))
+        xr = synth.activations(12, 10 * k + cb, rows, n_in)
+        yr = run(lin, xr).cpu().numpy()
+        check(yr, oracle.forward(xr, tr, suh, svh, k, cb, mode=1), TOL_MODE1_REL, TOL_MODE1_ULP,
+              f"{n_in}x{n_out} k{k} cb{cb} M={rows}")
+        for r in ((0, rows - 1) if rows > 1 else ()):
+            y1 = run(lin, xr[r:r + 1]).cpu().numpy()
+            assert np.array_equal(yr[r:r + 1].view(np.uint16), y1.view(np.uint16)), (k, cb, rows, r)
+
+
 def test_qmm_rows_independent_of_batch():
     lin, _ = make_layer(5000, 512, 384, 4, 0)
     x = synth.activations(7, 0, 300, 512)

@@ -110,11 +110,15 @@ def ulp_of(v, bf16):
     return float(np.spacing(np.float16(v))) * (8.0 if bf16 else 1.0)
 
 
-@pytest.mark.parametrize("rows", [1, 2, 17, 512])
+@pytest.mark.parametrize("rows, n_in", [(1, 512), (2, 512), (5, 512), (16, 512), (16, 4096),
+                                         (17, 512), (512, 512)])
 @pytest.mark.parametrize("dtype_name", ["bfloat16", "float32"])
 @pytest.mark.parametrize("bias", [False, True])
-def test_activation_dtypes_and_bias_vs_oracle(rows, dtype_name, bias):
-    """bf16 / f32 activations through the QMV (rows 1, 2) and the QMM (17, 512):
+def test_activation_dtypes_and_bias_vs_oracle(rows, n_in, dtype_name, bias):
+    """bf16 / f32 activations through the QMV (rows 1, 2, 5: single-row and
+    row-major exchange; 16: fragment-order exchange, with the prologue inside
+    the workgroup at 512 inputs and as its own launch at 4096) and the QMM (17,
+    512):
     the output dtype follows linear.rs:992-995 under MLX promotion (bf16 + f16
     bias -> f32), values vs the oracle at rel-L2 <= 1e-3 and max-abs <= 2 ulp
     at max|y| of the last format the value was rounded to (bf16 for bf16
@@ -122,9 +126,9 @@ def test_activation_dtypes_and_bias_vs_oracle(rows, dtype_name, bias):
     inner result can move the bf16 cast by one bf16 ulp; f16 otherwise)."""
     torch = torch_mod()
     dtype = getattr(torch, dtype_name)
-    print(f"dtypes rows={rows} {dtype_name} bias={bias}", flush=True)
-    lin, (tr, suh, svh, b) = make_layer(3000 + rows, 512, 384, 3, 1, bias=bias)
-    x32 = synth.activations(5, rows, rows, 512).astype(np.float32) * np.float32(1.37)
+    print(f"dtypes rows={rows} in={n_in} {dtype_name} bias={bias}", flush=True)
+    lin, (tr, suh, svh, b) = make_layer(3000 + rows + n_in, n_in, 384, 3, 1, bias=bias)
+    x32 = synth.activations(5, rows, rows, n_in).astype(np.float32) * np.float32(1.37)
     xt = torch.from_numpy(x32).to(dtype)
     y = lin.forward(xt.cuda())
     torch.cuda.synchronize()

@@ -156,16 +156,18 @@ def test_mlp_fused_equals_unfused_and_oracle(k, cb, rows):
         check_tol(y.cpu().numpy(), oracle.mlp_forward(x_np, *host), f"mlp k={k} cb={cb} rows={rows}")
 
 
-@pytest.mark.parametrize("hidden, rows", [(8192, 16), (20480, 4)])
-def test_mlp_separate_prologue_rows(hidden, rows):
+@pytest.mark.parametrize("hidden, rows, k, cb", [(8192, 16, 4, 0), (20480, 4, 4, 0),
+                                                 (8192, 16, 3, 2), (8192, 16, 2, 1),
+                                                 (20480, 4, 5, 1)])
+def test_mlp_separate_prologue_rows(hidden, rows, k, cb):
     """4096 -> hidden -> 4096 where the down projection would take its xhat
     from a prologue launch of its own (16 rows x 4-block K-ranges; 4 rows x 160
     blocks x 32 column blocks = 20 480 repeated jobs): the fused MLP's gate/up
     epilogue writes down's xhat instead, and the unfused path runs the
     prologue launch; fused == unfused bit-exact."""
     torch = torch_mod()
-    print(f"mlp separate prologue hidden={hidden} rows={rows}", flush=True)
-    mlp, parts, _ = mlp_case(4096, hidden, 4, 0, seed=9)
+    print(f"mlp separate prologue hidden={hidden} rows={rows} k={k} cb={cb}", flush=True)
+    mlp, parts, _ = mlp_case(4096, hidden, k, cb, seed=9)
     x = torch.from_numpy(synth.activations(3, rows, rows, 4096)).cuda()
     y = mlp.forward(x)
     y_ref = unfused(parts, x)

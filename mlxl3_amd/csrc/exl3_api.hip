@@ -145,9 +145,20 @@ static size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // (global split-K, reduced by the last workgroup of a column block); inside a
 // workgroup KW waves per column pair split the K-range again (LDS reduction).
 // Target: about 896 workgroups of 4 waves (3.5 per SIMD), with K-ranges of at
-// least 2 Hadamard blocks, at most 8 splits (the last arriver loads every
-// split's partials) and at most 8 blocks per range (xhat of 16 rows in 32 KB
-// of LDS, which outranks the other two).  Measured on MI355X (us, M = 1 / 4,
+// least 2 Hadamard blocks and at most 8 splits (the last arriver loads every
+// split's partials).  Long inputs need more splits: a range holds at most 12
+// blocks (xhat of 16 rows in 48 KB of LDS).  Where the target would leave more
+// than 8 blocks per range, the split count between those two bounds is the one
+// that puts the fewest blocks on the busiest CU (workgroups per CU, rounded
+// up, x blocks per range; ties to fewer splits): the workgroups of a launch
+// spread one per CU in turn, so a count whose last turn fills only part of the
+// CUs leaves those CUs one range more.  27648x5120 (40 column blocks, 216
+// blocks): 27 splits (5 workgroups of 8 blocks on some CUs) -> 18 (3 of 12),
+// same box, us, M = 1 / 4 / 8 / 16: 26.3 / 32.6 / 33.1 / 40.5 -> 25.7 / 29.9 /
+// 31.2 / 33.5 (24 splits, 4 of 9: 25.0 / 30.7 / 31.7 / 34.1); the 5120 ->
+// 2 x 27648 group 5 -> 4 splits, M = 4, 46.9 -> 45.5; 14336x4096 keeps 14
+// (12: 16.5 / 20.7 / 23.6 against 14.9 / 20.0 / 22.6 at M = 1 / 4 / 16).
+// Measured on MI355X (us, M = 1 / 4,
 // same box): 4096x14336 4 splits 14.10 / 17.68, 8 13.72 / 17.41; 2048x1536
 // 4: 7.57 / 9.98, 8: 6.59 / 8.50, 16: 7.32 / 9.83; 4096x6144 4: 11.41, 8:
 // 9.41, 16: 11.05; 4096x4096 8: 8.63, 16: 9.62; 14336x4096 14: 14.97, 20:
@@ -165,7 +176,7 @@ static size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 static int simd_count();
 static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
   const int nb = in / 128, col_blocks = out / 128;
-  const int min_splits = (nb + 7) / 8;
+  const int min_splits = (nb + 11) / 12, even_splits = (nb + 7) / 8;
   int kw = 0;
   if (const char* env = getenv("EXL3_QMV_KW")) {
     int v = atoi(env);
@@ -174,7 +185,20 @@ static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
   const int target_wgs = 896;
   int s = (target_wgs + col_blocks - 1) / col_blocks;
   s = std::min(s, std::max(1, std::min(8, nb / 2)));
-  s = std::max(s, min_splits);
+  if (s < even_splits) {
+    const int64_t cus = std::max(1, simd_count() / 4);
+    int best = even_splits;
+    int64_t best_cost = INT64_MAX;
+    for (int c = std::max(s, min_splits); c <= even_splits; ++c) {
+      const int64_t per_cu = ((int64_t)col_blocks * c + cus - 1) / cus;
+      const int64_t cost = per_cu * ((nb + c - 1) / c);
+      if (cost < best_cost) {
+        best_cost = cost;
+        best = c;
+      }
+    }
+    s = best;
+  }
   if (const char* env = getenv("EXL3_QMV_SPLITS")) {  // tuning: any split count that
     int v = atoi(env);                                 // keeps xhat within its LDS bound
     if (v >= 1) s = std::max(v, min_splits);

@@ -158,6 +158,13 @@ static size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // 31.2 / 33.5 (24 splits, 4 of 9: 25.0 / 30.7 / 31.7 / 34.1); the 5120 ->
 // 2 x 27648 group 5 -> 4 splits, M = 4, 46.9 -> 45.5; 14336x4096 keeps 14
 // (12: 16.5 / 20.7 / 23.6 against 14.9 / 20.0 / 22.6 at M = 1 / 4 / 16).
+// Shorter inputs may likewise go down to half the target, keeping their
+// K-parts per column pair, where that leaves fewer blocks on the busiest CU
+// (ties keep the larger count): 5120x5120 8 -> 6 splits (320 workgroups, 2 on
+// some CUs -> 240, one per CU), same box, us, M = 1 / 4 / 16: 10.14 / 13.21 /
+// 16.04 -> 9.64 / 12.03 / 15.06.  4096x6144 keeps 8 (5 would change its K-parts
+// and measured 9.52 against 9.31) and 5120x7168 keeps 8 (9: 11.19 / 14.69 /
+// 18.04 against 11.33 / 14.37 / 17.82).
 // Measured on MI355X (us, M = 1 / 4,
 // same box): 4096x14336 4 splits 14.10 / 17.68, 8 13.72 / 17.41; 2048x1536
 // 4: 7.57 / 9.98, 8: 6.59 / 8.50, 16: 7.32 / 9.83; 4096x6144 4: 11.41, 8:
@@ -185,13 +192,32 @@ static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
   const int target_wgs = 896;
   int s = (target_wgs + col_blocks - 1) / col_blocks;
   s = std::min(s, std::max(1, std::min(8, nb / 2)));
+  const int64_t cus = std::max(1, simd_count() / 4);
+  auto busiest = [&](int c) {  // blocks on the busiest CU
+    return (((int64_t)col_blocks * c + cus - 1) / cus) * ((nb + c - 1) / c);
+  };
+  auto k_parts = [&](int c) {
+    return (int64_t)col_blocks * c * 4 * 4 <= (int64_t)simd_count() * 5 ? 2 : 1;
+  };
   if (s < even_splits) {
-    const int64_t cus = std::max(1, simd_count() / 4);
     int best = even_splits;
     int64_t best_cost = INT64_MAX;
     for (int c = std::max(s, min_splits); c <= even_splits; ++c) {
-      const int64_t per_cu = ((int64_t)col_blocks * c + cus - 1) / cus;
-      const int64_t cost = per_cu * ((nb + c - 1) / c);
+      const int64_t cost = busiest(c);
+      if (cost < best_cost) {
+        best_cost = cost;
+        best = c;
+      }
+    }
+    s = best;
+  } else {
+    // down to half the target, at the same K-parts per column pair: a count
+    // whose workgroups spread more evenly over the CUs (ties keep the larger)
+    int best = s;
+    int64_t best_cost = busiest(s);
+    for (int c = s - 1; c >= std::max(even_splits, (s + 1) / 2); --c) {
+      if (k_parts(c) != k_parts(s)) continue;
+      const int64_t cost = busiest(c);
       if (cost < best_cost) {
         best_cost = cost;
         best = c;
@@ -204,7 +230,7 @@ static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
     if (v >= 1) s = std::max(v, min_splits);
   }
   s = std::max(1, std::min(s, nb));
-  if (kw == 0) kw = (int64_t)col_blocks * s * 4 * 4 <= (int64_t)simd_count() * 5 ? 2 : 1;
+  if (kw == 0) kw = k_parts(s);
   *splits_out = s;
   *kw_out = kw;
 }

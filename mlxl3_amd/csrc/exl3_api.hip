@@ -177,8 +177,11 @@ static size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // 4096x1792 8.12 / 9.77 / 11.20 / 14.73 -> 7.89 / 9.32 / 9.98 / 13.53;
 // 5120x5120 (1280) 10.45 / 12.58 / 13.58 / 17.8 -> 10.26 / 11.98 / 13.47 /
 // 16.9; 2048x1536 6.50 -> 6.51; above the bound it loses at M = 1: 4096x6144
-// (1536) 9.32 -> 9.62, 4096x10240 11.25 -> 12.43, 2048x12288 9.24 -> 9.56
-// (but 5120x7168, 1792 waves, 11.43 -> 11.18).
+// (1536) 9.32 -> 9.62, 4096x10240 11.25 -> 12.43, 2048x12288 9.24 -> 9.56.
+// Up to 2 waves per SIMD, ranges of at least 5 blocks (10 steps, 5 per wave
+// after the split) take 2 K-parts as well: 5120x7168 (1792 waves, 5 blocks)
+// 11.25 / 14.28 / 17.79 -> 10.92 / 13.76 / 16.92 at M = 1 / 4 / 16, 14336x4096
+// (1792, 8 blocks) 14.99 / 19.65 / 22.62 -> 15.09 / 18.81 / 22.36.
 // EXL3_QMV_SPLITS and EXL3_QMV_KW override (tuning).
 static int simd_count();
 static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
@@ -197,7 +200,8 @@ static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
     return (((int64_t)col_blocks * c + cus - 1) / cus) * ((nb + c - 1) / c);
   };
   auto k_parts = [&](int c) {
-    return (int64_t)col_blocks * c * 4 * 4 <= (int64_t)simd_count() * 5 ? 2 : 1;
+    const int64_t waves = (int64_t)col_blocks * c * 4, simds = simd_count();
+    return 4 * waves <= 5 * simds || (waves <= 2 * simds && (nb + c - 1) / c >= 5) ? 2 : 1;
   };
   if (s < even_splits) {
     int best = even_splits;

@@ -182,9 +182,19 @@ static size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // after the split) take 2 K-parts as well: 5120x7168 (1792 waves, 5 blocks)
 // 11.25 / 14.28 / 17.79 -> 10.92 / 13.76 / 16.92 at M = 1 / 4 / 16, 14336x4096
 // (1792, 8 blocks) 14.99 / 19.65 / 22.62 -> 15.09 / 18.81 / 22.36.
+// K = 5, 6 and 7 always take 2 K-parts: their weight loop keeps one slice in
+// flight per set (register budget) and the decode of a 16 % K != 0 width needs a
+// window per state, so a lone wave per column pair waits on its loads; twice the
+// waves cover that (same box, us, KW 1 -> 2, M = 1 / 4 / 16: 4096x14336 K5
+// 23.3 / 26.3 / 31.4 -> 21.6 / 21.5 / 27.3, K6 25.6 / 28.6 / 33.3 -> 21.7 / 21.8
+// / 28.4, K7 34.8 / 37.8 / 42.1 -> 26.2 / 25.4 / 31.4; 27648x5120 K5 51.6 / 57.0 /
+// 61.0 -> 33.5 / 45.9 / 53.6, K6 60.5 / 66.7 / 70.2 -> 34.0 / 47.0 / 55.1;
+// 5120x27648 K5 52.5 / 59.1 -> 36.7 / 41.8 at M = 1 / 4).  4 K-parts lose
+// (4096x14336 K5 M = 1 29.3); K = 3 and 8 lose with 2 (4096x14336 M = 1 K3 14.5
+// -> 18.1, K8 22.0 -> 27.7).
 // EXL3_QMV_SPLITS and EXL3_QMV_KW override (tuning).
 static int simd_count();
-static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
+static void choose_qmv_shape(int in, int out, int k, int* splits_out, int* kw_out) {
   const int nb = in / 128, col_blocks = out / 128;
   const int min_splits = (nb + 11) / 12, even_splits = (nb + 7) / 8;
   int kw = 0;
@@ -200,6 +210,7 @@ static void choose_qmv_shape(int in, int out, int* splits_out, int* kw_out) {
     return (((int64_t)col_blocks * c + cus - 1) / cus) * ((nb + c - 1) / c);
   };
   auto k_parts = [&](int c) {
+    if (k >= 5 && k <= 7) return 2;
     const int64_t waves = (int64_t)col_blocks * c * 4, simds = simd_count();
     return 4 * waves <= 5 * simds || (waves <= 2 * simds && (nb + c - 1) / c >= 5) ? 2 : 1;
   };
@@ -342,7 +353,7 @@ static void group_qmv_shape(const Group& g, int* splits, int* kw) {
     *splits = g.parts[0]->qmv_splits;
     *kw = g.parts[0]->qmv_kw;
   } else {
-    choose_qmv_shape(g.in, g.total_out, splits, kw);
+    choose_qmv_shape(g.in, g.total_out, g.k, splits, kw);
   }
 }
 
@@ -702,7 +713,7 @@ int exl3_linear_create(const uint16_t* trellis, int32_t in, int32_t out, int32_t
   h->out = out;
   h->k = k;
   h->cb = cb;
-  choose_qmv_shape(in, out, &h->qmv_splits, &h->qmv_kw);
+  choose_qmv_shape(in, out, k, &h->qmv_splits, &h->qmv_kw);
   h->owned = nullptr;
   *out_handle = h;
   return EXL3_OK;

@@ -190,8 +190,13 @@ static size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // / 28.4, K7 34.8 / 37.8 / 42.1 -> 26.2 / 25.4 / 31.4; 27648x5120 K5 51.6 / 57.0 /
 // 61.0 -> 33.5 / 45.9 / 53.6, K6 60.5 / 66.7 / 70.2 -> 34.0 / 47.0 / 55.1;
 // 5120x27648 K5 52.5 / 59.1 -> 36.7 / 41.8 at M = 1 / 4).  4 K-parts lose
-// (4096x14336 K5 M = 1 29.3); K = 3 and 8 lose with 2 (4096x14336 M = 1 K3 14.5
-// -> 18.1, K8 22.0 -> 27.7).
+// (4096x14336 K5 M = 1 29.3).  K = 3 (a window per state as well, two slices per
+// set) gains only with ranges of 8 or more blocks: 27648x5120 (12) 30.3 / 35.9 ->
+// 27.2 / 34.5 at M = 1 / 4, 5120x27648 (8) 29.4 / 36.6 -> 29.3 / 34.9, but
+// 4096x14336 (4) 14.5 / 18.3 / 22.9 -> 18.1 / 20.0 / 24.3 at M = 1 / 4 / 16.
+// K = 8 loses with 2 everywhere (4096x14336 M = 1 22.0 -> 27.7, 27648x5120 M = 4
+// 48.1 -> 56.9), and K = 4 does outside the waves rule (27648x5120 M = 4 29.9 ->
+// 35.1).
 // EXL3_QMV_SPLITS and EXL3_QMV_KW override (tuning).
 static int simd_count();
 static void choose_qmv_shape(int in, int out, int k, int* splits_out, int* kw_out) {
@@ -210,7 +215,7 @@ static void choose_qmv_shape(int in, int out, int k, int* splits_out, int* kw_ou
     return (((int64_t)col_blocks * c + cus - 1) / cus) * ((nb + c - 1) / c);
   };
   auto k_parts = [&](int c) {
-    if (k >= 5 && k <= 7) return 2;
+    if ((k >= 5 && k <= 7) || (k == 3 && (nb + c - 1) / c >= 8)) return 2;
     const int64_t waves = (int64_t)col_blocks * c * 4, simds = simd_count();
     return 4 * waves <= 5 * simds || (waves <= 2 * simds && (nb + c - 1) / c >= 5) ? 2 : 1;
   };

@@ -59,7 +59,7 @@ def same_bits(a, b):
     return bool(torch.equal(a.contiguous().view(as_int), b.contiguous().view(as_int)))
 
 
-@pytest.mark.parametrize("k, cb", [(2, 0), (4, 1), (3, 2), (8, 0)])
+@pytest.mark.parametrize("k, cb", [(2, 0), (4, 1), (3, 2), (8, 0), (5, 1), (6, 2), (7, 0)])
 @pytest.mark.parametrize("rows", [1, 5, 16, 17, 64, 200])
 def test_group_one_launch_equals_separate(k, cb, rows):
     import mlxl3_amd
